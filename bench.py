@@ -1,0 +1,317 @@
+#!/usr/bin/env python3
+"""Fused RMSNorm + residual, forward + backward, bf16 16384 x 4096 on one MI355X.
+
+One step = one forward (y, h, inv_rms from x, residual, weight) plus one backward (dx and fp32
+dweight from grad_y, the saved h and inv_rms) over one batch of synthetic rows, launched through
+the library's C ABI on torch's current stream.  Inputs are resident in HBM before timing starts.
+
+MALL hygiene: MI355X's 256 MB Infinity Cache would otherwise serve repeated inputs, so the step
+rotates over `--sets` independent buffer sets (768 MiB each at the default workload) and the
+backward of a step works on a different set than its forward, so no input of a step was
+touched by the step before it.
+
+Output: one JSON line (the driver's contract) with
+  value      = algorithmic bytes of a step / wall time of a step (GB/s, whole job, 1 GPU)
+  roofline   = the forward kernel (the larger of the two): algorithmic bytes per launch over its
+               mean launch duration from HIP events on the launch stream, against 8 TB/s HBM;
+               `traffic` comes from the committed rocprofv3 PMC summary when present
+  cpu_baseline = the NumPy restatement of the reference CPU path (oracle/) on a bounded sample of
+               rows of the same workload, on this host, single-threaded NumPy.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
+METRIC = "fused RMSNorm+residual fwd+bwd GB/s and % HBM peak, bf16 16384x4096"
+
+CONFIGS = {
+    # name: (rows, dim, eps, does backward)
+    "A": (512, 768, 1e-6, False),
+    "B": (8192, 4096, 1e-5, False),
+    "C": (16384, 4096, 1e-5, True),
+    "D": (32768, 8192, 1e-5, True),
+}
+
+
+def fwd_bytes(rows: int, d: int, s: int) -> int:
+    """Read x, residual, weight; write y, h (activation dtype) and fp32 inv_rms."""
+    return 4 * rows * d * s + d * s + 4 * rows
+
+
+def bwd_bytes(rows: int, d: int, s: int) -> int:
+    """Read grad_y, h, weight, fp32 inv_rms; write dx (activation dtype), fp32 dweight."""
+    return 3 * rows * d * s + d * s + 4 * rows + 4 * d
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", choices=sorted(CONFIGS), default="C")
+    p.add_argument("--sets", type=int, default=4, help="rotating buffer sets (MALL hygiene)")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="CPU-baseline budget; 0 skips it")
+    p.add_argument("--no-copy-ceiling", action="store_true")
+    return p.parse_args(argv)
+
+
+def lscpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(rows: int, d: int, eps: float, budget_s: float, with_bwd: bool):
+    """The oracle (NumPy restatement of fused.py:28-66) on a bounded sample of rows."""
+    import numpy as np
+
+    from oracle import fused_rmsnorm as ora
+
+    sample_rows = min(rows, 1024)
+    rng = np.random.default_rng(0)
+    # bf16-representable inputs upcast to fp32, prepared outside the timed region
+    def bf16ish(a):
+        u = a.astype(np.float32).view(np.uint32)
+        u = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+        return u.view(np.float32)
+    x = bf16ish(rng.standard_normal((sample_rows, d), dtype=np.float32))
+    res = bf16ish(rng.standard_normal((sample_rows, d), dtype=np.float32))
+    w = bf16ish((1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
+    g = bf16ish(rng.standard_normal((sample_rows, d), dtype=np.float32))
+
+    def one():
+        y, h, inv = ora.fused_rmsnorm_residual_forward(x, res, w, eps)
+        if with_bwd:
+            ora.fused_rmsnorm_residual_backward(g, h * inv, w, inv)
+
+    one()  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 5 and time.perf_counter() - t_start >= budget_s:
+            break
+    med = sorted(times)[len(times) // 2]
+    rows_per_s = sample_rows / med
+    per_row = (fwd_bytes(rows, d, 2) + (bwd_bytes(rows, d, 2) if with_bwd else 0)) / rows
+    return {
+        "value": round(rows_per_s * per_row / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{sample_rows} of {rows} rows x {d}, fwd{'+bwd' if with_bwd else ''}, fp32 "
+                   f"upcasts of bf16-representable inputs, NumPy (single-threaded ufuncs); median "
+                   f"of {len(times)} runs after 1 warm-up; GB/s = rows/s x the bf16 algorithmic "
+                   f"bytes per row of the GPU workload"),
+        "ms_median": round(med * 1e3, 3),
+        "rows_per_s": round(rows_per_s, 1),
+        "host_cpu": lscpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
+    }
+
+
+def load_traffic(config: str):
+    path = os.path.join(REPO, "profiles", f"pmc_traffic_config_{config}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("fwd_traffic_bytes_per_launch")
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus "
+              f"{args.gpus}", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from velograd_amd import _lib
+    from velograd_amd import kernels as vk
+
+    rows, d, eps, with_bwd = CONFIGS[args.config]
+    dt = torch.bfloat16 if args.config != "A" else torch.float32
+    s = 2 if dt == torch.bfloat16 else 4
+    code = _lib.TORCH_DTYPE_CODES[dt]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    ws_bytes = vk.bwd_workspace_bytes(rows, d, dev)
+    sets = []
+    for _ in range(args.sets):
+        b = {
+            "x": torch.randn(rows, d, device=dev, generator=gen).to(dt),
+            "res": torch.randn(rows, d, device=dev, generator=gen).to(dt),
+            "w": (1 + 0.1 * torch.randn(d, device=dev, generator=gen)).to(dt),
+            "y": torch.empty(rows, d, device=dev, dtype=dt),
+            "h": torch.empty(rows, d, device=dev, dtype=dt),
+            "inv": torch.empty(rows, device=dev, dtype=torch.float32),
+        }
+        if with_bwd:
+            b["g"] = torch.randn(rows, d, device=dev, generator=gen).to(dt)
+            b["dx"] = torch.empty(rows, d, device=dev, dtype=dt)
+            b["dw"] = torch.empty(d, device=dev, dtype=torch.float32)
+            b["ws"] = torch.empty(max(ws_bytes, 16), device=dev, dtype=torch.uint8)
+        sets.append(b)
+
+    fwd_fn = lib.velograd_rmsnorm_residual_fwd
+    bwd_fn = lib.velograd_rmsnorm_residual_bwd
+    fwd_args = [(b["x"].data_ptr(), b["res"].data_ptr(), b["w"].data_ptr(), b["y"].data_ptr(),
+                 b["h"].data_ptr(), b["inv"].data_ptr(), rows, d, d, d, d, d, code, code, eps, sp)
+                for b in sets]
+    bwd_args = []
+    if with_bwd:
+        bwd_args = [(b["g"].data_ptr(), b["h"].data_ptr(), 1, b["w"].data_ptr(),
+                     b["inv"].data_ptr(), b["dx"].data_ptr(), None, b["dw"].data_ptr(),
+                     b["ws"].data_ptr(), ws_bytes, rows, d, d, d, d, d, code, code, sp)
+                    for b in sets]
+
+    # every set gets a valid h / inv_rms before any backward reads it
+    for a in fwd_args:
+        _lib.check(fwd_fn(*a), "fwd")
+    torch.cuda.synchronize()
+
+    n = args.sets
+    half = n // 2
+
+    def step(k, evs=None):
+        if evs is not None:
+            evs[0].record(stream)
+        rc = fwd_fn(*fwd_args[k % n])
+        if evs is not None:
+            evs[1].record(stream)
+        if with_bwd:
+            rc |= bwd_fn(*bwd_args[(k + half) % n])
+            if evs is not None:
+                evs[2].record(stream)
+        return rc
+
+    for k in range(args.warmup):
+        _lib.check(step(k), "warm-up step")
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    rc = 0
+    for k in range(args.steps):
+        rc |= step(k, events[k])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.check(rc, "timed steps")
+
+    fwd_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
+    mean_fwd_ms = sum(fwd_ms) / len(fwd_ms)
+    med_fwd_ms = fwd_ms[len(fwd_ms) // 2]
+    fb = fwd_bytes(rows, d, s)
+    bb = bwd_bytes(rows, d, s) if with_bwd else 0
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    value = (fb + bb) / (ms_per_step * 1e-3) / 1e9
+
+    extra = {
+        "fwd_us_mean": round(mean_fwd_ms * 1e3, 2),
+        "fwd_us_median": round(med_fwd_ms * 1e3, 2),
+        "fwd_gbs": round(fb / (mean_fwd_ms * 1e-3) / 1e9, 1),
+        "fwd_bytes": fb,
+    }
+    if with_bwd:
+        bwd_ms = sorted(e[1].elapsed_time(e[2]) for e in events)
+        mean_bwd_ms = sum(bwd_ms) / len(bwd_ms)
+        extra.update({
+            "bwd_us_mean": round(mean_bwd_ms * 1e3, 2),
+            "bwd_us_median": round(bwd_ms[len(bwd_ms) // 2] * 1e3, 2),
+            "bwd_gbs": round(bb / (mean_bwd_ms * 1e-3) / 1e9, 1),
+            "bwd_bytes": bb,
+            "bwd_workspace_bytes": ws_bytes,
+        })
+    extra["rows_per_s"] = round(rows / (ms_per_step * 1e-3), 1)
+    extra["pct_hbm_peak"] = round(100.0 * value / HBM_PEAK_GBS, 2)
+
+    if not args.no_copy_ceiling:
+        src = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        srcs = [src, torch.empty_like(src)]
+        dsts = [dst, torch.empty_like(dst)]
+        for i in range(3):
+            dsts[i % 2].copy_(srcs[i % 2])
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        e0.record(stream)
+        for i in range(reps):
+            dsts[i % 2].copy_(srcs[i % 2])
+        e1.record(stream)
+        torch.cuda.synchronize()
+        copy_ms = e0.elapsed_time(e1) / reps
+        extra["copy_ceiling_gbs"] = round(2 * src.numel() / (copy_ms * 1e-3) / 1e9, 1)
+        del src, dst, srcs, dsts
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(rows, d, eps, args.cpu_seconds, with_bwd)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dt == torch.bfloat16 else "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"config {args.config}: fused RMSNorm+residual "
+                         f"{'fwd+bwd' if with_bwd else 'fwd'}, {rows}x{d} "
+                         f"{'bf16' if s == 2 else 'fp32'}, eps {eps}, x,residual,grad_y ~ "
+                         f"N(0,1), weight 1+0.1N(0,1), {args.sets} rotating buffer sets"),
+            "rows": rows,
+            "dim": d,
+            "algorithmic_bytes_per_step": fb + bb,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "fwd_vec_kernel",
+            "achieved": round(fb / (mean_fwd_ms * 1e-3) / 1e9, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(fb / (mean_fwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic(args.config),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,114 @@
+/*
+ * velograd_kernels.h — C ABI of the MI355X (gfx950) fused RMSNorm + residual-add kernels.
+ *
+ * These entry points sit below the Python functions `fused_rmsnorm_residual_forward`,
+ * `fused_rmsnorm_residual_backward` and `fused_rmsnorm_residual` of `velograd_amd.kernels`,
+ * which keep the call signatures of the reference's `velograd.kernels`
+ * (python/velograd/kernels/fused.py:28-66, python/velograd/kernels/__init__.py:19-32).
+ *
+ * Conventions (follow the reference's only C ABI, include/velograd/aot_compiler.h:74-90):
+ *   - `velograd_` prefix, default symbol visibility, `int32_t` status return.
+ *   - 0 = success; negative = argument error (nothing was launched); positive = the hipError_t
+ *     reported by the HIP runtime right after the launch.  The text of the last error of the
+ *     calling thread is returned by velograd_kernels_last_error().
+ *   - The library never allocates or frees device memory and never synchronises the host:
+ *     every buffer (outputs and the backward workspace) belongs to the caller, and every
+ *     launch is asynchronous on `hip_stream` (a hipStream_t; NULL = the null stream).
+ *   - Tensors are row-major [rows, dim] with unit stride along dim; `ld_*` is the row stride in
+ *     elements.  Rows are independent; the normalisation runs over dim.
+ *   - Results are deterministic: the same inputs on the same device give bitwise identical
+ *     outputs, dweight included (no floating-point atomics anywhere).
+ *   - Output buffers must not overlap input buffers.
+ */
+#ifndef VELOGRAD_KERNELS_H
+#define VELOGRAD_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VELOGRAD_API __attribute__((visibility("default")))
+
+/* Element types of activations (`dtype`) and of the weight vector (`w_dtype`). */
+#define VELOGRAD_DTYPE_F32 0
+#define VELOGRAD_DTYPE_F16 1
+#define VELOGRAD_DTYPE_BF16 2
+
+/* Negative status codes (argument errors, nothing launched). */
+#define VELOGRAD_ERR_INVALID_ARGUMENT (-1)
+#define VELOGRAD_ERR_UNSUPPORTED_DTYPE (-2)
+#define VELOGRAD_ERR_WORKSPACE_TOO_SMALL (-3)
+#define VELOGRAD_ERR_DEVICE_QUERY (-4)
+
+/*
+ * Forward: h = x + residual; inv_rms = 1 / sqrt(mean(h^2) + eps); y = (h * inv_rms) * weight.
+ * Replaces fused_rmsnorm_residual_forward (python/velograd/kernels/fused.py:28-46).
+ *
+ *   x, residual : [rows, dim] in `dtype`; residual may be NULL (then h is x, as fused.py:39).
+ *   weight      : [dim] in `w_dtype` (= dtype or F32); NULL means no scale (fused.py:44-45).
+ *   y           : [rows, dim] in `dtype` (required).
+ *   h           : [rows, dim] in `dtype`; may be NULL (not written).  Ignored when residual is
+ *                 NULL, since h is x itself then.
+ *   inv_rms     : [rows] fp32; may be NULL (not written).
+ *   eps         : added in fp32 to mean(h^2), as NumPy adds a Python float to a float32 array.
+ * All arithmetic is fp32; stores round to nearest even.  h feeds the row statistic and y
+ * unrounded (fp32), as the reference computes both from the fp32 sum.
+ */
+VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(
+    const void* x, const void* residual, const void* weight,
+    void* y, void* h, float* inv_rms,
+    int64_t rows, int64_t dim,
+    int64_t ld_x, int64_t ld_res, int64_t ld_y, int64_t ld_h,
+    int32_t dtype, int32_t w_dtype, float eps, void* hip_stream);
+
+/*
+ * Backward of the forward above.
+ * Replaces fused_rmsnorm_residual_backward (python/velograd/kernels/fused.py:48-66):
+ *   gw = grad_y * weight; m = mean(gw * xhat); dx = inv_rms * (gw - xhat * m);
+ *   dweight = sum over rows of grad_y * xhat.
+ *
+ *   grad_y      : [rows, dim] in `dtype`.
+ *   saved       : [rows, dim] in `dtype`: xhat = h * inv_rms (the reference's `normed_input`)
+ *                 when saved_is_h == 0, or h itself when saved_is_h != 0 (then xhat = h * inv_rms
+ *                 is formed in fp32 in registers; same bytes moved).
+ *   weight      : [dim] in `w_dtype`, or NULL (gw = grad_y; dweight is then not computed).
+ *   inv_rms     : [rows] fp32, as written by the forward.
+ *   dx          : [rows, dim] in `dtype` (required).  Since h = x + residual, it is also the
+ *                 gradient of residual.
+ *   dres        : optional [rows, dim] second copy of dx for callers that need two buffers.
+ *   dweight     : [dim] fp32, or NULL.  Reduced in two deterministic stages through `workspace`.
+ *   workspace   : device scratch of at least
+ *                 velograd_rmsnorm_residual_bwd_workspace_bytes(rows, dim, device) bytes,
+ *                 256-byte aligned; may be NULL when dweight is NULL.
+ */
+VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
+    const void* grad_y, const void* saved, int32_t saved_is_h,
+    const void* weight, const float* inv_rms,
+    void* dx, void* dres, float* dweight,
+    void* workspace, size_t ws_bytes,
+    int64_t rows, int64_t dim,
+    int64_t ld_g, int64_t ld_saved, int64_t ld_dx, int64_t ld_dres,
+    int32_t dtype, int32_t w_dtype, void* hip_stream);
+
+/*
+ * Workspace needed by velograd_rmsnorm_residual_bwd for dweight on `device` (a HIP device
+ * ordinal).  No counterpart in the reference, whose NumPy backward allocates its own
+ * temporaries (fused.py:58-65); returns 0 if the device cannot be queried.
+ */
+VELOGRAD_API size_t velograd_rmsnorm_residual_bwd_workspace_bytes(int64_t rows, int64_t dim,
+                                                                  int32_t device);
+
+/* Text of the calling thread's last error ("" if none).  No counterpart in the reference. */
+VELOGRAD_API const char* velograd_kernels_last_error(void);
+
+/* Library version string; mirrors velograd_get_version (include/velograd/aot_compiler.h:89). */
+VELOGRAD_API const char* velograd_kernels_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VELOGRAD_KERNELS_H */

@@ -1,0 +1,121 @@
+"""The C ABI library: it loads, exports exactly what include/velograd_kernels.h declares, and
+rejects bad arguments on the host before any HIP call (no GPU needed)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from velograd_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "velograd_kernels.h")
+
+
+def declared_functions():
+    with open(HEADER) as f:
+        text = f.read()
+    return re.findall(r"VELOGRAD_API\s+[\w\s\*]+?\b(velograd_\w+)\s*\(", text)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from velograd_amd.build import build_library
+        build_library()
+    return _lib.load()
+
+
+def test_header_declares_the_bound_functions():
+    names = declared_functions()
+    assert len(names) == len(set(names))
+    assert set(names) == set(_lib.SIGNATURES), (names, sorted(_lib.SIGNATURES))
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    # and nothing but the ABI is visible (-fvisibility=hidden)
+    out = os.popen(f"nm -D --defined-only {_lib.LIB_PATH}").read()
+    exported = set(re.findall(r"\b[TW] (velograd_\w+)", out))
+    assert exported == set(declared_functions())
+
+
+def test_version_string(lib):
+    v = lib.velograd_kernels_version().decode()
+    assert "gfx950" in v and "velograd_amd" in v
+
+
+def _fwd(lib, **kw):
+    args = dict(x=16, residual=None, weight=None, y=32, h=None, inv_rms=None, rows=4, dim=64,
+                ld_x=64, ld_res=64, ld_y=64, ld_h=64, dtype=2, w_dtype=2, eps=1e-5, stream=None)
+    args.update(kw)
+    return lib.velograd_rmsnorm_residual_fwd(*args.values())
+
+
+def _bwd(lib, **kw):
+    args = dict(g=16, saved=48, saved_is_h=0, weight=None, inv_rms=80, dx=32, dres=None,
+                dweight=None, ws=None, ws_bytes=0, rows=4, dim=64, ld_g=64, ld_s=64, ld_dx=64,
+                ld_dres=64, dtype=2, w_dtype=2, stream=None)
+    args.update(kw)
+    return lib.velograd_rmsnorm_residual_bwd(*args.values())
+
+
+# Every case below returns before the library touches the HIP runtime (the pointers are dummies
+# that are never dereferenced), so it runs on a host without a GPU.
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=7), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    (dict(dtype=0, w_dtype=2), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    (dict(dim=0), _lib.ERR_INVALID_ARGUMENT, "invalid shape"),
+    (dict(rows=-1), _lib.ERR_INVALID_ARGUMENT, "invalid shape"),
+    (dict(x=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(y=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(ld_x=63), _lib.ERR_INVALID_ARGUMENT, "row strides"),
+    (dict(y=16), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(residual=64, h=64), _lib.ERR_INVALID_ARGUMENT, "alias"),
+])
+def test_fwd_argument_errors(lib, kw, code, msg):
+    assert _fwd(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_fwd_zero_rows_is_a_no_op(lib):
+    assert _fwd(lib, rows=0, x=None, y=None) == 0
+    assert _lib.last_error() == ""
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=5), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    (dict(dtype=1, w_dtype=2), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    (dict(dim=-3), _lib.ERR_INVALID_ARGUMENT, "invalid shape"),
+    (dict(inv_rms=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(saved=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(ld_dx=1), _lib.ERR_INVALID_ARGUMENT, "row strides"),
+    (dict(dx=16), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(dres=48), _lib.ERR_INVALID_ARGUMENT, "alias"),
+])
+def test_bwd_argument_errors(lib, kw, code, msg):
+    assert _bwd(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_check_maps_status_to_python_exceptions():
+    with pytest.raises(TypeError):
+        _lib.check(_lib.ERR_UNSUPPORTED_DTYPE, "x")
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_INVALID_ARGUMENT, "x")
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_WORKSPACE_TOO_SMALL, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(98, "x")  # a hipError_t
+    _lib.check(0, "x")
+
+
+def test_dtype_codes_match_header():
+    with open(HEADER) as f:
+        text = f.read()
+    for name, val in (("F32", _lib.DTYPE_F32), ("F16", _lib.DTYPE_F16), ("BF16", _lib.DTYPE_BF16)):
+        assert re.search(rf"#define VELOGRAD_DTYPE_{name} {val}\b", text)
+    assert _lib.TORCH_DTYPE_CODES[torch.bfloat16] == _lib.DTYPE_BF16

@@ -1,0 +1,63 @@
+"""Build of the gfx950 HIP library `velograd_amd/lib/libvelograd_kernels.so`.
+
+The library is compiled in-tree with hipcc (no torch extension machinery, no hipify) so the
+same `.so` file travels with the source tree to the GPU host.  `python -m velograd_amd.build`
+runs it from the command line.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+SRC = os.path.join(PKG_DIR, "csrc", "rmsnorm_residual.hip")
+INCLUDE_DIR = os.path.join(REPO_DIR, "include")
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libvelograd_kernels.so")
+
+OFFLOAD_ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-fPIC",
+    "-shared",
+    "-fvisibility=hidden",
+    # Mirror the reference's rounding points exactly: no implicit multiply-add fusion.
+    "-ffp-contract=off",
+    # No packed-fp32 VALU instructions in the device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def find_hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: the HIP toolchain (ROCm) is required to build")
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile the kernels for gfx950 and return the path of the shared library."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    cmd = [find_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE_DIR, SRC, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(
+            "hipcc failed (exit %d):\n%s\n%s" % (proc.returncode, proc.stdout, proc.stderr)
+        )
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose="-v" in sys.argv[1:]))

@@ -1,0 +1,941 @@
+// Fused RMSNorm + residual add, forward and backward, hand-written for gfx950 (CDNA4, wave64).
+//
+// Math (reference: python/velograd/kernels/fused.py:28-66):
+//   forward   h = x + residual;  inv_rms = 1 / sqrt(mean(h^2) + eps);  y = (h * inv_rms) * w
+//   backward  gw = g * w;  m = mean(gw * xhat);  dx = inv_rms * (gw - xhat * m)
+//             dweight = sum over rows of g * xhat,  with xhat = h * inv_rms
+// Every operation is fp32 and rounds where the NumPy reference rounds (this file is built with
+// -ffp-contract=off so no multiply-add pair is fused behind the code's back); stores round to
+// nearest even.  Only the order of the row sums differs from NumPy's pairwise summation.
+//
+// Kernels
+//   fwd_vec_kernel      one row per `tpr` threads (1..16 wave64), `groups` rows per workgroup;
+//                       each thread holds NV 16-byte chunks of the row in registers, so every
+//                       element moves through HBM exactly once (read x, residual; write h, y).
+//   bwd_vec_kernel      persistent: each row slot walks rows slot, slot + S, ... with the next
+//                       row's loads in flight while the current row reduces; the weight chunk and
+//                       the fp32 dweight column accumulators stay in registers for the whole walk;
+//                       each slot finally writes one fp32 partial row (no atomics).
+//   dweight_reduce      stage 2: sums the partial rows in a fixed order -> dweight[dim].
+//   *_generic_kernel    any dim and any alignment: the same arithmetic with scalar accesses.
+// Row sums: DPP inside each 16-lane row of the wave, readlane across the four rows, LDS only
+// across the waves that share a row; every order is fixed, so results are bitwise reproducible.
+
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <atomic>
+
+#include "velograd_kernels.h"
+
+#define VG_VERSION_STRING "velograd_amd 0.1.0 fused-rmsnorm-residual gfx950"
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kMaxWavesPerRow = 16;  // 1024 threads per row at most
+constexpr int kMaxNV = 4;            // 16-byte chunks per thread in the register-resident path
+// Workgroup size bound of the register-resident kernels: with NV <= 2 chunks a thread fits in
+// 128 VGPRs (1024 threads per workgroup); NV = 3..4 get 256 VGPRs and at most 512 threads.
+__host__ __device__ constexpr int max_block_for_nv(int nv) { return nv <= 2 ? 1024 : 512; }
+constexpr int kGenericBlock = 256;
+
+// ------------------------------------------------------------------------------------------
+// Element codecs: 16 bytes <-> fp32 registers.
+// ------------------------------------------------------------------------------------------
+template <int DT>
+struct Codec;
+
+template <>
+struct Codec<VELOGRAD_DTYPE_F32> {
+  static constexpr int kBytes = 4;
+  static constexpr int kVec = 4;
+  __device__ static inline void unpack(const u32x4 v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, v[i]);
+  }
+  __device__ static inline u32x4 pack(const float* f) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __builtin_bit_cast(uint32_t, f[i]);
+    return v;
+  }
+  __device__ static inline float load1(const void* p, int64_t i) {
+    return static_cast<const float*>(p)[i];
+  }
+  __device__ static inline void store1(void* p, int64_t i, float f) {
+    static_cast<float*>(p)[i] = f;
+  }
+};
+
+template <>
+struct Codec<VELOGRAD_DTYPE_BF16> {
+  static constexpr int kBytes = 2;
+  static constexpr int kVec = 8;
+  __device__ static inline void unpack(const u32x4 v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __builtin_bit_cast(float, v[i] << 16);
+      f[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
+    }
+  }
+  __device__ static inline u32x4 pack(const float* f) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bf16x2 p = {(__bf16)f[2 * i], (__bf16)f[2 * i + 1]};  // v_cvt_pk_bf16_f32, RNE
+      v[i] = __builtin_bit_cast(uint32_t, p);
+    }
+    return v;
+  }
+  __device__ static inline float load1(const void* p, int64_t i) {
+    const uint32_t u = static_cast<const uint16_t*>(p)[i];
+    return __builtin_bit_cast(float, u << 16);
+  }
+  __device__ static inline void store1(void* p, int64_t i, float f) {
+    static_cast<__bf16*>(p)[i] = (__bf16)f;
+  }
+};
+
+template <>
+struct Codec<VELOGRAD_DTYPE_F16> {
+  static constexpr int kBytes = 2;
+  static constexpr int kVec = 8;
+  __device__ static inline void unpack(const u32x4 v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x2 h = __builtin_bit_cast(f16x2, v[i]);
+      f[2 * i] = (float)h[0];
+      f[2 * i + 1] = (float)h[1];
+    }
+  }
+  __device__ static inline u32x4 pack(const float* f) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x2 p = {(_Float16)f[2 * i], (_Float16)f[2 * i + 1]};
+      v[i] = __builtin_bit_cast(uint32_t, p);
+    }
+    return v;
+  }
+  __device__ static inline float load1(const void* p, int64_t i) {
+    return (float)static_cast<const _Float16*>(p)[i];
+  }
+  __device__ static inline void store1(void* p, int64_t i, float f) {
+    static_cast<_Float16*>(p)[i] = (_Float16)f;
+  }
+};
+
+template <int DT>
+__device__ inline u32x4 load16(const void* base, int64_t elem) {
+  return *reinterpret_cast<const u32x4*>(static_cast<const char*>(base) +
+                                         elem * Codec<DT>::kBytes);
+}
+
+template <int DT>
+__device__ inline void store16(void* base, int64_t elem, const u32x4 v) {
+  *reinterpret_cast<u32x4*>(static_cast<char*>(base) + elem * Codec<DT>::kBytes) = v;
+}
+
+// Weight chunk of kVec(DT) elements starting at column col0, in fp32.  The weight is stored
+// either in the activation dtype or in fp32.
+template <int DT, int WDT>
+__device__ inline void load_w_chunk(const void* w, int64_t col0, float* f) {
+  if constexpr (WDT == DT) {
+    Codec<DT>::unpack(load16<DT>(w, col0), f);
+  } else {
+    static_assert(WDT == VELOGRAD_DTYPE_F32, "weight is the activation dtype or fp32");
+#pragma unroll
+    for (int q = 0; q < Codec<DT>::kVec / 4; ++q)
+      Codec<VELOGRAD_DTYPE_F32>::unpack(load16<VELOGRAD_DTYPE_F32>(w, col0 + 4 * q), f + 4 * q);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Reductions.
+// ------------------------------------------------------------------------------------------
+template <int CTRL>
+__device__ inline float dpp_move(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wave; the result is wave-uniform.  Requires all lanes active.
+__device__ inline float wave_sum(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x124>(v);  // row_ror:4
+  v += dpp_move<0x128>(v);  // row_ror:8  -> each lane holds its 16-lane row's sum
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Sum over the `tpr` threads of row group `grp` (threads grp*tpr .. grp*tpr+tpr-1, whole waves).
+// `red` holds one float per wave of the block; the caller alternates buffers between calls
+// that reuse it so one barrier per call suffices.
+__device__ inline float row_sum(float v, int tpr, int grp, float* red) {
+  v = wave_sum(v);
+  if (tpr > kWave) {
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    const int wpr = tpr / kWave;
+    const float* p = red + grp * wpr;
+    float t = p[0];
+    for (int i = 1; i < wpr; ++i) t += p[i];
+    v = t;
+  }
+  return v;
+}
+
+// ------------------------------------------------------------------------------------------
+// Kernel arguments.
+// ------------------------------------------------------------------------------------------
+struct FwdArgs {
+  const void* x;
+  const void* res;
+  const void* w;
+  void* y;
+  void* h;
+  float* inv_rms;
+  int64_t rows;
+  int64_t ld_x, ld_res, ld_y, ld_h;
+  int32_t dim;
+  int32_t tpr;
+  float eps;
+};
+
+struct BwdArgs {
+  const void* g;
+  const void* saved;
+  const void* w;
+  const float* inv_rms;
+  void* dx;
+  void* dres;
+  float* partial;  // [slots, dim] fp32 or null
+  int64_t rows;
+  int64_t ld_g, ld_s, ld_dx, ld_dres;
+  int32_t dim;
+  int32_t tpr;
+  int32_t iters;  // rows visited per slot = ceil(rows / slots)
+};
+
+// ------------------------------------------------------------------------------------------
+// Forward, register-resident row.
+// ------------------------------------------------------------------------------------------
+template <int DT, int WDT, int NV>
+__global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const FwdArgs a) {
+  using C = Codec<DT>;
+  constexpr int V = C::kVec;
+  __shared__ float red[kMaxWavesPerRow];
+
+  const int tpr = a.tpr;
+  const int grp = threadIdx.x / tpr;
+  const int lt = threadIdx.x - grp * tpr;
+  const int groups = blockDim.x / tpr;
+  const int64_t row = (int64_t)blockIdx.x * groups + grp;
+  const bool row_ok = row < a.rows;
+  const int nchunk = a.dim / V;
+  const bool has_res = a.res != nullptr;
+  const bool has_w = a.w != nullptr;
+
+  u32x4 xv[NV], rv[NV];
+  float wf[NV][V];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = lt + k * tpr;
+    xv[k] = u32x4{0u, 0u, 0u, 0u};
+    rv[k] = u32x4{0u, 0u, 0u, 0u};
+    if (row_ok && c < nchunk) {
+      xv[k] = load16<DT>(a.x, row * a.ld_x + (int64_t)c * V);
+      if (has_res) rv[k] = load16<DT>(a.res, row * a.ld_res + (int64_t)c * V);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = lt + k * tpr;
+    if (has_w && c < nchunk) {
+      load_w_chunk<DT, WDT>(a.w, (int64_t)c * V, wf[k]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) wf[k][i] = 1.0f;
+    }
+  }
+
+  float hf[NV][V];
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    C::unpack(xv[k], hf[k]);
+    if (has_res) {
+      float rf[V];
+      C::unpack(rv[k], rf);
+#pragma unroll
+      for (int i = 0; i < V; ++i) hf[k][i] = hf[k][i] + rf[i];
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss += hf[k][i] * hf[k][i];
+  }
+
+  if (has_res && a.h != nullptr) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      if (row_ok && c < nchunk) store16<DT>(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf[k]));
+    }
+  }
+
+  ss = row_sum(ss, tpr, grp, red);
+  const float mean_sq = ss / (float)a.dim;
+  const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
+  if (row_ok && lt == 0 && a.inv_rms != nullptr) a.inv_rms[row] = r;
+
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = lt + k * tpr;
+    if (row_ok && c < nchunk) {
+      float yf[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float n = hf[k][i] * r;
+        yf[i] = has_w ? n * wf[k][i] : n;
+      }
+      store16<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Forward, any dim / alignment: one row per workgroup, two passes over the row (the second
+// re-reads x and residual, normally from L2, and recomputes the identical fp32 h).
+// ------------------------------------------------------------------------------------------
+template <int DT, int WDT>
+__global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArgs a) {
+  using C = Codec<DT>;
+  using CW = Codec<WDT>;
+  __shared__ float red[kGenericBlock / kWave];
+  const int64_t row = blockIdx.x;
+  const bool has_res = a.res != nullptr;
+  const bool has_w = a.w != nullptr;
+  const bool write_h = has_res && a.h != nullptr;
+
+  float ss = 0.0f;
+  for (int j = threadIdx.x; j < a.dim; j += blockDim.x) {
+    float hx = C::load1(a.x, row * a.ld_x + j);
+    if (has_res) hx = hx + C::load1(a.res, row * a.ld_res + j);
+    if (write_h) C::store1(a.h, row * a.ld_h + j, hx);
+    ss += hx * hx;
+  }
+  ss = row_sum(ss, blockDim.x, 0, red);
+  const float mean_sq = ss / (float)a.dim;
+  const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
+  if (threadIdx.x == 0 && a.inv_rms != nullptr) a.inv_rms[row] = r;
+
+  for (int j = threadIdx.x; j < a.dim; j += blockDim.x) {
+    float hx = C::load1(a.x, row * a.ld_x + j);
+    if (has_res) hx = hx + C::load1(a.res, row * a.ld_res + j);
+    const float n = hx * r;
+    C::store1(a.y, row * a.ld_y + j, has_w ? n * CW::load1(a.w, j) : n);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward, register-resident row, persistent row slots.
+// ------------------------------------------------------------------------------------------
+template <int DT, int WDT, int NV, bool SAVED_IS_H>
+__global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const BwdArgs a) {
+  using C = Codec<DT>;
+  constexpr int V = C::kVec;
+  __shared__ float red[2][kMaxWavesPerRow];
+
+  const int tpr = a.tpr;
+  const int grp = threadIdx.x / tpr;
+  const int lt = threadIdx.x - grp * tpr;
+  const int groups = blockDim.x / tpr;
+  const int64_t slot = (int64_t)blockIdx.x * groups + grp;
+  const int64_t nslots = (int64_t)gridDim.x * groups;
+  const int nchunk = a.dim / V;
+  const bool has_w = a.w != nullptr;
+  const bool has_dres = a.dres != nullptr;
+
+  float wf[NV][V];
+  float acc[NV][V];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = lt + k * tpr;
+    if (has_w && c < nchunk) {
+      load_w_chunk<DT, WDT>(a.w, (int64_t)c * V, wf[k]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) wf[k][i] = 1.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[k][i] = 0.0f;
+  }
+
+  // Loads of one row into (gv, sv, rr); zeros outside the tensor.
+  auto load_row = [&](int64_t row, u32x4* gv, u32x4* sv, float& rr) {
+    const bool ok = row < a.rows;
+    rr = ok ? a.inv_rms[row] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      gv[k] = u32x4{0u, 0u, 0u, 0u};
+      sv[k] = u32x4{0u, 0u, 0u, 0u};
+      if (ok && c < nchunk) {
+        gv[k] = load16<DT>(a.g, row * a.ld_g + (int64_t)c * V);
+        sv[k] = load16<DT>(a.saved, row * a.ld_s + (int64_t)c * V);
+      }
+    }
+  };
+
+  int64_t row = slot;
+  u32x4 gv[NV], sv[NV];
+  float rr;
+  load_row(row, gv, sv, rr);
+
+  for (int it = 0; it < a.iters; ++it) {
+    const bool ok = row < a.rows;
+    const int64_t nrow = row + nslots;
+    u32x4 gn[NV], sn[NV];
+    float rn = 0.0f;
+    if (it + 1 < a.iters) {
+      load_row(nrow, gn, sn, rn);
+    } else {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        gn[k] = u32x4{0u, 0u, 0u, 0u};
+        sn[k] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+
+    float gf[NV][V], xh[NV][V];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      C::unpack(gv[k], gf[k]);
+      C::unpack(sv[k], xh[k]);
+      if constexpr (SAVED_IS_H) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) xh[k][i] = xh[k][i] * rr;
+      }
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float gw = gf[k][i] * wf[k][i];
+        s += gw * xh[k][i];
+      }
+    }
+    s = row_sum(s, tpr, grp, red[it & 1]);
+    const float m = s / (float)a.dim;
+
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      if (ok && c < nchunk) {
+        float d[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const float gw = gf[k][i] * wf[k][i];
+          d[i] = rr * (gw - xh[k][i] * m);
+        }
+        const u32x4 pv = C::pack(d);
+        store16<DT>(a.dx, row * a.ld_dx + (int64_t)c * V, pv);
+        if (has_dres) store16<DT>(a.dres, row * a.ld_dres + (int64_t)c * V, pv);
+      }
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[k][i] += gf[k][i] * xh[k][i];
+    }
+
+    row = nrow;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      gv[k] = gn[k];
+      sv[k] = sn[k];
+    }
+    rr = rn;
+  }
+
+  if (a.partial != nullptr) {
+    float* prow = a.partial + slot * (int64_t)a.dim;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      if (c < nchunk) {
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q)
+          store16<VELOGRAD_DTYPE_F32>(prow, (int64_t)c * V + 4 * q,
+                                      Codec<VELOGRAD_DTYPE_F32>::pack(&acc[k][4 * q]));
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward, any dim / alignment: one row slot per workgroup, two passes per row; the slot's
+// dweight partial row is accumulated in place (each column owned by one thread).
+// ------------------------------------------------------------------------------------------
+template <int DT, int WDT, bool SAVED_IS_H>
+__global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArgs a) {
+  using C = Codec<DT>;
+  using CW = Codec<WDT>;
+  __shared__ float red[2][kGenericBlock / kWave];
+  const int64_t slot = blockIdx.x;
+  const int64_t nslots = gridDim.x;
+  const bool has_w = a.w != nullptr;
+  const bool has_dres = a.dres != nullptr;
+  float* prow = a.partial != nullptr ? a.partial + slot * (int64_t)a.dim : nullptr;
+
+  for (int it = 0; it < a.iters; ++it) {
+    const int64_t row = slot + (int64_t)it * nslots;
+    if (row >= a.rows) break;  // uniform across the workgroup
+    const float rr = a.inv_rms[row];
+    float s = 0.0f;
+    for (int j = threadIdx.x; j < a.dim; j += blockDim.x) {
+      const float gf = C::load1(a.g, row * a.ld_g + j);
+      float xh = C::load1(a.saved, row * a.ld_s + j);
+      if constexpr (SAVED_IS_H) xh = xh * rr;
+      const float gw = has_w ? gf * CW::load1(a.w, j) : gf;
+      s += gw * xh;
+    }
+    s = row_sum(s, blockDim.x, 0, red[it & 1]);
+    const float m = s / (float)a.dim;
+    for (int j = threadIdx.x; j < a.dim; j += blockDim.x) {
+      const float gf = C::load1(a.g, row * a.ld_g + j);
+      float xh = C::load1(a.saved, row * a.ld_s + j);
+      if constexpr (SAVED_IS_H) xh = xh * rr;
+      const float gw = has_w ? gf * CW::load1(a.w, j) : gf;
+      const float d = rr * (gw - xh * m);
+      C::store1(a.dx, row * a.ld_dx + j, d);
+      if (has_dres) C::store1(a.dres, row * a.ld_dres + j, d);
+      if (prow != nullptr) {
+        const float p = gf * xh;
+        prow[j] = (it == 0) ? p : prow[j] + p;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// dweight stage 2: dweight[j] = sum over partial rows p = 0..nparts-1, in a fixed order.
+// A workgroup owns 64 columns; wave w sums rows p = w, w + W, ... and the W wave sums are
+// added in wave order.
+// ------------------------------------------------------------------------------------------
+constexpr int kReduceBlock = 1024;
+__global__ __launch_bounds__(kReduceBlock) void dweight_reduce_kernel(const float* partial,
+                                                                       int32_t nparts,
+                                                                       int32_t dim,
+                                                                       float* dweight) {
+  __shared__ float red[kReduceBlock / kWave][kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int col = blockIdx.x * kWave + lane;
+  float s = 0.0f;
+  if (col < dim) {
+    for (int p = wave; p < nparts; p += nw) s += partial[(int64_t)p * dim + col];
+  }
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && col < dim) {
+    float t = red[0][lane];
+    for (int w = 1; w < nw; ++w) t += red[w][lane];
+    dweight[col] = t;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Host side: errors, device facts, launch plans.
+// ------------------------------------------------------------------------------------------
+thread_local char g_last_error[512] = "";
+
+int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int32_t fail(int32_t code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int32_t check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail((int32_t)e, "%s: launch failed: %s", what, hipGetErrorString(e));
+  g_last_error[0] = '\0';
+  return 0;
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int cu_count(int device) {
+  if (device < 0 || device >= kMaxDevices) return 0;
+  int v = g_cu_count[device].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      v <= 0)
+    return 0;
+  g_cu_count[device].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+int env_int(const char* name, int dflt, int lo, int hi) {
+  const char* s = getenv(name);
+  if (s == nullptr || *s == '\0') return dflt;
+  const long v = strtol(s, nullptr, 10);
+  if (v < lo || v > hi) return dflt;
+  return (int)v;
+}
+
+struct Tuning {
+  int fwd_nv;             // preferred 16-byte chunks per thread, forward (0 = automatic)
+  int bwd_nv;             // same, backward
+  int bwd_waves_per_cu;   // resident waves per CU targeted by the persistent backward grid
+};
+
+const Tuning& tuning() {
+  static const Tuning t = {
+      env_int("VELOGRAD_FWD_NV", 0, 0, kMaxNV),
+      env_int("VELOGRAD_BWD_NV", 0, 0, kMaxNV),
+      env_int("VELOGRAD_BWD_WAVES_PER_CU", 16, 1, 64),
+  };
+  return t;
+}
+
+struct RowPlan {
+  bool vec;    // register-resident path
+  int nv;      // 16-byte chunks per thread
+  int tpr;     // threads per row
+  int groups;  // rows per workgroup
+  int block;   // threads per workgroup
+};
+
+// Register-resident layout for rows of `dim` elements of `elem_bytes` bytes, or the generic
+// plan when the row does not split into 16-byte chunks or does not fit in registers.
+RowPlan plan_rows(int64_t dim, int elem_bytes, bool aligned, int prefer_nv) {
+  const int V = 16 / elem_bytes;
+  RowPlan p{false, 0, kGenericBlock, 1, kGenericBlock};
+  if (!aligned || dim <= 0 || dim % V != 0) return p;
+  const int64_t chunks = dim / V;
+  if (chunks > (int64_t)kMaxWavesPerRow * kWave * kMaxNV) return p;
+  // Preference order: few chunks per thread keeps registers low and waves many; take the first
+  // choice whose idle lanes stay under 1/8, else the least idle one.
+  const int order_auto[4] = {2, 3, 4, 1};
+  int order[4];
+  int n = 0;
+  if (prefer_nv > 0) order[n++] = prefer_nv;
+  for (int i = 0; i < 4; ++i)
+    if (order_auto[i] != prefer_nv) order[n++] = order_auto[i];
+  int best_nv = 0, best_wpr = 0;
+  int64_t best_waste = -1;
+  for (int i = 0; i < n; ++i) {
+    const int nv = order[i];
+    const int64_t wpr = (chunks + (int64_t)kWave * nv - 1) / ((int64_t)kWave * nv);
+    if (wpr * kWave > max_block_for_nv(nv)) continue;
+    const int64_t slots = wpr * kWave * nv;
+    const int64_t waste = slots - chunks;
+    if (waste * 8 <= slots) {
+      best_nv = nv;
+      best_wpr = (int)wpr;
+      break;
+    }
+    if (best_waste < 0 || waste < best_waste) {
+      best_waste = waste;
+      best_nv = nv;
+      best_wpr = (int)wpr;
+    }
+  }
+  if (best_nv == 0) return p;
+  p.vec = true;
+  p.nv = best_nv;
+  p.tpr = best_wpr * kWave;
+  p.groups = p.tpr >= 256 ? 1 : 256 / p.tpr;
+  p.block = p.tpr * p.groups;
+  return p;
+}
+
+// Number of persistent row slots of the backward for a plan.
+int64_t bwd_slots(const RowPlan& p, int64_t rows, int cus) {
+  const int64_t wgs_needed = (rows + p.groups - 1) / p.groups;
+  const int waves_per_wg = p.block / kWave;
+  int64_t wg_per_cu = tuning().bwd_waves_per_cu / waves_per_wg;
+  if (wg_per_cu < 1) wg_per_cu = 1;
+  int64_t wgs = (int64_t)cus * wg_per_cu;
+  if (wgs > wgs_needed) wgs = wgs_needed;
+  if (wgs < 1) wgs = 1;
+  return wgs * p.groups;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+bool ld_ok(int64_t ld, int elem_bytes) { return ((ld * elem_bytes) & 15) == 0; }
+
+int elem_bytes_of(int32_t dt) {
+  switch (dt) {
+    case VELOGRAD_DTYPE_F32: return 4;
+    case VELOGRAD_DTYPE_F16: return 2;
+    case VELOGRAD_DTYPE_BF16: return 2;
+    default: return 0;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Typed launchers.
+// ------------------------------------------------------------------------------------------
+template <int DT, int WDT>
+void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
+  if (!p.vec) {
+    hipLaunchKernelGGL((fwd_generic_kernel<DT, WDT>), dim3((uint32_t)a.rows), dim3(p.block), 0,
+                       st, a);
+    return;
+  }
+  const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups));
+  const dim3 block(p.block);
+  switch (p.nv) {
+    case 1: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 1>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 2>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 3>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 4>), grid, block, 0, st, a); break;
+  }
+}
+
+template <int DT, int WDT, bool H>
+void launch_bwd_h(const BwdArgs& a, const RowPlan& p, int64_t slots, hipStream_t st) {
+  const dim3 grid((uint32_t)(slots / p.groups));
+  const dim3 block(p.block);
+  if (!p.vec) {
+    hipLaunchKernelGGL((bwd_generic_kernel<DT, WDT, H>), grid, block, 0, st, a);
+    return;
+  }
+  switch (p.nv) {
+    case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, H>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 2, H>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 3, H>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 4, H>), grid, block, 0, st, a); break;
+  }
+}
+
+template <int DT, int WDT>
+void launch_bwd(const BwdArgs& a, bool saved_is_h, const RowPlan& p, int64_t slots,
+                hipStream_t st) {
+  if (saved_is_h)
+    launch_bwd_h<DT, WDT, true>(a, p, slots, st);
+  else
+    launch_bwd_h<DT, WDT, false>(a, p, slots, st);
+}
+
+// Supported (dtype, w_dtype) pairs: weight in the activation dtype, or fp32.
+bool types_ok(int32_t dt, int32_t wdt) {
+  if (elem_bytes_of(dt) == 0) return false;
+  return wdt == dt || wdt == VELOGRAD_DTYPE_F32;
+}
+
+#define VG_DISPATCH_TYPES(DT, WDT, CALL)                                       \
+  do {                                                                         \
+    if ((DT) == VELOGRAD_DTYPE_F32) {                                          \
+      constexpr int kD = VELOGRAD_DTYPE_F32, kW = VELOGRAD_DTYPE_F32;          \
+      CALL;                                                                    \
+    } else if ((DT) == VELOGRAD_DTYPE_BF16 && (WDT) == VELOGRAD_DTYPE_BF16) {  \
+      constexpr int kD = VELOGRAD_DTYPE_BF16, kW = VELOGRAD_DTYPE_BF16;        \
+      CALL;                                                                    \
+    } else if ((DT) == VELOGRAD_DTYPE_BF16) {                                  \
+      constexpr int kD = VELOGRAD_DTYPE_BF16, kW = VELOGRAD_DTYPE_F32;         \
+      CALL;                                                                    \
+    } else if ((WDT) == VELOGRAD_DTYPE_F16) {                                  \
+      constexpr int kD = VELOGRAD_DTYPE_F16, kW = VELOGRAD_DTYPE_F16;          \
+      CALL;                                                                    \
+    } else {                                                                   \
+      constexpr int kD = VELOGRAD_DTYPE_F16, kW = VELOGRAD_DTYPE_F32;          \
+      CALL;                                                                    \
+    }                                                                          \
+  } while (0)
+
+size_t workspace_bytes_for(int64_t rows, int64_t dim, int cus) {
+  if (rows <= 0 || dim <= 0 || cus <= 0) return 0;
+  // The plan depends on dtype and alignment, which the query does not know: return the
+  // largest need over every plan the backward can pick.
+  int64_t most = 0;
+  const int sizes[2] = {2, 4};
+  for (int si = 0; si < 2; ++si) {
+    for (int al = 0; al < 2; ++al) {
+      const RowPlan p = plan_rows(dim, sizes[si], al != 0, tuning().bwd_nv);
+      const int64_t s = bwd_slots(p, rows, cus);
+      if (s > most) most = s;
+    }
+  }
+  return (size_t)most * (size_t)dim * sizeof(float);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------
+// C ABI.
+// ------------------------------------------------------------------------------------------
+extern "C" {
+
+VELOGRAD_API const char* velograd_kernels_version(void) { return VG_VERSION_STRING; }
+
+VELOGRAD_API const char* velograd_kernels_last_error(void) { return g_last_error; }
+
+VELOGRAD_API size_t velograd_rmsnorm_residual_bwd_workspace_bytes(int64_t rows, int64_t dim,
+                                                                  int32_t device) {
+  return workspace_bytes_for(rows, dim, cu_count(device));
+}
+
+VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(const void* x, const void* residual,
+                                                   const void* weight, void* y, void* h,
+                                                   float* inv_rms, int64_t rows, int64_t dim,
+                                                   int64_t ld_x, int64_t ld_res, int64_t ld_y,
+                                                   int64_t ld_h, int32_t dtype, int32_t w_dtype,
+                                                   float eps, void* hip_stream) {
+  if (!types_ok(dtype, w_dtype))
+    return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
+                "fwd: unsupported dtype/w_dtype pair (%d, %d): weight must be the activation "
+                "dtype or fp32",
+                (int)dtype, (int)w_dtype);
+  if (rows < 0 || dim <= 0 || dim > INT32_MAX)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: invalid shape rows=%lld dim=%lld",
+                (long long)rows, (long long)dim);
+  if (rows == 0) {
+    g_last_error[0] = '\0';
+    return 0;
+  }
+  if (x == nullptr || y == nullptr)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: x and y must not be NULL");
+  if (residual == nullptr) h = nullptr;  // h is x itself
+  if (ld_x < dim || ld_y < dim || (residual && ld_res < dim) || (h && ld_h < dim))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "fwd: row strides must be >= dim (ld_x=%lld ld_res=%lld ld_y=%lld ld_h=%lld)",
+                (long long)ld_x, (long long)ld_res, (long long)ld_y, (long long)ld_h);
+  if (y == x || y == residual || (h && (h == x || h == residual || h == y)))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: outputs must not alias inputs");
+  if (rows > INT32_MAX)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: rows=%lld exceeds the grid limit",
+                (long long)rows);
+
+  const int eb = elem_bytes_of(dtype);
+  const bool aligned = aligned16(x) && aligned16(y) && ld_ok(ld_x, eb) && ld_ok(ld_y, eb) &&
+                       (!residual || (aligned16(residual) && ld_ok(ld_res, eb))) &&
+                       (!h || (aligned16(h) && ld_ok(ld_h, eb))) && (!weight || aligned16(weight));
+  const RowPlan p = plan_rows(dim, eb, aligned, tuning().fwd_nv);
+
+  FwdArgs a;
+  a.x = x;
+  a.res = residual;
+  a.w = weight;
+  a.y = y;
+  a.h = h;
+  a.inv_rms = inv_rms;
+  a.rows = rows;
+  a.ld_x = ld_x;
+  a.ld_res = ld_res;
+  a.ld_y = ld_y;
+  a.ld_h = ld_h;
+  a.dim = (int32_t)dim;
+  a.tpr = p.tpr;
+  a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(hip_stream);
+  VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW>(a, p, st)));
+  return check_launch("velograd_rmsnorm_residual_fwd");
+}
+
+VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
+    const void* grad_y, const void* saved, int32_t saved_is_h, const void* weight,
+    const float* inv_rms, void* dx, void* dres, float* dweight, void* workspace,
+    size_t ws_bytes, int64_t rows, int64_t dim, int64_t ld_g, int64_t ld_saved, int64_t ld_dx,
+    int64_t ld_dres, int32_t dtype, int32_t w_dtype, void* hip_stream) {
+  if (!types_ok(dtype, w_dtype))
+    return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
+                "bwd: unsupported dtype/w_dtype pair (%d, %d): weight must be the activation "
+                "dtype or fp32",
+                (int)dtype, (int)w_dtype);
+  if (rows < 0 || dim <= 0 || dim > INT32_MAX)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: invalid shape rows=%lld dim=%lld",
+                (long long)rows, (long long)dim);
+  if (weight == nullptr) dweight = nullptr;  // no weight, no weight gradient (fused.py:62-65)
+  hipStream_t st = static_cast<hipStream_t>(hip_stream);
+  if (rows == 0) {
+    // Sum over zero rows: dweight = 0, written by stage 2 with no partial rows.
+    if (dweight != nullptr) {
+      hipLaunchKernelGGL(dweight_reduce_kernel, dim3((uint32_t)((dim + kWave - 1) / kWave)),
+                         dim3(kReduceBlock), 0, st, (const float*)nullptr, 0, (int32_t)dim,
+                         dweight);
+      return check_launch("velograd_rmsnorm_residual_bwd(dweight)");
+    }
+    g_last_error[0] = '\0';
+    return 0;
+  }
+  if (grad_y == nullptr || saved == nullptr || inv_rms == nullptr || dx == nullptr)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "bwd: grad_y, saved, inv_rms and dx must not be NULL");
+  if (ld_g < dim || ld_saved < dim || ld_dx < dim || (dres && ld_dres < dim))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "bwd: row strides must be >= dim (ld_g=%lld ld_saved=%lld ld_dx=%lld "
+                "ld_dres=%lld)",
+                (long long)ld_g, (long long)ld_saved, (long long)ld_dx, (long long)ld_dres);
+  if (dx == grad_y || dx == saved || dx == dres || (dres && (dres == grad_y || dres == saved)))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: outputs must not alias inputs");
+
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess)
+    return fail(VELOGRAD_ERR_DEVICE_QUERY, "bwd: hipGetDevice failed");
+  const int cus = cu_count(device);
+  if (cus <= 0) return fail(VELOGRAD_ERR_DEVICE_QUERY, "bwd: cannot query the CU count");
+
+  const int eb = elem_bytes_of(dtype);
+  const bool aligned = aligned16(grad_y) && aligned16(saved) && aligned16(dx) &&
+                       ld_ok(ld_g, eb) && ld_ok(ld_saved, eb) && ld_ok(ld_dx, eb) &&
+                       (!dres || (aligned16(dres) && ld_ok(ld_dres, eb))) &&
+                       (!weight || aligned16(weight));
+  const RowPlan p = plan_rows(dim, eb, aligned, tuning().bwd_nv);
+  const int64_t slots = bwd_slots(p, rows, cus);
+  if (slots / p.groups > INT32_MAX)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: grid too large");
+
+  float* partial = nullptr;
+  if (dweight != nullptr) {
+    const size_t need = (size_t)slots * (size_t)dim * sizeof(float);
+    if (workspace == nullptr || ws_bytes < need)
+      return fail(VELOGRAD_ERR_WORKSPACE_TOO_SMALL,
+                  "bwd: workspace of %zu bytes given, %zu needed", ws_bytes, need);
+    if (!aligned16(workspace))
+      return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: workspace must be 16-byte aligned");
+    partial = static_cast<float*>(workspace);
+  }
+
+  BwdArgs a;
+  a.g = grad_y;
+  a.saved = saved;
+  a.w = weight;
+  a.inv_rms = inv_rms;
+  a.dx = dx;
+  a.dres = dres;
+  a.partial = partial;
+  a.rows = rows;
+  a.ld_g = ld_g;
+  a.ld_s = ld_saved;
+  a.ld_dx = ld_dx;
+  a.ld_dres = ld_dres;
+  a.dim = (int32_t)dim;
+  a.tpr = p.tpr;
+  a.iters = (int32_t)((rows + slots - 1) / slots);
+  VG_DISPATCH_TYPES(dtype, w_dtype, (launch_bwd<kD, kW>(a, saved_is_h != 0, p, slots, st)));
+  int32_t rc = check_launch("velograd_rmsnorm_residual_bwd");
+  if (rc != 0 || dweight == nullptr) return rc;
+  hipLaunchKernelGGL(dweight_reduce_kernel, dim3((uint32_t)((dim + kWave - 1) / kWave)),
+                     dim3(kReduceBlock), 0, st, (const float*)partial, (int32_t)slots,
+                     (int32_t)dim, dweight);
+  return check_launch("velograd_rmsnorm_residual_bwd(dweight)");
+}
+
+}  // extern "C"

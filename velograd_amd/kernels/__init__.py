@@ -1,0 +1,303 @@
+"""Drop-in `velograd.kernels` fused RMSNorm + residual functions on MI355X HIP kernels.
+
+Same names, positional order, defaults and return arity as the reference:
+
+  fused_rmsnorm_residual_forward(x, residual=None, weight=None, eps=1e-6) -> (y, h, inv_rms)
+      python/velograd/kernels/fused.py:28-46
+  fused_rmsnorm_residual_backward(grad_out, normed_input, weight, inv_rms) -> (grad_x, grad_weight)
+      python/velograd/kernels/fused.py:48-66
+  fused_rmsnorm_residual(x, residual=None, weight=None, eps=1e-6) -> y
+      python/velograd/kernels/__init__.py:19-32
+
+Inputs
+  * torch tensors on a ROCm device (torch's device type is named "cuda") run in their own dtype
+    (float32, float16 or bfloat16; fp32 arithmetic inside): y, h and grad_x come back in that
+    dtype, inv_rms ([..., 1]) and grad_weight ([D]) in float32.
+  * NumPy arrays, lists and CPU tensors follow the reference wrapper
+    (python/velograd/kernels/__init__.py:21-27): they are cast to float32, computed on the GPU
+    and returned as float32 NumPy arrays.
+There is no CPU implementation behind these functions: without the HIP library or a visible
+ROCm device they raise.
+
+Reference semantics kept: the last axis is normalised and every leading axis is a row;
+`residual=None` makes `h` the very object `x` (fused.py:39); `weight=None` skips the scale and
+returns `grad_weight=None` (fused.py:44-45, 62-65); NaN and Inf propagate (no clamping);
+`normed_input` of the backward is xhat = h * inv_rms, before the weight.  Since h = x + residual,
+`grad_x` is also the gradient of `residual`.
+
+Additions (keyword-only, off by default): `saved_is_h=True` lets the backward take h instead of
+xhat (xhat is then formed in registers; same bytes moved), and `dresidual_out=` receives a
+second copy of grad_x in a caller-owned buffer.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional, Tuple
+
+import numpy as np
+import torch
+
+from .. import _lib
+
+__all__ = [
+    "fused_rmsnorm_residual",
+    "fused_rmsnorm_residual_forward",
+    "fused_rmsnorm_residual_backward",
+    "bwd_workspace_bytes",
+]
+
+
+# ---------------------------------------------------------------------------------------------
+# Argument handling
+# ---------------------------------------------------------------------------------------------
+def _is_device_tensor(t: Any) -> bool:
+    return isinstance(t, torch.Tensor) and t.device.type == "cuda"
+
+
+def _require_gpu() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError(
+            "velograd_amd.kernels computes on an MI355X and no ROCm device is visible; "
+            "there is no CPU fallback")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _rows_view(t: torch.Tensor, name: str) -> torch.Tensor:
+    """[..., D] -> [rows, D] with unit stride along D (a view when possible, else a copy)."""
+    if t.dim() == 0:
+        raise ValueError(f"{name} must have at least one dimension")
+    d = t.shape[-1]
+    if t.dim() == 1:
+        t2 = t.unsqueeze(0)
+    else:
+        try:
+            t2 = t.view(-1, d)
+        except RuntimeError:
+            t2 = t.reshape(-1, d)
+    if d > 0 and t2.shape[0] > 0 and t2.stride(-1) != 1:
+        t2 = t2.contiguous()
+    return t2
+
+
+def _ld(t2: torch.Tensor) -> int:
+    # Row stride in elements; a single row may report any stride, use D then.
+    return t2.stride(0) if t2.shape[0] > 1 else t2.shape[1]
+
+
+def _dtype_code(t: torch.Tensor, name: str) -> int:
+    code = _lib.TORCH_DTYPE_CODES.get(t.dtype)
+    if code is None:
+        raise TypeError(f"{name}: unsupported dtype {t.dtype}; use float32, float16 or bfloat16")
+    return code
+
+
+def _prep_weight(weight: Optional[torch.Tensor], d: int, act_dtype: torch.dtype,
+                 device: torch.device) -> Tuple[Optional[torch.Tensor], int]:
+    """Weight as a contiguous [D] tensor in the activation dtype or float32."""
+    if weight is None:
+        return None, _lib.TORCH_DTYPE_CODES[act_dtype]
+    if not isinstance(weight, torch.Tensor):
+        weight = torch.as_tensor(np.asarray(weight, dtype=np.float32), device=device)
+    if weight.device != device:
+        raise ValueError(f"weight is on {weight.device}, activations on {device}")
+    if weight.numel() != d:
+        raise ValueError(f"weight has {weight.numel()} elements, expected {d} (shape [D] or [1, D])")
+    w = weight.reshape(d)
+    if w.dtype not in (act_dtype, torch.float32):
+        w = w.to(torch.float32)
+    w = w.contiguous()
+    return w, _lib.TORCH_DTYPE_CODES[w.dtype]
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def bwd_workspace_bytes(rows: int, dim: int, device: Optional[torch.device] = None) -> int:
+    """Bytes of scratch the backward needs for the two-stage dweight reduction."""
+    dev = device if device is not None else _require_gpu()
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return int(_lib.load().velograd_rmsnorm_residual_bwd_workspace_bytes(rows, dim, idx))
+
+
+# ---------------------------------------------------------------------------------------------
+# Device paths
+# ---------------------------------------------------------------------------------------------
+def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
+                    weight: Optional[torch.Tensor], eps: float):
+    lib = _lib.load()
+    device = x.device
+    code = _dtype_code(x, "x")
+    if residual is not None:
+        if not isinstance(residual, torch.Tensor) or residual.device != device:
+            raise ValueError("residual must be a tensor on the same device as x")
+        if residual.dtype != x.dtype:
+            raise TypeError(f"residual dtype {residual.dtype} differs from x dtype {x.dtype}")
+        if residual.shape != x.shape:
+            # NumPy broadcasting of `x + residual` (fused.py:39), materialised.
+            x, residual = torch.broadcast_tensors(x, residual)
+            x, residual = x.contiguous(), residual.contiguous()
+    out_shape = x.shape
+    d = out_shape[-1] if x.dim() > 0 else 0
+    w, wcode = _prep_weight(weight, d, x.dtype, device)
+
+    x2 = _rows_view(x, "x")
+    rows = x2.shape[0]
+    y = torch.empty(out_shape, dtype=x.dtype, device=device)
+    h = torch.empty(out_shape, dtype=x.dtype, device=device) if residual is not None else x
+    inv_rms = torch.empty(tuple(out_shape[:-1]) + (1,), dtype=torch.float32, device=device)
+    if rows == 0:
+        return y, h, inv_rms
+    if d == 0:
+        # mean over an empty axis is NaN in NumPy; y and h are empty.
+        inv_rms.fill_(float("nan"))
+        return y, h, inv_rms
+
+    r2 = _rows_view(residual, "residual") if residual is not None else None
+    y2 = y.view(-1, d)
+    h2 = h.view(-1, d) if residual is not None else None
+    with torch.cuda.device(device):
+        rc = lib.velograd_rmsnorm_residual_fwd(
+            x2.data_ptr(), _ptr(r2), _ptr(w),
+            y2.data_ptr(), _ptr(h2), inv_rms.data_ptr(),
+            rows, d,
+            _ld(x2), _ld(r2) if r2 is not None else d, d, d,
+            code, wcode, float(eps), _stream(device))
+    _lib.check(rc, "velograd_rmsnorm_residual_fwd")
+    return y, h, inv_rms
+
+
+def _backward_device(grad_out: torch.Tensor, saved: torch.Tensor,
+                     weight: Optional[torch.Tensor], inv_rms: torch.Tensor,
+                     saved_is_h: bool, dresidual_out: Optional[torch.Tensor]):
+    lib = _lib.load()
+    device = grad_out.device
+    code = _dtype_code(grad_out, "grad_out")
+    if not isinstance(saved, torch.Tensor) or saved.device != device:
+        raise ValueError("normed_input must be a tensor on the same device as grad_out")
+    if saved.dtype != grad_out.dtype:
+        raise TypeError(f"normed_input dtype {saved.dtype} differs from grad_out dtype "
+                        f"{grad_out.dtype}")
+    if saved.shape != grad_out.shape:
+        raise ValueError(f"normed_input shape {tuple(saved.shape)} differs from grad_out shape "
+                         f"{tuple(grad_out.shape)}")
+    shape = grad_out.shape
+    d = shape[-1] if grad_out.dim() > 0 else 0
+    w, wcode = _prep_weight(weight, d, grad_out.dtype, device)
+
+    g2 = _rows_view(grad_out, "grad_out")
+    s2 = _rows_view(saved, "normed_input")
+    rows = g2.shape[0]
+    if not isinstance(inv_rms, torch.Tensor) or inv_rms.device != device:
+        raise ValueError("inv_rms must be a tensor on the same device as grad_out")
+    if inv_rms.numel() != rows:
+        raise ValueError(f"inv_rms has {inv_rms.numel()} elements, expected one per row ({rows})")
+    r = inv_rms.reshape(rows)
+    if r.dtype != torch.float32:
+        r = r.to(torch.float32)
+    r = r.contiguous()
+
+    dx = torch.empty(shape, dtype=grad_out.dtype, device=device)
+    dres2 = None
+    if dresidual_out is not None:
+        if (not isinstance(dresidual_out, torch.Tensor) or dresidual_out.shape != shape
+                or dresidual_out.dtype != grad_out.dtype or dresidual_out.device != device
+                or not dresidual_out.is_contiguous()):
+            raise ValueError("dresidual_out must be a contiguous tensor shaped and typed like "
+                             "grad_out on the same device")
+        dres2 = dresidual_out.view(-1, d) if d > 0 else None
+    dweight = torch.empty((d,), dtype=torch.float32, device=device) if w is not None else None
+    if d == 0:
+        return dx, dweight
+    if rows == 0:
+        if dweight is not None:
+            dweight.zero_()
+        return dx, dweight
+
+    ws = None
+    ws_bytes = 0
+    if dweight is not None:
+        ws_bytes = bwd_workspace_bytes(rows, d, device)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=device)
+    dx2 = dx.view(-1, d)
+    with torch.cuda.device(device):
+        rc = lib.velograd_rmsnorm_residual_bwd(
+            g2.data_ptr(), s2.data_ptr(), 1 if saved_is_h else 0,
+            _ptr(w), r.data_ptr(),
+            dx2.data_ptr(), _ptr(dres2), _ptr(dweight),
+            _ptr(ws), ws_bytes,
+            rows, d,
+            _ld(g2), _ld(s2), d, d,
+            code, wcode, _stream(device))
+    _lib.check(rc, "velograd_rmsnorm_residual_bwd")
+    return dx, dweight
+
+
+# ---------------------------------------------------------------------------------------------
+# Host (array-like) inputs: reference wrapper semantics, computed on the GPU.
+# ---------------------------------------------------------------------------------------------
+def _host_to_device_f32(a: Any, device: torch.device) -> torch.Tensor:
+    if isinstance(a, torch.Tensor):
+        a = a.detach().cpu().numpy()
+    arr = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+    return torch.from_numpy(arr).to(device)
+
+
+def _to_host(t: Optional[torch.Tensor]) -> Optional[np.ndarray]:
+    return None if t is None else t.cpu().numpy()
+
+
+# ---------------------------------------------------------------------------------------------
+# Public API
+# ---------------------------------------------------------------------------------------------
+def fused_rmsnorm_residual_forward(x: Any, residual: Optional[Any] = None,
+                                   weight: Optional[Any] = None, eps: float = 1e-6):
+    """(x + residual) -> RMS-normalise over the last axis -> scale by weight.
+
+    Returns (normed_output, combined_residual, inv_rms) like fused.py:28-46.
+    """
+    if _is_device_tensor(x):
+        return _forward_device(x, residual, weight, eps)
+    device = _require_gpu()
+    xd = _host_to_device_f32(x, device)
+    rd = _host_to_device_f32(residual, device) if residual is not None else None
+    wd = _host_to_device_f32(weight, device) if weight is not None else None
+    if wd is not None and wd.numel() != xd.shape[-1]:
+        raise ValueError(f"weight has {wd.numel()} elements, expected {xd.shape[-1]}")
+    y, h, inv_rms = _forward_device(xd, rd, wd, eps)
+    y_np = _to_host(y)
+    # With residual=None the reference returns its (float32) x as h.
+    h_np = _to_host(h) if residual is not None else np.asarray(x, dtype=np.float32)
+    return y_np, h_np, _to_host(inv_rms)
+
+
+def fused_rmsnorm_residual_backward(grad_out: Any, normed_input: Any, weight: Optional[Any],
+                                    inv_rms: Any, *, saved_is_h: bool = False,
+                                    dresidual_out: Optional[torch.Tensor] = None):
+    """Analytic backward of the forward; returns (grad_x, grad_weight) like fused.py:48-66.
+
+    `normed_input` is xhat = h * inv_rms (or h itself with saved_is_h=True); grad_weight is None
+    when weight is None.
+    """
+    if _is_device_tensor(grad_out):
+        return _backward_device(grad_out, normed_input, weight, inv_rms, saved_is_h,
+                                dresidual_out)
+    if dresidual_out is not None:
+        raise ValueError("dresidual_out is only supported for device tensors")
+    device = _require_gpu()
+    gd = _host_to_device_f32(grad_out, device)
+    sd = _host_to_device_f32(normed_input, device)
+    wd = _host_to_device_f32(weight, device) if weight is not None else None
+    rd = _host_to_device_f32(inv_rms, device)
+    dx, dw = _backward_device(gd, sd, wd, rd, saved_is_h, None)
+    return _to_host(dx), _to_host(dw)
+
+
+def fused_rmsnorm_residual(x: Any, residual: Optional[Any] = None, weight: Optional[Any] = None,
+                           eps: float = 1e-6):
+    """Wrapper returning only the normalised output, like kernels/__init__.py:19-32."""
+    return fused_rmsnorm_residual_forward(x, residual, weight, eps)[0]
