@@ -61,7 +61,12 @@ struct Codec<VELOGRAD_DTYPE_F32> {
   static constexpr int kVec = 4;
   __device__ static inline void unpack(const u32x4 v, float* f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, v[i]);
+    for (int i = 0; i < 4; ++i) {
+      // Copy the element out first: hipcc 7.2 bit-casts an ext_vector element lvalue
+      // (`__builtin_bit_cast(float, v[i])`) as element 0 whatever i is.
+      const uint32_t u = v[i];
+      f[i] = __builtin_bit_cast(float, u);
+    }
   }
   __device__ static inline u32x4 pack(const float* f) {
     u32x4 v;
@@ -113,7 +118,8 @@ struct Codec<VELOGRAD_DTYPE_F16> {
   __device__ static inline void unpack(const u32x4 v, float* f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const f16x2 h = __builtin_bit_cast(f16x2, v[i]);
+      const uint32_t u = v[i];  // scalar copy: see the fp32 codec
+      const f16x2 h = __builtin_bit_cast(f16x2, u);
       f[2 * i] = (float)h[0];
       f[2 * i + 1] = (float)h[1];
     }

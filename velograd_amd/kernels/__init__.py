@@ -32,6 +32,7 @@ second copy of grad_x in a caller-owned buffer.
 
 from __future__ import annotations
 
+import math
 from typing import Any, Optional, Tuple
 
 import numpy as np
@@ -67,13 +68,14 @@ def _rows_view(t: torch.Tensor, name: str) -> torch.Tensor:
     if t.dim() == 0:
         raise ValueError(f"{name} must have at least one dimension")
     d = t.shape[-1]
+    rows = math.prod(t.shape[:-1])
     if t.dim() == 1:
         t2 = t.unsqueeze(0)
     else:
         try:
-            t2 = t.view(-1, d)
+            t2 = t.view(rows, d)
         except RuntimeError:
-            t2 = t.reshape(-1, d)
+            t2 = t.reshape(rows, d)
     if d > 0 and t2.shape[0] > 0 and t2.stride(-1) != 1:
         t2 = t2.contiguous()
     return t2
