@@ -1,0 +1,116 @@
+// CPU check of the kernels' launch planner (velograd_amd/csrc/launch_plan.h), built by
+// tests/test_launch_plan.py with AddressSanitizer and UBSan.  For every row length, element
+// size, alignment, tuning preference and row count it checks the facts the kernels rely on:
+//   * the register-resident plan covers every 16-byte chunk of a row exactly once, with whole
+//     wave64s per row, and its workgroup fits the kernel's launch bound for that NV;
+//   * the backward's workgroups, LDS and partial rows fit the workspace the size query reports.
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <vector>
+
+#include "launch_plan.h"
+
+using namespace vg_plan;
+
+static int failures = 0;
+
+#define CHECK(cond, ...)                                   \
+  do {                                                     \
+    if (!(cond)) {                                         \
+      if (failures < 20) {                                 \
+        fprintf(stderr, "FAIL %s:%d: %s: ", __FILE__, __LINE__, #cond); \
+        fprintf(stderr, __VA_ARGS__);                      \
+        fputc('\n', stderr);                               \
+      }                                                    \
+      ++failures;                                          \
+    }                                                      \
+  } while (0)
+
+static void check_row_plan(const RowPlan& p, int64_t dim, int eb, bool aligned) {
+  const int V = 16 / eb;
+  CHECK(row_plan_valid(p, dim, eb), "row_plan_valid rejects a plan the planner made (dim=%lld)",
+        (long long)dim);
+  if (!p.vec) {
+    CHECK(p.block == kGenericBlock && p.groups == 1 && p.tpr == kGenericBlock,
+          "generic plan shape dim=%lld", (long long)dim);
+    return;
+  }
+  CHECK(aligned && dim % V == 0, "vector plan for unaligned/ragged dim=%lld", (long long)dim);
+  CHECK(p.nv >= 1 && p.nv <= kMaxNV, "nv=%d", p.nv);
+  CHECK(p.tpr >= kWave && p.tpr % kWave == 0, "tpr=%d", p.tpr);
+  CHECK(p.groups >= 1 && p.block == p.tpr * p.groups, "groups=%d block=%d", p.groups, p.block);
+  CHECK(p.block <= max_block_for_nv(p.nv), "block %d over bound for nv %d", p.block, p.nv);
+  const int64_t nchunk = dim / V;
+  CHECK((int64_t)p.nv * p.tpr >= nchunk, "plan covers %lld of %lld chunks",
+        (long long)p.nv * p.tpr, (long long)nchunk);
+  // Exactly-once coverage of the chunks by (lane, k) as the kernels index them.
+  if (nchunk <= 4096) {
+    std::vector<int> seen((size_t)nchunk, 0);
+    for (int lt = 0; lt < p.tpr; ++lt)
+      for (int k = 0; k < p.nv; ++k) {
+        const int64_t c = lt + (int64_t)k * p.tpr;
+        if (c < nchunk) seen[(size_t)c]++;
+      }
+    for (int64_t c = 0; c < nchunk; ++c)
+      CHECK(seen[(size_t)c] == 1, "chunk %lld seen %d times (dim=%lld)", (long long)c,
+            seen[(size_t)c], (long long)dim);
+  }
+}
+
+int main() {
+  const int cus_list[3] = {1, 80, 256};
+  const int64_t rows_list[6] = {1, 7, 64, 257, 16384, 32768};
+  long plans = 0;
+  for (int eb = 2; eb <= 4; eb += 2) {
+    for (int aligned = 0; aligned < 2; ++aligned) {
+      for (int64_t dim = 1; dim <= 70000; dim += (dim < 2048 ? 1 : 61)) {
+        for (int prefer = -1; prefer <= kMaxNV + 1; ++prefer) {
+          const RowPlan p = plan_rows(dim, eb, aligned != 0, prefer);
+          check_row_plan(p, dim, eb, aligned != 0);
+          ++plans;
+        }
+      }
+    }
+  }
+  // Backward plans and the workspace query, on the dims the benchmarks and tests use plus a
+  // spread of others, for every tuning knob value range.
+  const int64_t dims[] = {1, 4, 13, 16, 64, 100, 768, 4096, 4104, 5120, 7168, 8192, 16384,
+                          20000, 40000};
+  for (int64_t dim : dims) {
+    for (int64_t rows : rows_list) {
+      for (int cus : cus_list) {
+        for (int prefer = 0; prefer <= kMaxNV; ++prefer) {
+          for (int max_block = 64; max_block <= 1024; max_block *= 2) {
+            for (int waves = 1; waves <= 64; waves *= 2) {
+              const size_t ws = bwd_workspace_bytes(rows, dim, cus, prefer, max_block, waves);
+              for (int eb = 2; eb <= 4; eb += 2) {
+                for (int aligned = 0; aligned < 2; ++aligned) {
+                  const BwdPlan b =
+                      plan_bwd(rows, dim, eb, aligned != 0, cus, prefer, max_block, waves);
+                  check_row_plan(b.rp, dim, eb, aligned != 0);
+                  CHECK(b.wgs >= 1 && b.wgs <= (rows + b.rp.groups - 1) / b.rp.groups,
+                        "wgs=%lld rows=%lld groups=%d", (long long)b.wgs, (long long)rows,
+                        b.rp.groups);
+                  CHECK((size_t)b.wgs * (size_t)dim * sizeof(float) <= ws,
+                        "partials %lld x %lld exceed workspace %zu", (long long)b.wgs,
+                        (long long)dim, ws);
+                  CHECK(b.lds_bytes <= 64 * 1024, "lds %zu", b.lds_bytes);
+                  CHECK(b.lds_bytes == 0 || (b.rp.vec && b.rp.groups > 1),
+                        "lds without a group combine");
+                  ++plans;
+                }
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+  if (failures) {
+    fprintf(stderr, "%d failures over %ld plans\n", failures, plans);
+    return 1;
+  }
+  printf("plan_check ok: %ld plans\n", plans);
+  return 0;
+}

@@ -350,14 +350,21 @@ def test_workspace_too_small_is_rejected():
     dw = torch.empty(512, device="cuda")
     w = torch.ones(512, device="cuda")
     inv = torch.ones(64, device="cuda")
+    # The query covers every plan the backward may pick (dtype and alignment are unknown to it),
+    # so it is at least one partial row of dim floats; a buffer smaller than that one row is
+    # too small for any plan.
     need = vk.bwd_workspace_bytes(64, 512)
-    assert need > 0
-    ws = torch.empty(need - 16, dtype=torch.uint8, device="cuda")
+    assert need >= 512 * 4
+    small = 512 * 4 - 16
+    ws = torch.empty(small, dtype=torch.uint8, device="cuda")
     rc = lib.velograd_rmsnorm_residual_bwd(
         g.data_ptr(), g.data_ptr(), 1, w.data_ptr(), inv.data_ptr(), dx.data_ptr(), None,
-        dw.data_ptr(), ws.data_ptr(), need - 16, 64, 512, 512, 512, 512, 512,
+        dw.data_ptr(), ws.data_ptr(), small, 64, 512, 512, 512, 512, 512,
         _lib.DTYPE_F32, _lib.DTYPE_F32, torch.cuda.current_stream().cuda_stream)
     assert rc == _lib.ERR_WORKSPACE_TOO_SMALL
+    assert "needed" in _lib.last_error()
+    with pytest.raises(ValueError):
+        _lib.check(rc, "bwd")
 
 
 def test_dtype_mismatch_raises():

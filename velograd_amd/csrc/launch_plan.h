@@ -1,0 +1,154 @@
+// Launch plans of the fused RMSNorm + residual kernels (host-only C++, no HIP dependency), so
+// the planner can be compiled and checked on a CPU (tests/plan_check.cpp, under ASan/UBSan).
+//
+// A row of `dim` elements is cut into 16-byte chunks (8 bf16/fp16 or 4 fp32 elements).  The
+// register-resident kernels give each row `tpr` threads (whole wave64s) and each thread NV
+// chunks, c = lane + k * tpr for k < NV, so that consecutive lanes touch consecutive 16-byte
+// chunks (coalesced 1 KiB per wave instruction).  Rows whose length is not a multiple of the
+// chunk, misaligned rows, and rows too long for registers use the generic looping kernels.
+#ifndef VELOGRAD_LAUNCH_PLAN_H
+#define VELOGRAD_LAUNCH_PLAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef VG_HOST_DEVICE
+#define VG_HOST_DEVICE
+#endif
+
+namespace vg_plan {
+
+constexpr int kWave = 64;
+constexpr int kMaxWavesPerRow = 16;  // 1024 threads per row at most
+// 16-byte chunks per thread in the register-resident path.  Capped at 4: the one-wave-per-row
+// forward with 8 chunks per thread (191 VGPRs) made an illegal memory access on MI355X although
+// its launch plan was correct (checked on the CPU by intercepting the launch); until that is
+// understood, NV 5..8 are neither planned nor compiled.
+constexpr int kMaxNV = 4;
+constexpr int kGenericBlock = 256;
+
+// Workgroup size bound of the register-resident kernels, so that a thread's packed chunks fit
+// its VGPR budget (512 VGPRs per SIMD lane shared by the block's waves on that SIMD):
+// NV <= 2 -> 1024 threads (128 VGPRs), NV 3..4 -> 512 (256).
+VG_HOST_DEVICE constexpr int max_block_for_nv(int nv) { return nv <= 2 ? 1024 : 512; }
+
+struct RowPlan {
+  bool vec;    // register-resident path
+  int nv;      // 16-byte chunks per thread
+  int tpr;     // threads per row
+  int groups;  // rows per workgroup
+  int block;   // threads per workgroup = tpr * groups
+};
+
+// Register-resident layout for rows of `dim` elements of `elem_bytes` bytes, or the generic
+// plan when the row does not split into 16-byte chunks or does not fit in registers.
+// `prefer_nv` (1..kMaxNV, 0 = automatic) is tried first.  Automatic order: few chunks per
+// thread keep registers low and waves many; the first choice whose idle lanes stay under 1/8
+// wins, else the least idle one.
+inline RowPlan plan_rows(int64_t dim, int elem_bytes, bool aligned, int prefer_nv) {
+  RowPlan p{false, 0, kGenericBlock, 1, kGenericBlock};
+  if (elem_bytes != 2 && elem_bytes != 4) return p;
+  const int V = 16 / elem_bytes;
+  if (!aligned || dim <= 0 || dim % V != 0) return p;
+  const int64_t chunks = dim / V;
+  const int order_auto[4] = {2, 3, 4, 1};
+  int order[1 + 4];
+  int n = 0;
+  if (prefer_nv >= 1 && prefer_nv <= kMaxNV) order[n++] = prefer_nv;
+  for (int i = 0; i < 4; ++i)
+    if (order_auto[i] != prefer_nv) order[n++] = order_auto[i];
+  int best_nv = 0, best_wpr = 0;
+  int64_t best_waste = -1;
+  for (int i = 0; i < n; ++i) {
+    const int nv = order[i];
+    const int64_t wpr = (chunks + (int64_t)kWave * nv - 1) / ((int64_t)kWave * nv);
+    if (wpr * kWave > max_block_for_nv(nv)) continue;
+    const int64_t slots = wpr * kWave * nv;
+    const int64_t waste = slots - chunks;
+    if (waste * 8 <= slots) {
+      best_nv = nv;
+      best_wpr = (int)wpr;
+      break;
+    }
+    if (best_waste < 0 || waste < best_waste) {
+      best_waste = waste;
+      best_nv = nv;
+      best_wpr = (int)wpr;
+    }
+  }
+  if (best_nv == 0) return p;
+  p.vec = true;
+  p.nv = best_nv;
+  p.tpr = best_wpr * kWave;
+  p.groups = p.tpr >= 256 ? 1 : 256 / p.tpr;
+  p.block = p.tpr * p.groups;
+  return p;
+}
+
+// The facts the kernels' indexing relies on; the C entry points refuse to launch a plan that
+// breaks one of them.
+inline bool row_plan_valid(const RowPlan& p, int64_t dim, int elem_bytes) {
+  if (!p.vec)
+    return p.tpr == kGenericBlock && p.groups == 1 && p.block == kGenericBlock;
+  if (elem_bytes != 2 && elem_bytes != 4) return false;
+  const int V = 16 / elem_bytes;
+  return dim > 0 && dim % V == 0 && p.nv >= 1 && p.nv <= kMaxNV && p.tpr >= kWave &&
+         p.tpr % kWave == 0 && p.groups >= 1 && p.block == p.tpr * p.groups &&
+         p.block <= max_block_for_nv(p.nv) && (int64_t)p.nv * p.tpr * V >= dim;
+}
+
+// Backward launch: row layout, row groups per workgroup, persistent grid size and dynamic LDS.
+// The register-resident kernel packs as many row groups into a workgroup as its size bound
+// allows (capped by `max_block`), because the groups' dweight columns are combined in LDS and
+// each workgroup writes one partial row: fewer, larger workgroups mean fewer partial rows for
+// stage 2.  The grid targets `waves_per_cu` resident waves on each of `cus` compute units.
+struct BwdPlan {
+  RowPlan rp;
+  int64_t wgs;       // workgroups = dweight partial rows
+  size_t lds_bytes;  // dynamic LDS of the group combine
+};
+
+inline BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
+                        int prefer_nv, int max_block, int waves_per_cu) {
+  BwdPlan b;
+  b.rp = plan_rows(dim, elem_bytes, aligned, prefer_nv);
+  RowPlan& p = b.rp;
+  if (p.vec) {
+    int mb = max_block_for_nv(p.nv);
+    if (max_block < mb) mb = max_block;
+    p.groups = mb / p.tpr;
+    if (p.groups < 1) p.groups = 1;
+    p.block = p.tpr * p.groups;
+  }
+  const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
+  int64_t wg_per_cu = waves_per_cu / (p.block / kWave);
+  if (wg_per_cu < 1) wg_per_cu = 1;
+  int64_t wgs = (int64_t)(cus > 0 ? cus : 1) * wg_per_cu;
+  if (wgs > wgs_needed) wgs = wgs_needed;
+  if (wgs < 1) wgs = 1;
+  b.wgs = wgs;
+  b.lds_bytes = (p.vec && p.groups > 1) ? (size_t)dim * sizeof(float) : 0;
+  return b;
+}
+
+// Workspace of the backward's dweight partial rows.  The plan depends on the element size and
+// on pointer alignment, which a size query does not know, so this is the largest need over
+// every plan the backward can pick for (rows, dim).
+inline size_t bwd_workspace_bytes(int64_t rows, int64_t dim, int cus, int prefer_nv,
+                                  int max_block, int waves_per_cu) {
+  if (rows <= 0 || dim <= 0 || cus <= 0) return 0;
+  int64_t most = 0;
+  const int sizes[2] = {2, 4};
+  for (int si = 0; si < 2; ++si) {
+    for (int al = 0; al < 2; ++al) {
+      const int64_t n =
+          plan_bwd(rows, dim, sizes[si], al != 0, cus, prefer_nv, max_block, waves_per_cu).wgs;
+      if (n > most) most = n;
+    }
+  }
+  return (size_t)most * (size_t)dim * sizeof(float);
+}
+
+}  // namespace vg_plan
+
+#endif  // VELOGRAD_LAUNCH_PLAN_H

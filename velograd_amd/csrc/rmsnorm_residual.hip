@@ -33,6 +33,9 @@
 
 #include "velograd_kernels.h"
 
+#define VG_HOST_DEVICE __host__ __device__
+#include "launch_plan.h"
+
 #define VG_VERSION_STRING "velograd_amd 0.1.0 fused-rmsnorm-residual gfx950"
 
 namespace {
@@ -41,13 +44,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWave = 64;
-constexpr int kMaxWavesPerRow = 16;  // 1024 threads per row at most
-constexpr int kMaxNV = 4;            // 16-byte chunks per thread in the register-resident path
-// Workgroup size bound of the register-resident kernels: with NV <= 2 chunks a thread fits in
-// 128 VGPRs (1024 threads per workgroup); NV = 3..4 get 256 VGPRs and at most 512 threads.
-__host__ __device__ constexpr int max_block_for_nv(int nv) { return nv <= 2 ? 1024 : 512; }
-constexpr int kGenericBlock = 256;
+using vg_plan::BwdPlan;
+using vg_plan::kGenericBlock;
+using vg_plan::kMaxNV;
+using vg_plan::kMaxWavesPerRow;
+using vg_plan::kWave;
+using vg_plan::max_block_for_nv;
+using vg_plan::RowPlan;
 
 // ------------------------------------------------------------------------------------------
 // Element codecs: 16 bytes <-> fp32 registers.
@@ -152,19 +155,64 @@ __device__ inline void store16(void* base, int64_t elem, const u32x4 v) {
   *reinterpret_cast<u32x4*>(static_cast<char*>(base) + elem * Codec<DT>::kBytes) = v;
 }
 
-// Weight chunk of kVec(DT) elements starting at column col0, in fp32.  The weight is stored
-// either in the activation dtype or in fp32.
-template <int DT, int WDT>
-__device__ inline void load_w_chunk(const void* w, int64_t col0, float* f) {
-  if constexpr (WDT == DT) {
-    Codec<DT>::unpack(load16<DT>(w, col0), f);
-  } else {
-    static_assert(WDT == VELOGRAD_DTYPE_F32, "weight is the activation dtype or fp32");
-#pragma unroll
-    for (int q = 0; q < Codec<DT>::kVec / 4; ++q)
-      Codec<VELOGRAD_DTYPE_F32>::unpack(load16<VELOGRAD_DTYPE_F32>(w, col0 + 4 * q), f + 4 * q);
-  }
+// Streamed activations are touched once per launch: non-temporal loads and stores keep them from
+// displacing reusable lines (weight, partial sums) in L2 and the MALL.  A stream-pattern probe
+// with the fwd (2 reads + 2 writes) and bwd (2 reads + 1 write) shapes measured +8..12% from the
+// non-temporal forms on MI355X.  Build with -DVG_STREAM_NT=0 to compare.
+#ifndef VG_STREAM_NT
+#define VG_STREAM_NT 1
+#endif
+
+template <int DT>
+__device__ inline u32x4 load16_stream(const void* base, int64_t elem) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const char*>(base) +
+                                                  elem * Codec<DT>::kBytes);
+#if VG_STREAM_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
 }
+
+template <int DT>
+__device__ inline void store16_stream(void* base, int64_t elem, const u32x4 v) {
+  u32x4* p = reinterpret_cast<u32x4*>(static_cast<char*>(base) + elem * Codec<DT>::kBytes);
+#if VG_STREAM_NT
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
+
+// The weight values of one activation chunk (kVec(DT) columns), kept packed in registers: one
+// 16-byte vector when the weight has the activation dtype, kVec/4 vectors when it is fp32.
+// No weight (NULL) reads as 1.0, which leaves (h * r) * w == h * r and g * w == g exactly.
+template <int DT, int WDT>
+struct WeightChunk {
+  static_assert(WDT == DT || WDT == VELOGRAD_DTYPE_F32, "weight is the activation dtype or fp32");
+  static constexpr int kParts = (WDT == DT) ? 1 : Codec<DT>::kVec / 4;
+  u32x4 q[kParts];
+
+  __device__ inline void load(const void* w, int64_t col0) {
+    if (w == nullptr) {
+      // fp32 1.0 in every slot, decoded through the fp32 codec below
+#pragma unroll
+      for (int i = 0; i < kParts; ++i) q[i] = u32x4{0u, 0u, 0u, 0u};
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < kParts; ++i) q[i] = load16<WDT>(w, col0 + i * Codec<WDT>::kVec);
+  }
+  __device__ inline void unpack(bool has_w, float* f) const {
+    if (!has_w) {
+#pragma unroll
+      for (int i = 0; i < Codec<DT>::kVec; ++i) f[i] = 1.0f;
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < kParts; ++i) Codec<WDT>::unpack(q[i], f + i * Codec<WDT>::kVec);
+  }
+};
 
 // ------------------------------------------------------------------------------------------
 // Reductions.
@@ -174,6 +222,11 @@ __device__ inline float dpp_move(float v) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+
+// Empty register barrier: the compiler must assume `v` changed here, so values it decoded from
+// `v` before this point are decoded again afterwards instead of being held in extra VGPRs
+// across the row reduction.  Emits no instruction.
+__device__ inline void forget(u32x4& v) { asm volatile("" : "+v"(v)); }
 
 // Sum over the 64 lanes of a wave; the result is wave-uniform.  Requires all lanes active.
 __device__ inline float wave_sum(float v) {
@@ -256,50 +309,48 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
   const bool has_res = a.res != nullptr;
   const bool has_w = a.w != nullptr;
 
+  // Only the packed 16-byte chunks stay live across the row reduction; fp32 h is formed again
+  // after it (the same single fp32 add, so the same bits), which keeps VGPRs low enough for
+  // up to 8 chunks per thread.
   u32x4 xv[NV], rv[NV];
-  float wf[NV][V];
+  WeightChunk<DT, WDT> wc[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int c = lt + k * tpr;
     xv[k] = u32x4{0u, 0u, 0u, 0u};
     rv[k] = u32x4{0u, 0u, 0u, 0u};
     if (row_ok && c < nchunk) {
-      xv[k] = load16<DT>(a.x, row * a.ld_x + (int64_t)c * V);
-      if (has_res) rv[k] = load16<DT>(a.res, row * a.ld_res + (int64_t)c * V);
+      xv[k] = load16_stream<DT>(a.x, row * a.ld_x + (int64_t)c * V);
+      if (has_res) rv[k] = load16_stream<DT>(a.res, row * a.ld_res + (int64_t)c * V);
     }
   }
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int c = lt + k * tpr;
-    if (has_w && c < nchunk) {
-      load_w_chunk<DT, WDT>(a.w, (int64_t)c * V, wf[k]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i) wf[k][i] = 1.0f;
-    }
+    wc[k].load((has_w && c < nchunk) ? a.w : nullptr, (int64_t)c * V);
   }
 
-  float hf[NV][V];
-  float ss = 0.0f;
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    C::unpack(xv[k], hf[k]);
+  auto make_h = [&](int k, float* hf) {
+    C::unpack(xv[k], hf);
     if (has_res) {
       float rf[V];
       C::unpack(rv[k], rf);
 #pragma unroll
-      for (int i = 0; i < V; ++i) hf[k][i] = hf[k][i] + rf[i];
+      for (int i = 0; i < V; ++i) hf[i] = hf[i] + rf[i];
     }
-#pragma unroll
-    for (int i = 0; i < V; ++i) ss += hf[k][i] * hf[k][i];
-  }
+  };
 
-  if (has_res && a.h != nullptr) {
+  const bool write_h = has_res && a.h != nullptr;
+  float ss = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int c = lt + k * tpr;
-      if (row_ok && c < nchunk) store16<DT>(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf[k]));
-    }
+  for (int k = 0; k < NV; ++k) {
+    float hf[V];
+    make_h(k, hf);
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss += hf[i] * hf[i];
+    const int c = lt + k * tpr;
+    if (write_h && row_ok && c < nchunk)
+      store16_stream<DT>(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf));
   }
 
   ss = row_sum(ss, tpr, grp, red);
@@ -309,15 +360,21 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
+    forget(xv[k]);
+    forget(rv[k]);
+#pragma unroll
+    for (int i = 0; i < WeightChunk<DT, WDT>::kParts; ++i) forget(wc[k].q[i]);
+  }
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
     const int c = lt + k * tpr;
     if (row_ok && c < nchunk) {
-      float yf[V];
+      float hf[V], wf[V], yf[V];
+      make_h(k, hf);
+      wc[k].unpack(has_w, wf);
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float n = hf[k][i] * r;
-        yf[i] = has_w ? n * wf[k][i] : n;
-      }
-      store16<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
+      for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
+      store16_stream<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
     }
   }
 }
@@ -375,17 +432,14 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
   const bool has_w = a.w != nullptr;
   const bool has_dres = a.dres != nullptr;
 
-  float wf[NV][V];
+  // Packed weight chunks and the fp32 dweight column accumulators live for the whole walk; the
+  // row's g and saved chunks stay packed and are decoded once per pass.
+  WeightChunk<DT, WDT> wc[NV];
   float acc[NV][V];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int c = lt + k * tpr;
-    if (has_w && c < nchunk) {
-      load_w_chunk<DT, WDT>(a.w, (int64_t)c * V, wf[k]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i) wf[k][i] = 1.0f;
-    }
+    wc[k].load((has_w && c < nchunk) ? a.w : nullptr, (int64_t)c * V);
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[k][i] = 0.0f;
   }
@@ -400,10 +454,21 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
       gv[k] = u32x4{0u, 0u, 0u, 0u};
       sv[k] = u32x4{0u, 0u, 0u, 0u};
       if (ok && c < nchunk) {
-        gv[k] = load16<DT>(a.g, row * a.ld_g + (int64_t)c * V);
-        sv[k] = load16<DT>(a.saved, row * a.ld_s + (int64_t)c * V);
+        gv[k] = load16_stream<DT>(a.g, row * a.ld_g + (int64_t)c * V);
+        sv[k] = load16_stream<DT>(a.saved, row * a.ld_s + (int64_t)c * V);
       }
     }
+  };
+  // Decoded chunk k of the current row: g, xhat (h * inv_rms when h was saved), weight.
+  auto decode = [&](const u32x4* gv, const u32x4* sv, float rr, int k, float* gf, float* xh,
+                    float* wf) {
+    C::unpack(gv[k], gf);
+    C::unpack(sv[k], xh);
+    if constexpr (SAVED_IS_H) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) xh[i] = xh[i] * rr;
+    }
+    wc[k].unpack(has_w, wf);
   };
 
   int64_t row = slot;
@@ -426,20 +491,15 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
       }
     }
 
-    float gf[NV][V], xh[NV][V];
     float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      C::unpack(gv[k], gf[k]);
-      C::unpack(sv[k], xh[k]);
-      if constexpr (SAVED_IS_H) {
-#pragma unroll
-        for (int i = 0; i < V; ++i) xh[k][i] = xh[k][i] * rr;
-      }
+      float gf[V], xh[V], wf[V];
+      decode(gv, sv, rr, k, gf, xh, wf);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        const float gw = gf[k][i] * wf[k][i];
-        s += gw * xh[k][i];
+        const float gw = gf[i] * wf[i];
+        s += gw * xh[i];
       }
     }
     s = row_sum(s, tpr, grp, red[it & 1]);
@@ -447,20 +507,27 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
 
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
+      forget(gv[k]);
+      forget(sv[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
       const int c = lt + k * tpr;
+      float gf[V], xh[V], wf[V];
+      decode(gv, sv, rr, k, gf, xh, wf);
       if (ok && c < nchunk) {
         float d[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) {
-          const float gw = gf[k][i] * wf[k][i];
-          d[i] = rr * (gw - xh[k][i] * m);
+          const float gw = gf[i] * wf[i];
+          d[i] = rr * (gw - xh[i] * m);
         }
         const u32x4 pv = C::pack(d);
-        store16<DT>(a.dx, row * a.ld_dx + (int64_t)c * V, pv);
-        if (has_dres) store16<DT>(a.dres, row * a.ld_dres + (int64_t)c * V, pv);
+        store16_stream<DT>(a.dx, row * a.ld_dx + (int64_t)c * V, pv);
+        if (has_dres) store16_stream<DT>(a.dres, row * a.ld_dres + (int64_t)c * V, pv);
       }
 #pragma unroll
-      for (int i = 0; i < V; ++i) acc[k][i] += gf[k][i] * xh[k][i];
+      for (int i = 0; i < V; ++i) acc[k][i] += gf[i] * xh[i];
     }
 
     row = nrow;
@@ -472,8 +539,11 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
     rr = rn;
   }
 
-  if (a.partial != nullptr) {
-    float* prow = a.partial + slot * (int64_t)a.dim;
+  if (a.partial == nullptr) return;
+  // One fp32 partial row per workgroup.  Row groups are added in group order through LDS
+  // (dim floats of dynamic LDS), so the partial does not depend on timing.
+  float* prow = a.partial + (int64_t)blockIdx.x * a.dim;
+  if (groups == 1) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = lt + k * tpr;
@@ -484,7 +554,25 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
                                       Codec<VELOGRAD_DTYPE_F32>::pack(&acc[k][4 * q]));
       }
     }
+    return;
   }
+  extern __shared__ __align__(16) float comb[];
+  for (int gi = 0; gi < groups; ++gi) {
+    if (grp == gi) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int c = lt + k * tpr;
+        if (c < nchunk) {
+#pragma unroll
+          for (int i = 0; i < V; ++i)
+            comb[c * V + i] = (gi == 0) ? acc[k][i] : comb[c * V + i] + acc[k][i];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  for (int q = threadIdx.x; q < a.dim / 4; q += blockDim.x)
+    store16<VELOGRAD_DTYPE_F32>(prow, 4 * (int64_t)q, *reinterpret_cast<const u32x4*>(comb + 4 * q));
 }
 
 // ------------------------------------------------------------------------------------------
@@ -549,7 +637,19 @@ __global__ __launch_bounds__(kReduceBlock) void dweight_reduce_kernel(const floa
   const int col = blockIdx.x * kWave + lane;
   float s = 0.0f;
   if (col < dim) {
-    for (int p = wave; p < nparts; p += nw) s += partial[(int64_t)p * dim + col];
+    int p = wave;
+    // Four loads in flight per lane; the additions keep ascending p order.
+    for (; p + 3 * nw < nparts; p += 4 * nw) {
+      const float v0 = partial[(int64_t)p * dim + col];
+      const float v1 = partial[(int64_t)(p + nw) * dim + col];
+      const float v2 = partial[(int64_t)(p + 2 * nw) * dim + col];
+      const float v3 = partial[(int64_t)(p + 3 * nw) * dim + col];
+      s += v0;
+      s += v1;
+      s += v2;
+      s += v3;
+    }
+    for (; p < nparts; p += nw) s += partial[(int64_t)p * dim + col];
   }
   red[wave][lane] = s;
   __syncthreads();
@@ -604,10 +704,14 @@ int env_int(const char* name, int dflt, int lo, int hi) {
   return (int)v;
 }
 
+// Launch-shape knobs, read once per process from the environment (for tuning sweeps; the
+// defaults are the measured best on MI355X).  Results do not depend on them except through the
+// dweight summation order, which stays fixed for a given setting.
 struct Tuning {
   int fwd_nv;             // preferred 16-byte chunks per thread, forward (0 = automatic)
   int bwd_nv;             // same, backward
   int bwd_waves_per_cu;   // resident waves per CU targeted by the persistent backward grid
+  int bwd_block;          // upper bound on backward workgroup size (row groups per workgroup)
 };
 
 const Tuning& tuning() {
@@ -615,72 +719,19 @@ const Tuning& tuning() {
       env_int("VELOGRAD_FWD_NV", 0, 0, kMaxNV),
       env_int("VELOGRAD_BWD_NV", 0, 0, kMaxNV),
       env_int("VELOGRAD_BWD_WAVES_PER_CU", 16, 1, 64),
+      env_int("VELOGRAD_BWD_BLOCK", 1024, 64, 1024),
   };
   return t;
 }
 
-struct RowPlan {
-  bool vec;    // register-resident path
-  int nv;      // 16-byte chunks per thread
-  int tpr;     // threads per row
-  int groups;  // rows per workgroup
-  int block;   // threads per workgroup
-};
-
-// Register-resident layout for rows of `dim` elements of `elem_bytes` bytes, or the generic
-// plan when the row does not split into 16-byte chunks or does not fit in registers.
-RowPlan plan_rows(int64_t dim, int elem_bytes, bool aligned, int prefer_nv) {
-  const int V = 16 / elem_bytes;
-  RowPlan p{false, 0, kGenericBlock, 1, kGenericBlock};
-  if (!aligned || dim <= 0 || dim % V != 0) return p;
-  const int64_t chunks = dim / V;
-  if (chunks > (int64_t)kMaxWavesPerRow * kWave * kMaxNV) return p;
-  // Preference order: few chunks per thread keeps registers low and waves many; take the first
-  // choice whose idle lanes stay under 1/8, else the least idle one.
-  const int order_auto[4] = {2, 3, 4, 1};
-  int order[4];
-  int n = 0;
-  if (prefer_nv > 0) order[n++] = prefer_nv;
-  for (int i = 0; i < 4; ++i)
-    if (order_auto[i] != prefer_nv) order[n++] = order_auto[i];
-  int best_nv = 0, best_wpr = 0;
-  int64_t best_waste = -1;
-  for (int i = 0; i < n; ++i) {
-    const int nv = order[i];
-    const int64_t wpr = (chunks + (int64_t)kWave * nv - 1) / ((int64_t)kWave * nv);
-    if (wpr * kWave > max_block_for_nv(nv)) continue;
-    const int64_t slots = wpr * kWave * nv;
-    const int64_t waste = slots - chunks;
-    if (waste * 8 <= slots) {
-      best_nv = nv;
-      best_wpr = (int)wpr;
-      break;
-    }
-    if (best_waste < 0 || waste < best_waste) {
-      best_waste = waste;
-      best_nv = nv;
-      best_wpr = (int)wpr;
-    }
-  }
-  if (best_nv == 0) return p;
-  p.vec = true;
-  p.nv = best_nv;
-  p.tpr = best_wpr * kWave;
-  p.groups = p.tpr >= 256 ? 1 : 256 / p.tpr;
-  p.block = p.tpr * p.groups;
-  return p;
+RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned) {
+  return vg_plan::plan_rows(dim, elem_bytes, aligned, tuning().fwd_nv);
 }
 
-// Number of persistent row slots of the backward for a plan.
-int64_t bwd_slots(const RowPlan& p, int64_t rows, int cus) {
-  const int64_t wgs_needed = (rows + p.groups - 1) / p.groups;
-  const int waves_per_wg = p.block / kWave;
-  int64_t wg_per_cu = tuning().bwd_waves_per_cu / waves_per_wg;
-  if (wg_per_cu < 1) wg_per_cu = 1;
-  int64_t wgs = (int64_t)cus * wg_per_cu;
-  if (wgs > wgs_needed) wgs = wgs_needed;
-  if (wgs < 1) wgs = 1;
-  return wgs * p.groups;
+BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus) {
+  const Tuning& t = tuning();
+  return vg_plan::plan_bwd(rows, dim, elem_bytes, aligned, cus, t.bwd_nv, t.bwd_block,
+                           t.bwd_waves_per_cu);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -716,28 +767,29 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
 }
 
 template <int DT, int WDT, bool H>
-void launch_bwd_h(const BwdArgs& a, const RowPlan& p, int64_t slots, hipStream_t st) {
-  const dim3 grid((uint32_t)(slots / p.groups));
+void launch_bwd_h(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
+  const RowPlan& p = b.rp;
+  const dim3 grid((uint32_t)b.wgs);
   const dim3 block(p.block);
+  const size_t lds = b.lds_bytes;
   if (!p.vec) {
     hipLaunchKernelGGL((bwd_generic_kernel<DT, WDT, H>), grid, block, 0, st, a);
     return;
   }
   switch (p.nv) {
-    case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, H>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 2, H>), grid, block, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 3, H>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 4, H>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, H>), grid, block, lds, st, a); break;
+    case 2: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 2, H>), grid, block, lds, st, a); break;
+    case 3: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 3, H>), grid, block, lds, st, a); break;
+    default: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 4, H>), grid, block, lds, st, a); break;
   }
 }
 
 template <int DT, int WDT>
-void launch_bwd(const BwdArgs& a, bool saved_is_h, const RowPlan& p, int64_t slots,
-                hipStream_t st) {
+void launch_bwd(const BwdArgs& a, bool saved_is_h, const BwdPlan& b, hipStream_t st) {
   if (saved_is_h)
-    launch_bwd_h<DT, WDT, true>(a, p, slots, st);
+    launch_bwd_h<DT, WDT, true>(a, b, st);
   else
-    launch_bwd_h<DT, WDT, false>(a, p, slots, st);
+    launch_bwd_h<DT, WDT, false>(a, b, st);
 }
 
 // Supported (dtype, w_dtype) pairs: weight in the activation dtype, or fp32.
@@ -767,19 +819,8 @@ bool types_ok(int32_t dt, int32_t wdt) {
   } while (0)
 
 size_t workspace_bytes_for(int64_t rows, int64_t dim, int cus) {
-  if (rows <= 0 || dim <= 0 || cus <= 0) return 0;
-  // The plan depends on dtype and alignment, which the query does not know: return the
-  // largest need over every plan the backward can pick.
-  int64_t most = 0;
-  const int sizes[2] = {2, 4};
-  for (int si = 0; si < 2; ++si) {
-    for (int al = 0; al < 2; ++al) {
-      const RowPlan p = plan_rows(dim, sizes[si], al != 0, tuning().bwd_nv);
-      const int64_t s = bwd_slots(p, rows, cus);
-      if (s > most) most = s;
-    }
-  }
-  return (size_t)most * (size_t)dim * sizeof(float);
+  const Tuning& t = tuning();
+  return vg_plan::bwd_workspace_bytes(rows, dim, cus, t.bwd_nv, t.bwd_block, t.bwd_waves_per_cu);
 }
 
 }  // namespace
@@ -833,7 +874,10 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(const void* x, const void* re
   const bool aligned = aligned16(x) && aligned16(y) && ld_ok(ld_x, eb) && ld_ok(ld_y, eb) &&
                        (!residual || (aligned16(residual) && ld_ok(ld_res, eb))) &&
                        (!h || (aligned16(h) && ld_ok(ld_h, eb))) && (!weight || aligned16(weight));
-  const RowPlan p = plan_rows(dim, eb, aligned, tuning().fwd_nv);
+  const RowPlan p = plan_fwd(dim, eb, aligned);
+  if (!vg_plan::row_plan_valid(p, dim, eb))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: internal launch plan rejected (dim=%lld)",
+                (long long)dim);
 
   FwdArgs a;
   a.x = x;
@@ -903,14 +947,16 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
                        ld_ok(ld_g, eb) && ld_ok(ld_saved, eb) && ld_ok(ld_dx, eb) &&
                        (!dres || (aligned16(dres) && ld_ok(ld_dres, eb))) &&
                        (!weight || aligned16(weight));
-  const RowPlan p = plan_rows(dim, eb, aligned, tuning().bwd_nv);
-  const int64_t slots = bwd_slots(p, rows, cus);
-  if (slots / p.groups > INT32_MAX)
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: grid too large");
+  const BwdPlan plan = plan_bwd(rows, dim, eb, aligned, cus);
+  if (!vg_plan::row_plan_valid(plan.rp, dim, eb) || plan.wgs < 1 || plan.wgs > INT32_MAX ||
+      plan.lds_bytes > 64 * 1024)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: internal launch plan rejected (dim=%lld)",
+                (long long)dim);
+  const int64_t slots = plan.wgs * plan.rp.groups;  // row slots walking the rows
 
   float* partial = nullptr;
   if (dweight != nullptr) {
-    const size_t need = (size_t)slots * (size_t)dim * sizeof(float);
+    const size_t need = (size_t)plan.wgs * (size_t)dim * sizeof(float);
     if (workspace == nullptr || ws_bytes < need)
       return fail(VELOGRAD_ERR_WORKSPACE_TOO_SMALL,
                   "bwd: workspace of %zu bytes given, %zu needed", ws_bytes, need);
@@ -933,13 +979,13 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
   a.ld_dx = ld_dx;
   a.ld_dres = ld_dres;
   a.dim = (int32_t)dim;
-  a.tpr = p.tpr;
+  a.tpr = plan.rp.tpr;
   a.iters = (int32_t)((rows + slots - 1) / slots);
-  VG_DISPATCH_TYPES(dtype, w_dtype, (launch_bwd<kD, kW>(a, saved_is_h != 0, p, slots, st)));
+  VG_DISPATCH_TYPES(dtype, w_dtype, (launch_bwd<kD, kW>(a, saved_is_h != 0, plan, st)));
   int32_t rc = check_launch("velograd_rmsnorm_residual_bwd");
   if (rc != 0 || dweight == nullptr) return rc;
   hipLaunchKernelGGL(dweight_reduce_kernel, dim3((uint32_t)((dim + kWave - 1) / kWave)),
-                     dim3(kReduceBlock), 0, st, (const float*)partial, (int32_t)slots,
+                     dim3(kReduceBlock), 0, st, (const float*)partial, (int32_t)plan.wgs,
                      (int32_t)dim, dweight);
   return check_launch("velograd_rmsnorm_residual_bwd(dweight)");
 }
