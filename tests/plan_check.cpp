@@ -66,9 +66,11 @@ int main() {
     for (int aligned = 0; aligned < 2; ++aligned) {
       for (int64_t dim = 1; dim <= 70000; dim += (dim < 2048 ? 1 : 61)) {
         for (int prefer = -1; prefer <= kMaxNV + 1; ++prefer) {
-          const RowPlan p = plan_rows(dim, eb, aligned != 0, prefer);
-          check_row_plan(p, dim, eb, aligned != 0);
-          ++plans;
+          check_row_plan(plan_rows(dim, eb, aligned != 0, prefer, kFwdOrder), dim, eb,
+                         aligned != 0);
+          check_row_plan(plan_rows(dim, eb, aligned != 0, prefer, kBwdOrder), dim, eb,
+                         aligned != 0);
+          plans += 2;
         }
       }
     }

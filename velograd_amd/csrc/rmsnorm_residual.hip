@@ -637,17 +637,16 @@ __global__ __launch_bounds__(kReduceBlock) void dweight_reduce_kernel(const floa
   const int col = blockIdx.x * kWave + lane;
   float s = 0.0f;
   if (col < dim) {
+    // Batches of 16 loads in flight per lane (one HBM round trip for the usual 256 partial rows
+    // over 16 waves); the additions keep ascending p order.
+    constexpr int kBatch = 16;
     int p = wave;
-    // Four loads in flight per lane; the additions keep ascending p order.
-    for (; p + 3 * nw < nparts; p += 4 * nw) {
-      const float v0 = partial[(int64_t)p * dim + col];
-      const float v1 = partial[(int64_t)(p + nw) * dim + col];
-      const float v2 = partial[(int64_t)(p + 2 * nw) * dim + col];
-      const float v3 = partial[(int64_t)(p + 3 * nw) * dim + col];
-      s += v0;
-      s += v1;
-      s += v2;
-      s += v3;
+    for (; p + (kBatch - 1) * nw < nparts; p += kBatch * nw) {
+      float v[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) v[b] = partial[(int64_t)(p + b * nw) * dim + col];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) s += v[b];
     }
     for (; p < nparts; p += nw) s += partial[(int64_t)p * dim + col];
   }
@@ -725,7 +724,7 @@ const Tuning& tuning() {
 }
 
 RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned) {
-  return vg_plan::plan_rows(dim, elem_bytes, aligned, tuning().fwd_nv);
+  return vg_plan::plan_rows(dim, elem_bytes, aligned, tuning().fwd_nv, vg_plan::kFwdOrder);
 }
 
 BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus) {
