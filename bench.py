@@ -66,7 +66,8 @@ def parse_args(argv=None):
                    help="record per-kernel HIP events on every N-th timed step")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU-baseline budget; 0 skips it")
-    p.add_argument("--no-copy-ceiling", action="store_true")
+    p.add_argument("--no-copy-ceiling", action="store_true",
+                   help="skip the same-run stream-probe ceilings")
     return p.parse_args(argv)
 
 
@@ -139,6 +140,48 @@ def load_traffic(config: str):
         return None
     with open(path) as f:
         return json.load(f).get("fwd_traffic_bytes_per_launch")
+
+
+def stream_ceilings(sets, stream_bytes: int, stream) -> dict:
+    """Same-run practical ceiling: plain streaming kernels (velograd_amd/csrc/stream_probe.hip)
+    with the forward's (2 reads + 2 writes) and the backward's (2 reads + 1 write) byte pattern
+    over tensors of the workload's size, rotating over the same buffer sets (cold MALL)."""
+    import ctypes
+
+    import torch
+
+    from velograd_amd.build import PROBE_LIB_PATH
+
+    if not os.path.exists(PROBE_LIB_PATH):
+        return {}
+    lib = ctypes.CDLL(PROBE_LIB_PATH)
+    fn = lib.velograd_stream_probe
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p]
+    n16 = stream_bytes // 16
+    sp = stream.cuda_stream
+    out = {}
+    for name, pattern, nstreams, keys in (("copy", 0, 2, ("x", None, "y", None)),
+                                          ("fwd_pattern", 1, 4, ("x", "res", "y", "h")),
+                                          ("bwd_pattern", 2, 3, ("x", "res", "y", None))):
+        def run(i):
+            b = sets[i % len(sets)]
+            ptrs = [b[k].data_ptr() if k else None for k in keys]
+            rc = fn(pattern, ptrs[0], ptrs[1], ptrs[2], ptrs[3], n16, sp)
+            if rc != 0:
+                raise RuntimeError(f"stream probe {name} failed: {rc}")
+        for i in range(len(sets)):
+            run(i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        e0.record(stream)
+        for i in range(reps):
+            run(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        out[f"ceiling_{name}_gbs"] = round(nstreams * n16 * 16 / (us * 1e-6) / 1e9, 1)
+    return out
 
 
 def main(argv=None) -> int:
@@ -262,22 +305,15 @@ def main(argv=None) -> int:
     extra["pct_hbm_peak"] = round(100.0 * value / HBM_PEAK_GBS, 2)
 
     if not args.no_copy_ceiling:
-        src = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        srcs = [src, torch.empty_like(src)]
-        dsts = [dst, torch.empty_like(dst)]
-        for i in range(3):
-            dsts[i % 2].copy_(srcs[i % 2])
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 20
-        e0.record(stream)
-        for i in range(reps):
-            dsts[i % 2].copy_(srcs[i % 2])
-        e1.record(stream)
-        torch.cuda.synchronize()
-        copy_ms = e0.elapsed_time(e1) / reps
-        extra["copy_ceiling_gbs"] = round(2 * src.numel() / (copy_ms * 1e-3) / 1e9, 1)
-        del src, dst, srcs, dsts
+        ceil = stream_ceilings(sets, rows * d * s, stream)
+        extra.update(ceil)
+        if ceil:
+            # A step whose forward and backward each ran at their pattern's probe speed.
+            t_ideal = fb / (ceil["ceiling_fwd_pattern_gbs"] * 1e9)
+            if with_bwd:
+                t_ideal += bb / (ceil["ceiling_bwd_pattern_gbs"] * 1e9)
+            extra["ceiling_step_gbs"] = round((fb + bb) / t_ideal / 1e9, 1)
+            extra["frac_of_ceiling"] = round(value / extra["ceiling_step_gbs"], 4)
 
     cpu = None
     if args.cpu_seconds > 0:

@@ -15,9 +15,13 @@ import sys
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
 SRC = os.path.join(PKG_DIR, "csrc", "rmsnorm_residual.hip")
+PROBE_SRC = os.path.join(PKG_DIR, "csrc", "stream_probe.hip")
 INCLUDE_DIR = os.path.join(REPO_DIR, "include")
+CSRC_DIR = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libvelograd_kernels.so")
+# Bench-only helper (same-run HBM ceiling); not part of the kernels' C ABI.
+PROBE_LIB_PATH = os.path.join(LIB_DIR, "libvelograd_stream_probe.so")
 
 OFFLOAD_ARCH = "gfx950"
 
@@ -43,11 +47,9 @@ def find_hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP toolchain (ROCm) is required to build")
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compile the kernels for gfx950 and return the path of the shared library."""
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [find_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE_DIR, SRC, "-o", tmp]
+def _hipcc(src: str, out: str, verbose: bool) -> None:
+    tmp = out + ".tmp"
+    cmd = [find_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE_DIR, "-I", CSRC_DIR, src, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -55,7 +57,14 @@ def build_library(verbose: bool = False) -> str:
         raise RuntimeError(
             "hipcc failed (exit %d):\n%s\n%s" % (proc.returncode, proc.stdout, proc.stderr)
         )
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out)
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile the kernels (and the bench's stream probe) for gfx950; return the kernels' .so."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    _hipcc(SRC, LIB_PATH, verbose)
+    _hipcc(PROBE_SRC, PROBE_LIB_PATH, verbose)
     return LIB_PATH
 
 
