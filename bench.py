@@ -233,8 +233,8 @@ def main(argv=None) -> int:
     bwd_args = []
     if with_bwd:
         bwd_args = [(b["g"].data_ptr(), b["h"].data_ptr(), 1, b["w"].data_ptr(),
-                     b["inv"].data_ptr(), b["dx"].data_ptr(), None, b["dw"].data_ptr(),
-                     b["ws"].data_ptr(), ws_bytes, rows, d, d, d, d, d, code, code, sp)
+                     b["inv"].data_ptr(), None, b["dx"].data_ptr(), None, b["dw"].data_ptr(),
+                     b["ws"].data_ptr(), ws_bytes, rows, d, d, d, d, d, d, code, code, sp)
                     for b in sets]
 
     # every set gets a valid h / inv_rms before any backward reads it

@@ -76,21 +76,26 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(
  *                 is formed in fp32 in registers; same bytes moved).
  *   weight      : [dim] in `w_dtype`, or NULL (gw = grad_y; dweight is then not computed).
  *   inv_rms     : [rows] fp32, as written by the forward.
+ *   grad_h      : optional [rows, dim] in `dtype`: gradient that reaches h from its other
+ *                 consumer (in a pre-norm block, the next residual add, models/llama.py:48-56);
+ *                 when given, dx = backward + grad_h, added in fp32 before the one rounding.
+ *                 No counterpart in the reference's backward (fused.py:48-66), which stops at
+ *                 the norm.  dx may be grad_h itself (accumulate in place, same row stride).
  *   dx          : [rows, dim] in `dtype` (required).  Since h = x + residual, it is also the
  *                 gradient of residual.
  *   dres        : optional [rows, dim] second copy of dx for callers that need two buffers.
  *   dweight     : [dim] fp32, or NULL.  Reduced in two deterministic stages through `workspace`.
  *   workspace   : device scratch of at least
  *                 velograd_rmsnorm_residual_bwd_workspace_bytes(rows, dim, device) bytes,
- *                 256-byte aligned; may be NULL when dweight is NULL.
+ *                 16-byte aligned; may be NULL when dweight is NULL.
  */
 VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
     const void* grad_y, const void* saved, int32_t saved_is_h,
-    const void* weight, const float* inv_rms,
+    const void* weight, const float* inv_rms, const void* grad_h,
     void* dx, void* dres, float* dweight,
     void* workspace, size_t ws_bytes,
     int64_t rows, int64_t dim,
-    int64_t ld_g, int64_t ld_saved, int64_t ld_dx, int64_t ld_dres,
+    int64_t ld_g, int64_t ld_saved, int64_t ld_grad_h, int64_t ld_dx, int64_t ld_dres,
     int32_t dtype, int32_t w_dtype, void* hip_stream);
 
 /*

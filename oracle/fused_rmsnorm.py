@@ -67,6 +67,19 @@ def backward_from_h(grad_out: np.ndarray, h: np.ndarray, weight: Optional[np.nda
     return fused_rmsnorm_residual_backward(grad_out, h * inv_rms, weight, inv_rms)
 
 
+def backward_with_residual_grad(grad_out: np.ndarray, normed_input: np.ndarray,
+                                weight: Optional[np.ndarray], inv_rms: np.ndarray,
+                                grad_h: np.ndarray) -> Tuple[np.ndarray, Optional[np.ndarray]]:
+    """fused.py:48-66 plus the gradient that reaches h from its other consumer.
+
+    In a pre-norm block h = x + residual feeds both the norm and the next residual add
+    (python/velograd/models/llama.py:48-56), so dL/dh = (norm backward, fused.py:60) + grad_h,
+    added once in the working precision.  dweight is unchanged.
+    """
+    grad_x, grad_weight = fused_rmsnorm_residual_backward(grad_out, normed_input, weight, inv_rms)
+    return grad_x + grad_h, grad_weight
+
+
 def fused_rmsnorm_residual(x, residual=None, weight=None, eps: float = 1e-6) -> np.ndarray:
     """kernels/__init__.py:19-32 for array-like inputs: cast to float32, return only y."""
     x_arr = np.asarray(x, dtype=np.float32)                                     # :21

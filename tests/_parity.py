@@ -10,6 +10,7 @@ Tolerances (the north star's gates, written out):
     first term bounds the subtraction, the second bounds the error of the row mean m, whose
     terms cancel (so no order of summation makes |m| itself the scale).
   * dx in fp32: |a - b| <= 1e-5 * S.
+  * with a residual-stream gradient grad_h added to dx, S also includes |grad_h|.
   * dweight (fp32): |a - b| <= 1e-3 * max(|b|, rms(b)) elementwise.
 """
 
@@ -75,8 +76,9 @@ def assert_dx_fp32(got: torch.Tensor, ref32: np.ndarray, gw, xhat, r, what: str 
 
 
 def dx_check(got: torch.Tensor, ref32: np.ndarray, gw: np.ndarray, xhat: np.ndarray,
-             r: np.ndarray, what: str = "dx") -> int:
-    """1-ulp test with the operand-scaled fp32 floor; returns how many needed the floor."""
+             r: np.ndarray, what: str = "dx", grad_h=None) -> int:
+    """1-ulp test with the operand-scaled fp32 floor; returns how many needed the floor.
+    With a residual-stream gradient added to dx, |grad_h| joins the operand scale."""
     got_c = got.detach().cpu()
     ref = round_like(ref32, got_c.dtype).reshape(got_c.shape)
     d = ulp_distance(got_c, ref).numpy()
@@ -85,7 +87,10 @@ def dx_check(got: torch.Tensor, ref32: np.ndarray, gw: np.ndarray, xhat: np.ndar
     if n_floor:
         g = got_c.float().numpy().reshape(ref32.shape).astype(np.float64)
         diff = np.abs(g - ref32.astype(np.float64))
-        floor = DX_FLOOR * dx_scale(gw, xhat, r)
+        scale = dx_scale(gw, xhat, r)
+        if grad_h is not None:
+            scale = scale + np.abs(np.asarray(grad_h, np.float64))
+        floor = DX_FLOOR * scale
         # Rounding the fp32 value to the output dtype adds up to half an ulp of it.
         half_ulp = np.abs(ref.float().numpy().reshape(ref32.shape)) * 2.0 ** -8
         ok = diff <= floor + half_ulp

@@ -56,9 +56,9 @@ def _fwd(lib, **kw):
 
 
 def _bwd(lib, **kw):
-    args = dict(g=16, saved=48, saved_is_h=0, weight=None, inv_rms=80, dx=32, dres=None,
-                dweight=None, ws=None, ws_bytes=0, rows=4, dim=64, ld_g=64, ld_s=64, ld_dx=64,
-                ld_dres=64, dtype=2, w_dtype=2, stream=None)
+    args = dict(g=16, saved=48, saved_is_h=0, weight=None, inv_rms=80, grad_h=None, dx=32,
+                dres=None, dweight=None, ws=None, ws_bytes=0, rows=4, dim=64, ld_g=64, ld_s=64,
+                ld_gh=64, ld_dx=64, ld_dres=64, dtype=2, w_dtype=2, stream=None)
     args.update(kw)
     return lib.velograd_rmsnorm_residual_bwd(*args.values())
 
@@ -95,6 +95,9 @@ def test_fwd_zero_rows_is_a_no_op(lib):
     (dict(ld_dx=1), _lib.ERR_INVALID_ARGUMENT, "row strides"),
     (dict(dx=16), _lib.ERR_INVALID_ARGUMENT, "alias"),
     (dict(dres=48), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(grad_h=96, dres=96), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(grad_h=96, ld_gh=8), _lib.ERR_INVALID_ARGUMENT, "row strides"),
+    (dict(grad_h=32, ld_gh=128), _lib.ERR_INVALID_ARGUMENT, "same row stride"),
 ])
 def test_bwd_argument_errors(lib, kw, code, msg):
     assert _bwd(lib, **kw) == code

@@ -358,8 +358,8 @@ def test_workspace_too_small_is_rejected():
     small = 512 * 4 - 16
     ws = torch.empty(small, dtype=torch.uint8, device="cuda")
     rc = lib.velograd_rmsnorm_residual_bwd(
-        g.data_ptr(), g.data_ptr(), 1, w.data_ptr(), inv.data_ptr(), dx.data_ptr(), None,
-        dw.data_ptr(), ws.data_ptr(), small, 64, 512, 512, 512, 512, 512,
+        g.data_ptr(), g.data_ptr(), 1, w.data_ptr(), inv.data_ptr(), None, dx.data_ptr(), None,
+        dw.data_ptr(), ws.data_ptr(), small, 64, 512, 512, 512, 512, 512, 512,
         _lib.DTYPE_F32, _lib.DTYPE_F32, torch.cuda.current_stream().cuda_stream)
     assert rc == _lib.ERR_WORKSPACE_TOO_SMALL
     assert "needed" in _lib.last_error()
@@ -373,3 +373,55 @@ def test_dtype_mismatch_raises():
         vk.fused_rmsnorm_residual_forward(x, x.float())
     with pytest.raises(TypeError):
         vk.fused_rmsnorm_residual_forward(x.double())
+
+
+# ---------------------------------------------------------------------------------------------
+# Residual-stream gradient (grad_h) fused into the backward.
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,rows,d", [(torch.bfloat16, 16384, 4096),
+                                          (torch.bfloat16, 300, 4104),
+                                          (torch.float16, 64, 768),
+                                          (torch.float32, 37, 13)])
+def test_backward_with_residual_stream_gradient(dtype, rows, d):
+    _say(f"grad_h {dtype} {rows}x{d}")
+    rng = np.random.default_rng(rows + d)
+    h = P.to_device(P.gaussian(rng, (rows, d)), dtype)
+    g = P.to_device(P.gaussian(rng, (rows, d)), dtype)
+    gh = P.to_device(P.gaussian(rng, (rows, d)), dtype)
+    w = P.to_device(P.weight_vec(rng, d), dtype)
+    _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
+    dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=gh)
+    g32, h32, w32, r32, gh32 = (P.upcast(t) for t in (g, h, w, inv, gh))
+    xhat = h32 * r32
+    rdx, rdw = ora.backward_with_residual_grad(g32, xhat, w32, r32, gh32)
+    if dtype == torch.float32:
+        scale = P.dx_scale(g32 * w32, xhat, r32) + np.abs(gh32)
+        assert np.max(np.abs(P.upcast(dx) - rdx) / scale) <= P.FP32_REL_TOL
+    else:
+        P.dx_check(dx, rdx, g32 * w32, xhat, r32, "dx+grad_h", grad_h=gh32)
+    P.assert_dweight(P.upcast(dw), rdw)
+    # the same dweight as without grad_h, bit for bit
+    _, dw0 = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True)
+    assert torch.equal(dw, dw0)
+
+
+def test_residual_stream_gradient_accumulates_in_place():
+    """dx may be grad_h itself: the C ABI reads each element before writing it."""
+    from velograd_amd import _lib
+    lib = _lib.load()
+    rows, d = 1024, 4096
+    rng = np.random.default_rng(3)
+    h = P.to_device(P.gaussian(rng, (rows, d)), torch.bfloat16)
+    g = P.to_device(P.gaussian(rng, (rows, d)), torch.bfloat16)
+    gh = P.to_device(P.gaussian(rng, (rows, d)), torch.bfloat16)
+    w = P.to_device(P.weight_vec(rng, d), torch.bfloat16)
+    _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
+    ref, _ = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=gh)
+    acc = gh.clone()
+    inv1 = inv.reshape(rows).contiguous()
+    rc = lib.velograd_rmsnorm_residual_bwd(
+        g.data_ptr(), h.data_ptr(), 1, w.data_ptr(), inv1.data_ptr(), acc.data_ptr(),
+        acc.data_ptr(), None, None, None, 0, rows, d, d, d, d, d, d,
+        _lib.DTYPE_BF16, _lib.DTYPE_BF16, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "bwd in place")
+    assert torch.equal(acc, ref)

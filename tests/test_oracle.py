@@ -140,6 +140,29 @@ def test_backward_matches_torch_autograd():
     assert np.max(np.abs(dw - tw.grad.numpy())) < 1e-12
 
 
+def test_residual_stream_gradient_matches_torch_autograd():
+    """L = sum(g*y) + sum(gh*h) with h = x + res: dL/dx = dL/dres = norm backward + gh."""
+    rng = np.random.default_rng(4)
+    x, res, g, gh = (rng.standard_normal((4, 80)) for _ in range(4))
+    w = 1 + 0.1 * rng.standard_normal(80)
+    eps = 1e-5
+    tx = torch.tensor(x, requires_grad=True)
+    tr = torch.tensor(res, requires_grad=True)
+    tw = torch.tensor(w, requires_grad=True)
+    th = tx + tr
+    y = torch.nn.functional.rms_norm(th, (80,), tw, eps)
+    ((y * torch.from_numpy(g)).sum() + (th * torch.from_numpy(gh)).sum()).backward()
+    _, h, inv = ora.fused_rmsnorm_residual_forward(x, res, w, eps)
+    dx, dw = ora.backward_with_residual_grad(g, h * inv, w, inv, gh)
+    assert np.max(np.abs(dx - tx.grad.numpy())) < 1e-12
+    assert np.max(np.abs(dx - tr.grad.numpy())) < 1e-12
+    assert np.max(np.abs(dw - tw.grad.numpy())) < 1e-12
+    # zero residual-stream gradient is the plain backward, bit for bit
+    z = ora.backward_with_residual_grad(g, h * inv, w, inv, np.zeros_like(gh))
+    p = ora.fused_rmsnorm_residual_backward(g, h * inv, w, inv)
+    assert np.array_equal(z[0], p[0]) and np.array_equal(z[1], p[1])
+
+
 def test_backward_from_h_equals_xhat_form():
     rng = np.random.default_rng(2)
     h = rng.standard_normal((3, 40)).astype(np.float32)

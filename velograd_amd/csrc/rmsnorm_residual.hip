@@ -280,11 +280,12 @@ struct BwdArgs {
   const void* saved;
   const void* w;
   const float* inv_rms;
+  const void* gh;  // residual-stream gradient added to dx, or null
   void* dx;
   void* dres;
   float* partial;  // [slots, dim] fp32 or null
   int64_t rows;
-  int64_t ld_g, ld_s, ld_dx, ld_dres;
+  int64_t ld_g, ld_s, ld_gh, ld_dx, ld_dres;
   int32_t dim;
   int32_t tpr;
   int32_t iters;  // rows visited per slot = ceil(rows / slots)
@@ -415,11 +416,19 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
 
 // ------------------------------------------------------------------------------------------
 // Backward, register-resident row, persistent row slots.
+// FLAGS: kSavedIsH (the saved tensor is h, xhat = h * inv_rms is formed in registers),
+//        kGradH (a residual-stream gradient grad_h is added to dx in the same pass).
 // ------------------------------------------------------------------------------------------
-template <int DT, int WDT, int NV, bool SAVED_IS_H>
+constexpr int kSavedIsH = 1;
+constexpr int kGradH = 2;
+
+template <int DT, int WDT, int NV, int FLAGS>
 __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const BwdArgs a) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
+  constexpr bool SAVED_IS_H = (FLAGS & kSavedIsH) != 0;
+  constexpr bool HAS_GH = (FLAGS & kGradH) != 0;
+  constexpr int NH = HAS_GH ? NV : 1;  // grad_h chunks (a dummy slot when absent)
   __shared__ float red[2][kMaxWavesPerRow];
 
   const int tpr = a.tpr;
@@ -444,8 +453,8 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
     for (int i = 0; i < V; ++i) acc[k][i] = 0.0f;
   }
 
-  // Loads of one row into (gv, sv, rr); zeros outside the tensor.
-  auto load_row = [&](int64_t row, u32x4* gv, u32x4* sv, float& rr) {
+  // Loads of one row into (gv, sv, hv, rr); zeros outside the tensor.
+  auto load_row = [&](int64_t row, u32x4* gv, u32x4* sv, u32x4* hv, float& rr) {
     const bool ok = row < a.rows;
     rr = ok ? a.inv_rms[row] : 0.0f;
 #pragma unroll
@@ -453,9 +462,11 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
       const int c = lt + k * tpr;
       gv[k] = u32x4{0u, 0u, 0u, 0u};
       sv[k] = u32x4{0u, 0u, 0u, 0u};
+      if constexpr (HAS_GH) hv[k] = u32x4{0u, 0u, 0u, 0u};
       if (ok && c < nchunk) {
         gv[k] = load16_stream<DT>(a.g, row * a.ld_g + (int64_t)c * V);
         sv[k] = load16_stream<DT>(a.saved, row * a.ld_s + (int64_t)c * V);
+        if constexpr (HAS_GH) hv[k] = load16_stream<DT>(a.gh, row * a.ld_gh + (int64_t)c * V);
       }
     }
   };
@@ -472,22 +483,23 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
   };
 
   int64_t row = slot;
-  u32x4 gv[NV], sv[NV];
+  u32x4 gv[NV], sv[NV], hv[NH];
   float rr;
-  load_row(row, gv, sv, rr);
+  load_row(row, gv, sv, hv, rr);
 
   for (int it = 0; it < a.iters; ++it) {
     const bool ok = row < a.rows;
     const int64_t nrow = row + nslots;
-    u32x4 gn[NV], sn[NV];
+    u32x4 gn[NV], sn[NV], hn[NH];
     float rn = 0.0f;
     if (it + 1 < a.iters) {
-      load_row(nrow, gn, sn, rn);
+      load_row(nrow, gn, sn, hn, rn);
     } else {
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         gn[k] = u32x4{0u, 0u, 0u, 0u};
         sn[k] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (HAS_GH) hn[k] = u32x4{0u, 0u, 0u, 0u};
       }
     }
 
@@ -522,6 +534,12 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
           const float gw = gf[i] * wf[i];
           d[i] = rr * (gw - xh[i] * m);
         }
+        if constexpr (HAS_GH) {
+          float ghf[V];
+          C::unpack(hv[k], ghf);
+#pragma unroll
+          for (int i = 0; i < V; ++i) d[i] = d[i] + ghf[i];
+        }
         const u32x4 pv = C::pack(d);
         store16_stream<DT>(a.dx, row * a.ld_dx + (int64_t)c * V, pv);
         if (has_dres) store16_stream<DT>(a.dres, row * a.ld_dres + (int64_t)c * V, pv);
@@ -535,6 +553,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
     for (int k = 0; k < NV; ++k) {
       gv[k] = gn[k];
       sv[k] = sn[k];
+      if constexpr (HAS_GH) hv[k] = hn[k];
     }
     rr = rn;
   }
@@ -579,10 +598,12 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
 // Backward, any dim / alignment: one row slot per workgroup, two passes per row; the slot's
 // dweight partial row is accumulated in place (each column owned by one thread).
 // ------------------------------------------------------------------------------------------
-template <int DT, int WDT, bool SAVED_IS_H>
+template <int DT, int WDT, int FLAGS>
 __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArgs a) {
   using C = Codec<DT>;
   using CW = Codec<WDT>;
+  constexpr bool SAVED_IS_H = (FLAGS & kSavedIsH) != 0;
+  constexpr bool HAS_GH = (FLAGS & kGradH) != 0;
   __shared__ float red[2][kGenericBlock / kWave];
   const int64_t slot = blockIdx.x;
   const int64_t nslots = gridDim.x;
@@ -609,7 +630,8 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
       float xh = C::load1(a.saved, row * a.ld_s + j);
       if constexpr (SAVED_IS_H) xh = xh * rr;
       const float gw = has_w ? gf * CW::load1(a.w, j) : gf;
-      const float d = rr * (gw - xh * m);
+      float d = rr * (gw - xh * m);
+      if constexpr (HAS_GH) d = d + C::load1(a.gh, row * a.ld_gh + j);
       C::store1(a.dx, row * a.ld_dx + j, d);
       if (has_dres) C::store1(a.dres, row * a.ld_dres + j, d);
       if (prow != nullptr) {
@@ -765,30 +787,33 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
   }
 }
 
-template <int DT, int WDT, bool H>
-void launch_bwd_h(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
+template <int DT, int WDT, int F>
+void launch_bwd_flags(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
   const RowPlan& p = b.rp;
   const dim3 grid((uint32_t)b.wgs);
   const dim3 block(p.block);
   const size_t lds = b.lds_bytes;
   if (!p.vec) {
-    hipLaunchKernelGGL((bwd_generic_kernel<DT, WDT, H>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((bwd_generic_kernel<DT, WDT, F>), grid, block, 0, st, a);
     return;
   }
   switch (p.nv) {
-    case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, H>), grid, block, lds, st, a); break;
-    case 2: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 2, H>), grid, block, lds, st, a); break;
-    case 3: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 3, H>), grid, block, lds, st, a); break;
-    default: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 4, H>), grid, block, lds, st, a); break;
+    case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, F>), grid, block, lds, st, a); break;
+    case 2: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 2, F>), grid, block, lds, st, a); break;
+    case 3: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 3, F>), grid, block, lds, st, a); break;
+    default: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 4, F>), grid, block, lds, st, a); break;
   }
 }
 
 template <int DT, int WDT>
 void launch_bwd(const BwdArgs& a, bool saved_is_h, const BwdPlan& b, hipStream_t st) {
-  if (saved_is_h)
-    launch_bwd_h<DT, WDT, true>(a, b, st);
-  else
-    launch_bwd_h<DT, WDT, false>(a, b, st);
+  const int flags = (saved_is_h ? kSavedIsH : 0) | (a.gh != nullptr ? kGradH : 0);
+  switch (flags) {
+    case 0: launch_bwd_flags<DT, WDT, 0>(a, b, st); break;
+    case kSavedIsH: launch_bwd_flags<DT, WDT, kSavedIsH>(a, b, st); break;
+    case kGradH: launch_bwd_flags<DT, WDT, kGradH>(a, b, st); break;
+    default: launch_bwd_flags<DT, WDT, kSavedIsH | kGradH>(a, b, st); break;
+  }
 }
 
 // Supported (dtype, w_dtype) pairs: weight in the activation dtype, or fp32.
@@ -900,9 +925,10 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(const void* x, const void* re
 
 VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
     const void* grad_y, const void* saved, int32_t saved_is_h, const void* weight,
-    const float* inv_rms, void* dx, void* dres, float* dweight, void* workspace,
-    size_t ws_bytes, int64_t rows, int64_t dim, int64_t ld_g, int64_t ld_saved, int64_t ld_dx,
-    int64_t ld_dres, int32_t dtype, int32_t w_dtype, void* hip_stream) {
+    const float* inv_rms, const void* grad_h, void* dx, void* dres, float* dweight,
+    void* workspace, size_t ws_bytes, int64_t rows, int64_t dim, int64_t ld_g, int64_t ld_saved,
+    int64_t ld_grad_h, int64_t ld_dx, int64_t ld_dres, int32_t dtype, int32_t w_dtype,
+    void* hip_stream) {
   if (!types_ok(dtype, w_dtype))
     return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
                 "bwd: unsupported dtype/w_dtype pair (%d, %d): weight must be the activation "
@@ -927,13 +953,21 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
   if (grad_y == nullptr || saved == nullptr || inv_rms == nullptr || dx == nullptr)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
                 "bwd: grad_y, saved, inv_rms and dx must not be NULL");
-  if (ld_g < dim || ld_saved < dim || ld_dx < dim || (dres && ld_dres < dim))
+  if (ld_g < dim || ld_saved < dim || ld_dx < dim || (dres && ld_dres < dim) ||
+      (grad_h && ld_grad_h < dim))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
-                "bwd: row strides must be >= dim (ld_g=%lld ld_saved=%lld ld_dx=%lld "
-                "ld_dres=%lld)",
-                (long long)ld_g, (long long)ld_saved, (long long)ld_dx, (long long)ld_dres);
-  if (dx == grad_y || dx == saved || dx == dres || (dres && (dres == grad_y || dres == saved)))
+                "bwd: row strides must be >= dim (ld_g=%lld ld_saved=%lld ld_grad_h=%lld "
+                "ld_dx=%lld ld_dres=%lld)",
+                (long long)ld_g, (long long)ld_saved, (long long)ld_grad_h, (long long)ld_dx,
+                (long long)ld_dres);
+  // dx may be grad_h itself (accumulating in place: each element is read before it is written
+  // by the same thread); no other output may alias an input.
+  if (dx == grad_y || dx == saved || dx == dres ||
+      (dres && (dres == grad_y || dres == saved || dres == grad_h)))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: outputs must not alias inputs");
+  if (grad_h == dx && ld_grad_h != ld_dx)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "bwd: dx may alias grad_h only with the same row stride");
 
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess)
@@ -945,6 +979,7 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
   const bool aligned = aligned16(grad_y) && aligned16(saved) && aligned16(dx) &&
                        ld_ok(ld_g, eb) && ld_ok(ld_saved, eb) && ld_ok(ld_dx, eb) &&
                        (!dres || (aligned16(dres) && ld_ok(ld_dres, eb))) &&
+                       (!grad_h || (aligned16(grad_h) && ld_ok(ld_grad_h, eb))) &&
                        (!weight || aligned16(weight));
   const BwdPlan plan = plan_bwd(rows, dim, eb, aligned, cus);
   if (!vg_plan::row_plan_valid(plan.rp, dim, eb) || plan.wgs < 1 || plan.wgs > INT32_MAX ||
@@ -969,11 +1004,13 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
   a.saved = saved;
   a.w = weight;
   a.inv_rms = inv_rms;
+  a.gh = grad_h;
   a.dx = dx;
   a.dres = dres;
   a.partial = partial;
   a.rows = rows;
   a.ld_g = ld_g;
+  a.ld_gh = ld_grad_h;
   a.ld_s = ld_saved;
   a.ld_dx = ld_dx;
   a.ld_dres = ld_dres;

@@ -26,8 +26,9 @@ returns `grad_weight=None` (fused.py:44-45, 62-65); NaN and Inf propagate (no cl
 `grad_x` is also the gradient of `residual`.
 
 Additions (keyword-only, off by default): `saved_is_h=True` lets the backward take h instead of
-xhat (xhat is then formed in registers; same bytes moved), and `dresidual_out=` receives a
-second copy of grad_x in a caller-owned buffer.
+xhat (xhat is then formed in registers; same bytes moved), `dresidual_out=` receives a second
+copy of grad_x in a caller-owned buffer, and `grad_h=` adds the residual-stream gradient (the
+gradient reaching h from the next residual add) to grad_x in the same pass.
 """
 
 from __future__ import annotations
@@ -175,7 +176,8 @@ def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
 
 def _backward_device(grad_out: torch.Tensor, saved: torch.Tensor,
                      weight: Optional[torch.Tensor], inv_rms: torch.Tensor,
-                     saved_is_h: bool, dresidual_out: Optional[torch.Tensor]):
+                     saved_is_h: bool, dresidual_out: Optional[torch.Tensor],
+                     grad_h: Optional[torch.Tensor] = None):
     lib = _lib.load()
     device = grad_out.device
     code = _dtype_code(grad_out, "grad_out")
@@ -202,6 +204,13 @@ def _backward_device(grad_out: torch.Tensor, saved: torch.Tensor,
     if r.dtype != torch.float32:
         r = r.to(torch.float32)
     r = r.contiguous()
+    gh2 = None
+    if grad_h is not None:
+        if (not isinstance(grad_h, torch.Tensor) or grad_h.device != device
+                or grad_h.dtype != grad_out.dtype or grad_h.shape != shape):
+            raise ValueError("grad_h must be a tensor shaped and typed like grad_out on the same "
+                             "device")
+        gh2 = _rows_view(grad_h, "grad_h") if d > 0 else None
 
     dx = torch.empty(shape, dtype=grad_out.dtype, device=device)
     dres2 = None
@@ -229,11 +238,11 @@ def _backward_device(grad_out: torch.Tensor, saved: torch.Tensor,
     with torch.cuda.device(device):
         rc = lib.velograd_rmsnorm_residual_bwd(
             g2.data_ptr(), s2.data_ptr(), 1 if saved_is_h else 0,
-            _ptr(w), r.data_ptr(),
+            _ptr(w), r.data_ptr(), _ptr(gh2),
             dx2.data_ptr(), _ptr(dres2), _ptr(dweight),
             _ptr(ws), ws_bytes,
             rows, d,
-            _ld(g2), _ld(s2), d, d,
+            _ld(g2), _ld(s2), _ld(gh2) if gh2 is not None else d, d, d,
             code, wcode, _stream(device))
     _lib.check(rc, "velograd_rmsnorm_residual_bwd")
     return dx, dweight
@@ -279,15 +288,17 @@ def fused_rmsnorm_residual_forward(x: Any, residual: Optional[Any] = None,
 
 def fused_rmsnorm_residual_backward(grad_out: Any, normed_input: Any, weight: Optional[Any],
                                     inv_rms: Any, *, saved_is_h: bool = False,
-                                    dresidual_out: Optional[torch.Tensor] = None):
+                                    dresidual_out: Optional[torch.Tensor] = None,
+                                    grad_h: Optional[Any] = None):
     """Analytic backward of the forward; returns (grad_x, grad_weight) like fused.py:48-66.
 
     `normed_input` is xhat = h * inv_rms (or h itself with saved_is_h=True); grad_weight is None
-    when weight is None.
+    when weight is None.  `grad_h`, the gradient reaching h from its other consumer (the next
+    residual add of a pre-norm block), is added to grad_x in the same pass.
     """
     if _is_device_tensor(grad_out):
         return _backward_device(grad_out, normed_input, weight, inv_rms, saved_is_h,
-                                dresidual_out)
+                                dresidual_out, grad_h)
     if dresidual_out is not None:
         raise ValueError("dresidual_out is only supported for device tensors")
     device = _require_gpu()
@@ -295,7 +306,8 @@ def fused_rmsnorm_residual_backward(grad_out: Any, normed_input: Any, weight: Op
     sd = _host_to_device_f32(normed_input, device)
     wd = _host_to_device_f32(weight, device) if weight is not None else None
     rd = _host_to_device_f32(inv_rms, device)
-    dx, dw = _backward_device(gd, sd, wd, rd, saved_is_h, None)
+    ghd = _host_to_device_f32(grad_h, device) if grad_h is not None else None
+    dx, dw = _backward_device(gd, sd, wd, rd, saved_is_h, None, ghd)
     return _to_host(dx), _to_host(dw)
 
 

@@ -1,0 +1,100 @@
+"""Autograd and module wrappers that put the fused kernels on a model's training path.
+
+The reference's models call a pure-Python `nn.RMSNorm` (python/velograd/nn.py:328-389, used by
+models/llama.py:44-56) followed by a separate residual add, and its fused kernel wrapper has no
+gradient function (python/velograd/kernels/__init__.py:30-31).  Here:
+
+* `FusedRMSNormResidualFunction` — forward `(y, h) = fused(x, residual, weight, eps)` saving
+  `(h, inv_rms)`; backward runs the fused backward once, adding the gradient that reaches `h`
+  from its other consumer (the next residual add) in the same pass, and returns
+  dx = dresidual and dweight.
+* `RMSNorm(dim, eps=1e-6)` — the reference module's constructor and call
+  (`nn.py:330-337`): y = x * inv_rms * weight with weight initialised to ones.  The reference
+  also floors mean(x^2) at 1e-12 before adding eps (`nn.py:349`); with the default eps that
+  changes inv_rms by at most 5e-7 relative, and only for rows whose mean square is below 1e-12.
+* `FusedAddRMSNorm(dim, eps=1e-6)` — `(y, h) = module(x, residual)` for pre-norm blocks.
+
+All computation runs in the HIP kernels; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import kernels as _k
+
+__all__ = ["FusedRMSNormResidualFunction", "fused_add_rmsnorm", "RMSNorm", "FusedAddRMSNorm"]
+
+
+class FusedRMSNormResidualFunction(torch.autograd.Function):
+    """(y, h) = fused RMSNorm + residual; differentiable in x, residual and weight."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, residual: Optional[torch.Tensor],
+                weight: Optional[torch.Tensor], eps: float):
+        y, h, inv_rms = _k.fused_rmsnorm_residual_forward(x, residual, weight, eps)
+        if residual is None:
+            h = x.view_as(x)  # a distinct output object that aliases x (fused.py:39)
+        ctx.save_for_backward(h, weight, inv_rms)
+        ctx.has_residual = residual is not None
+        return y, h
+
+    @staticmethod
+    def backward(ctx, grad_y: Optional[torch.Tensor], grad_h: Optional[torch.Tensor]):
+        h, weight, inv_rms = ctx.saved_tensors
+        if grad_y is None:
+            grad_y = torch.zeros_like(h)
+        if grad_h is not None and grad_h.dtype != h.dtype:
+            grad_h = grad_h.to(h.dtype)
+        dx, dweight = _k.fused_rmsnorm_residual_backward(
+            grad_y.contiguous(), h, weight, inv_rms, saved_is_h=True,
+            grad_h=None if grad_h is None else grad_h.contiguous())
+        need_x, need_res, need_w, _ = ctx.needs_input_grad
+        if dweight is not None and weight is not None and dweight.dtype != weight.dtype:
+            dweight = dweight.to(weight.dtype)
+        return (dx if need_x else None,
+                dx if (need_res and ctx.has_residual) else None,
+                dweight.view_as(weight) if (need_w and dweight is not None) else None,
+                None)
+
+
+def fused_add_rmsnorm(x: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                      weight: Optional[torch.Tensor] = None,
+                      eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Differentiable `(y, h)`: h = x + residual, y = RMSNorm(h) * weight."""
+    return FusedRMSNormResidualFunction.apply(x, residual, weight, eps)
+
+
+class RMSNorm(torch.nn.Module):
+    """Drop-in for the reference's `velograd.nn.RMSNorm(dim, eps=1e-6)` (nn.py:328-389)."""
+
+    def __init__(self, dim: int, eps: float = 1e-6, device=None, dtype=None):
+        super().__init__()
+        self.dim = dim
+        self.eps = eps
+        self.weight = torch.nn.Parameter(torch.ones(dim, device=device, dtype=dtype))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return fused_add_rmsnorm(x, None, self.weight, self.eps)[0]
+
+    def extra_repr(self) -> str:
+        return f"{self.dim}, eps={self.eps}"
+
+
+class FusedAddRMSNorm(torch.nn.Module):
+    """Pre-norm block helper: `(y, h) = module(x, residual)` with h = x + residual."""
+
+    def __init__(self, dim: int, eps: float = 1e-6, device=None, dtype=None):
+        super().__init__()
+        self.dim = dim
+        self.eps = eps
+        self.weight = torch.nn.Parameter(torch.ones(dim, device=device, dtype=dtype))
+
+    def forward(self, x: torch.Tensor,
+                residual: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+        return fused_add_rmsnorm(x, residual, self.weight, self.eps)
+
+    def extra_repr(self) -> str:
+        return f"{self.dim}, eps={self.eps}"
