@@ -130,8 +130,50 @@ def bwd_workspace_bytes(rows: int, dim: int, device: Optional[torch.device] = No
 # ---------------------------------------------------------------------------------------------
 # Device paths
 # ---------------------------------------------------------------------------------------------
+def _forward_fast(x: torch.Tensor, residual: Optional[torch.Tensor],
+                  weight: Optional[torch.Tensor], eps: float):
+    """The common case without views or copies, for launch-latency-bound (decode) calls:
+    contiguous tensors of one dtype on the current device, weight [D] in that dtype or fp32.
+    Returns None when the call does not qualify (the general path then handles it)."""
+    code = _lib.TORCH_DTYPE_CODES.get(x.dtype)
+    if code is None or x.dim() == 0 or not x.is_contiguous():
+        return None
+    d = x.shape[-1]
+    rows = x.numel() // d if d > 0 else 0
+    if rows == 0:
+        return None
+    dev = x.device
+    if dev.index != torch.cuda.current_device():
+        return None
+    if residual is not None and not (
+            isinstance(residual, torch.Tensor) and residual.dtype == x.dtype
+            and residual.shape == x.shape and residual.is_contiguous() and residual.device == dev):
+        return None
+    wcode = code
+    if weight is not None:
+        if not (isinstance(weight, torch.Tensor) and weight.dim() == 1 and weight.shape[0] == d
+                and weight.is_contiguous() and weight.device == dev):
+            return None
+        wcode = _lib.TORCH_DTYPE_CODES.get(weight.dtype)
+        if wcode != code and wcode != _lib.DTYPE_F32:
+            return None
+    y = torch.empty_like(x)
+    h = torch.empty_like(x) if residual is not None else x
+    inv_rms = torch.empty(x.shape[:-1] + (1,), dtype=torch.float32, device=dev)
+    rc = _lib.load().velograd_rmsnorm_residual_fwd(
+        x.data_ptr(), None if residual is None else residual.data_ptr(),
+        None if weight is None else weight.data_ptr(),
+        y.data_ptr(), None if residual is None else h.data_ptr(), inv_rms.data_ptr(),
+        rows, d, d, d, d, d, code, wcode, float(eps), torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "velograd_rmsnorm_residual_fwd")
+    return y, h, inv_rms
+
+
 def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
                     weight: Optional[torch.Tensor], eps: float):
+    fast = _forward_fast(x, residual, weight, eps)
+    if fast is not None:
+        return fast
     lib = _lib.load()
     device = x.device
     code = _dtype_code(x, "x")
