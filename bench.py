@@ -66,6 +66,8 @@ def parse_args(argv=None):
                    help="record per-kernel HIP events on every N-th timed step")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU-baseline budget; 0 skips it")
+    p.add_argument("--no-fp8", action="store_true",
+                   help="skip timing the fp8-epilogue forward (reported under extra)")
     p.add_argument("--no-copy-ceiling", action="store_true",
                    help="skip the same-run stream-probe ceilings")
     return p.parse_args(argv)
@@ -182,6 +184,38 @@ def stream_ceilings(sets, stream_bytes: int, stream) -> dict:
         us = e0.elapsed_time(e1) * 1e3 / reps
         out[f"ceiling_{name}_gbs"] = round(nstreams * n16 * 16 / (us * 1e-6) / 1e9, 1)
     return out
+
+
+def fp8_forward_timing(lib, sets, rows: int, d: int, s: int, code: int, eps: float,
+                       stream) -> dict:
+    """The forward with the fp8 output epilogue (velograd_rmsnorm_residual_fwd_fp8) on the same
+    rotating buffer sets: y leaves as one e4m3 byte per element (written into the first half of
+    each set's y buffer) plus one fp32 scale per row."""
+    import torch
+
+    from velograd_amd import _lib
+
+    fn = lib.velograd_rmsnorm_residual_fwd_fp8
+    scales = [torch.empty(rows, device=b["x"].device, dtype=torch.float32) for b in sets]
+    args = [(b["x"].data_ptr(), b["res"].data_ptr(), b["w"].data_ptr(), b["y"].data_ptr(),
+             sc.data_ptr(), b["h"].data_ptr(), b["inv"].data_ptr(), rows, d, d, d, d, d, code,
+             code, eps, stream.cuda_stream) for b, sc in zip(sets, scales)]
+    for a in args:
+        _lib.check(fn(*a), "fwd_fp8 warm-up")
+    reps = 40
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    rc = 0
+    for i in range(reps):
+        rc |= fn(*args[i % len(args)])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    _lib.check(rc, "fwd_fp8 timed")
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    nbytes = 3 * rows * d * s + rows * d + d * s + 8 * rows
+    return {"fp8_fwd_us_mean": round(us, 2), "fp8_fwd_bytes": nbytes,
+            "fp8_fwd_gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
 
 
 def main(argv=None) -> int:
@@ -314,6 +348,9 @@ def main(argv=None) -> int:
                 t_ideal += bb / (ceil["ceiling_bwd_pattern_gbs"] * 1e9)
             extra["ceiling_step_gbs"] = round((fb + bb) / t_ideal / 1e9, 1)
             extra["frac_of_ceiling"] = round(value / extra["ceiling_step_gbs"], 4)
+
+    if not args.no_fp8:
+        extra.update(fp8_forward_timing(lib, sets, rows, d, s, code, eps, stream))
 
     cpu = None
     if args.cpu_seconds > 0:

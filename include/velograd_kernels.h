@@ -65,6 +65,31 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(
     int32_t dtype, int32_t w_dtype, float eps, void* hip_stream);
 
 /*
+ * Forward with an fp8 output epilogue: h and inv_rms as velograd_rmsnorm_residual_fwd, while y
+ * leaves as fp8 E4M3 codes with one dequantisation scale per row, ready for an fp8 GEMM:
+ *   amax = max |y| over the row (fp32 y, before any rounding; NaN if the row holds a NaN)
+ *   y_scale[row] = amax / 448                     (fp32; 448 is E4M3's largest finite value)
+ *   y_fp8 = e4m3(y * inv), inv = 1 / y_scale in fp32, or inv = 1 where y_scale is below the
+ *           smallest normal float (an all-zero row)
+ * e4m3 rounds to nearest even and saturates to +-448; NaN maps to the NaN code with its sign.
+ * The format is OCP "e4m3fn" (bias 7, no infinities, S.1111.111 = NaN), the E4M3 that the
+ * reference enumerates and decodes (include/velograd/kernels.h:29-37 PrecisionMode::FP8_E4M3,
+ * :58-73 fp8_e4m3_to_f32).  The reference has no fused quantising forward; this replaces the
+ * pair "fused_rmsnorm_residual_forward (fused.py:28-46) then a separate quantisation pass".
+ * Dequantise as y ~= float(y_fp8) * y_scale.
+ *
+ *   y_fp8   : [rows, dim] bytes; ld_y is its row stride in bytes.
+ *   y_scale : [rows] fp32 (required).
+ * Other arguments as velograd_rmsnorm_residual_fwd.
+ */
+VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_fp8(
+    const void* x, const void* residual, const void* weight,
+    uint8_t* y_fp8, float* y_scale, void* h, float* inv_rms,
+    int64_t rows, int64_t dim,
+    int64_t ld_x, int64_t ld_res, int64_t ld_y, int64_t ld_h,
+    int32_t dtype, int32_t w_dtype, float eps, void* hip_stream);
+
+/*
  * Backward of the forward above.
  * Replaces fused_rmsnorm_residual_backward (python/velograd/kernels/fused.py:48-66):
  *   gw = grad_y * weight; m = mean(gw * xhat); dx = inv_rms * (gw - xhat * m);

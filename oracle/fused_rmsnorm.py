@@ -87,3 +87,82 @@ def fused_rmsnorm_residual(x, residual=None, weight=None, eps: float = 1e-6) -> 
     w_arr = None if weight is None else np.asarray(weight, dtype=np.float32)   # :25-27
     normed, _, _ = fused_rmsnorm_residual_forward(x_arr, res_arr, w_arr, eps)   # :29
     return normed                                                               # :32
+
+
+# ---------------------------------------------------------------------------------------------
+# fp8 output epilogue (quantised y for the next GEMM).  The reference has no fused quantising
+# forward; its E4M3 format is fixed by include/velograd/kernels.h:29-37 (PrecisionMode::FP8_E4M3)
+# and the decoder at kernels.h:58-73 (bias 7, subnormals 2^-6 * m/8, S.1111.111 not a number).
+# ---------------------------------------------------------------------------------------------
+E4M3_MAX = np.float32(448.0)
+
+
+def e4m3fn_decode(codes: np.ndarray) -> np.ndarray:
+    """OCP e4m3fn byte -> float32: (-1)^s * 2^(e-7) * (1 + m/8), subnormal 2^-6 * m/8, NaN at
+    S.1111.111 (kernels.h:58-73 decodes the same values but returns 0 for the NaN codes)."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    e = (c >> 3) & 0xF
+    m = c & 7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    mag = np.where((c & 0x7F) == 0x7F, np.nan, mag)
+    return np.where((c >> 7) == 1, -mag, mag).astype(np.float32)
+
+
+# The 127 non-negative finite values, codes 0x00..0x7E, in ascending order.
+_E4M3_TABLE = e4m3fn_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)
+
+
+def e4m3fn_encode(v: np.ndarray) -> np.ndarray:
+    """float32 -> e4m3fn byte: the nearest finite value (ties to the even code), saturating at
+    +-448 (infinities included); NaN -> 0x7F with v's sign.  Written as a nearest-value search
+    over the table above, not with the bit arithmetic the device code uses."""
+    v = np.asarray(v, dtype=np.float32)
+    with np.errstate(invalid="ignore"):  # signalling-NaN bit patterns
+        a = np.abs(v).astype(np.float64)
+    nan = np.isnan(a)
+    a = np.where(nan, 0.0, np.minimum(a, 448.0))
+    hi = np.clip(np.searchsorted(_E4M3_TABLE, a, side="left"), 1, 0x7E)
+    lo = hi - 1
+    d_lo = a - _E4M3_TABLE[lo]
+    d_hi = _E4M3_TABLE[hi] - a
+    code = np.where(d_lo < d_hi, lo, np.where(d_hi < d_lo, hi, np.where(lo % 2 == 0, lo, hi)))
+    code = np.where(nan, 0x7F, code)
+    return (code | (np.signbit(v).astype(np.int64) << 7)).astype(np.uint8)
+
+
+def e4m3_inverse_scale(scale: np.ndarray) -> np.ndarray:
+    """1 / scale in float32, or 1 where scale is below the smallest normal float (zero rows, and
+    scales whose reciprocal could overflow); NaN stays NaN."""
+    scale = np.asarray(scale, dtype=np.float32)
+    tiny = np.float32(np.finfo(np.float32).tiny)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return np.where(scale < tiny, np.float32(1), np.float32(1) / scale).astype(np.float32)
+
+
+def quantize_rows_e4m3(y: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """Per-row fp8 quantisation: amax = max|y| over the last axis (NaN propagates),
+    scale = amax / 448 in float32, codes = e4m3(y * e4m3_inverse_scale(scale))."""
+    y = np.asarray(y, dtype=np.float32)
+    amax = np.max(np.abs(y), axis=-1, keepdims=True)
+    scale = (amax / E4M3_MAX).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        v = y * e4m3_inverse_scale(scale)
+    return e4m3fn_encode(v), scale
+
+
+def fused_rmsnorm_residual_forward_fp8(x: np.ndarray, residual: Optional[np.ndarray] = None,
+                                       weight: Optional[np.ndarray] = None, eps: float = 1e-6,
+                                       inv_rms: Optional[np.ndarray] = None):
+    """fused.py:28-46 followed by quantize_rows_e4m3 of y.  Returns (codes, scale, h, inv_rms).
+
+    Given `inv_rms` (e.g. the device's), y = (h * inv_rms) * weight is formed from it instead of
+    the recomputed statistic, so that every later step is elementwise and exactly reproducible.
+    """
+    y, h, r = fused_rmsnorm_residual_forward(x, residual, weight, eps)
+    if inv_rms is not None:
+        r = np.asarray(inv_rms, dtype=h.dtype).reshape(r.shape)
+        y = h * r
+        if weight is not None:
+            y = y * weight
+    codes, scale = quantize_rows_e4m3(y)
+    return codes, scale, h, r

@@ -86,6 +86,34 @@ def test_fwd_zero_rows_is_a_no_op(lib):
     assert _lib.last_error() == ""
 
 
+def _fwd_fp8(lib, **kw):
+    args = dict(x=16, residual=None, weight=None, y=32, y_scale=112, h=None, inv_rms=None,
+                rows=4, dim=64, ld_x=64, ld_res=64, ld_y=64, ld_h=64, dtype=2, w_dtype=2,
+                eps=1e-5, stream=None)
+    args.update(kw)
+    return lib.velograd_rmsnorm_residual_fwd_fp8(*args.values())
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=9), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    (dict(y_scale=None), _lib.ERR_INVALID_ARGUMENT, "y_scale must not be NULL"),
+    (dict(dim=0), _lib.ERR_INVALID_ARGUMENT, "invalid shape"),
+    (dict(y=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(ld_y=32), _lib.ERR_INVALID_ARGUMENT, "row strides"),
+    (dict(y_scale=16), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(y_scale=32), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(residual=48, h=112), _lib.ERR_INVALID_ARGUMENT, "alias"),
+])
+def test_fwd_fp8_argument_errors(lib, kw, code, msg):
+    assert _fwd_fp8(lib, **kw) == code
+    assert msg in _lib.last_error() and "fwd_fp8" in _lib.last_error()
+
+
+def test_fwd_fp8_zero_rows_is_a_no_op(lib):
+    assert _fwd_fp8(lib, rows=0, x=None, y=None, y_scale=None) == 0
+    assert _lib.last_error() == ""
+
+
 @pytest.mark.parametrize("kw,code,msg", [
     (dict(dtype=5), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
     (dict(dtype=1, w_dtype=2), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),

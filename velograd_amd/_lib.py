@@ -47,6 +47,16 @@ SIGNATURES = {
          _c_i32, _c_i32, ctypes.c_float,    # dtype, w_dtype, eps
          _c_ptr],                           # hip_stream
     ),
+    "velograd_rmsnorm_residual_fwd_fp8": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_ptr,            # x, residual, weight
+         _c_ptr, _c_ptr,                    # y_fp8, y_scale
+         _c_ptr, _c_ptr,                    # h, inv_rms
+         _c_i64, _c_i64,                    # rows, dim
+         _c_i64, _c_i64, _c_i64, _c_i64,    # ld_x, ld_res, ld_y (bytes), ld_h
+         _c_i32, _c_i32, ctypes.c_float,    # dtype, w_dtype, eps
+         _c_ptr],                           # hip_stream
+    ),
     "velograd_rmsnorm_residual_bwd": (
         _c_i32,
         [_c_ptr, _c_ptr, _c_i32,            # grad_y, saved, saved_is_h

@@ -34,6 +34,7 @@
 #include "velograd_kernels.h"
 
 #define VG_HOST_DEVICE __host__ __device__
+#include "fp8_e4m3.h"
 #include "launch_plan.h"
 
 #define VG_VERSION_STRING "velograd_amd 0.1.0 fused-rmsnorm-residual gfx950"
@@ -41,9 +42,12 @@
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+using vg_fp8::inverse_scale;
+using vg_fp8::kE4M3Max;
 using vg_plan::BwdPlan;
 using vg_plan::kGenericBlock;
 using vg_plan::kMaxNV;
@@ -258,6 +262,68 @@ __device__ inline float row_sum(float v, int tpr, int grp, float* red) {
   return v;
 }
 
+// Largest |value| over the `tpr` threads of row group `grp`, on the bit patterns of |value|
+// (sign cleared): for non-negative IEEE floats the unsigned order is the numeric order, and
+// every NaN pattern lies above +inf, so a NaN anywhere in the row wins (NaN propagates).
+template <int CTRL>
+__device__ inline uint32_t dpp_move_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+__device__ inline uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+__device__ inline uint32_t row_max_abs_bits(uint32_t v, int tpr, int grp, uint32_t* red) {
+  v = umax(v, dpp_move_u32<0xB1>(v));
+  v = umax(v, dpp_move_u32<0x4E>(v));
+  v = umax(v, dpp_move_u32<0x124>(v));
+  v = umax(v, dpp_move_u32<0x128>(v));
+  v = umax(umax((uint32_t)__builtin_amdgcn_readlane((int)v, 0),
+                (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
+           umax((uint32_t)__builtin_amdgcn_readlane((int)v, 32),
+                (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
+  if (tpr > kWave) {
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    const int wpr = tpr / kWave;
+    const uint32_t* p = red + grp * wpr;
+    uint32_t t = p[0];
+    for (int i = 1; i < wpr; ++i) t = umax(t, p[i]);
+    v = t;
+  }
+  return v;
+}
+
+// ------------------------------------------------------------------------------------------
+// fp8 E4M3 codes on the device.  gfx950's v_cvt_pk_fp8_f32 converts two fp32 values to OCP
+// e4m3fn with round to nearest even (one instruction per pair instead of the integer steps of
+// vg_fp8::e4m3_encode, which the CPU tests pin against the oracle).  It is not saturating, and
+// needs not be here: the inputs are y * (1 / scale) with |y| <= amax, so |y * inv| <=
+// 448 * (1 + 2^-22), which rounds to 448 (values up to the 464 midpoint do); the exception,
+// inv = 1 for a row whose scale is below the smallest normal float, has |y| < 2^-117.  NaN
+// converts to a NaN code.  Build with -DVG_FP8_SOFT_ENCODE=1 to use the integer encoder.
+// ------------------------------------------------------------------------------------------
+#ifndef VG_FP8_SOFT_ENCODE
+#define VG_FP8_SOFT_ENCODE 0
+#endif
+
+__device__ inline uint32_t e4m3x4(float a, float b, float c, float d) {
+#if VG_FP8_SOFT_ENCODE
+  return vg_fp8::e4m3_encode(a) | (vg_fp8::e4m3_encode(b) << 8) | (vg_fp8::e4m3_encode(c) << 16) |
+         (vg_fp8::e4m3_encode(d) << 24);
+#else
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+#endif
+}
+
+__device__ inline uint32_t e4m3x1(float a) {
+#if VG_FP8_SOFT_ENCODE
+  return vg_fp8::e4m3_encode(a);
+#else
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, a, 0, false) & 0xffu;
+#endif
+}
+
 // ------------------------------------------------------------------------------------------
 // Kernel arguments.
 // ------------------------------------------------------------------------------------------
@@ -265,9 +331,10 @@ struct FwdArgs {
   const void* x;
   const void* res;
   const void* w;
-  void* y;
+  void* y;          // activation dtype, or fp8 e4m3 codes (one byte each) for the fp8 epilogue
   void* h;
   float* inv_rms;
+  float* y_scale;   // fp8 epilogue: per-row dequantisation scale amax(|y|) / 448
   int64_t rows;
   int64_t ld_x, ld_res, ld_y, ld_h;
   int32_t dim;
@@ -294,7 +361,10 @@ struct BwdArgs {
 // ------------------------------------------------------------------------------------------
 // Forward, register-resident row.
 // ------------------------------------------------------------------------------------------
-template <int DT, int WDT, int NV>
+// Q8: the fp8 epilogue.  y is not stored in the activation dtype; a second row reduction finds
+// amax = max |y| over the row (fp32 y, before any rounding), the row's scale is amax / 448, and
+// y * (1 / scale) is stored as e4m3 codes: 8 bytes per bf16/fp16 chunk, 4 per fp32 chunk.
+template <int DT, int WDT, int NV, bool Q8>
 __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const FwdArgs a) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
@@ -366,16 +436,61 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 #pragma unroll
     for (int i = 0; i < WeightChunk<DT, WDT>::kParts; ++i) forget(wc[k].q[i]);
   }
+  auto make_y = [&](int k, float* yf) {
+    float hf[V], wf[V];
+    make_h(k, hf);
+    wc[k].unpack(has_w, wf);
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int c = lt + k * tpr;
-    if (row_ok && c < nchunk) {
-      float hf[V], wf[V], yf[V];
-      make_h(k, hf);
-      wc[k].unpack(has_w, wf);
+    for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
+  };
+
+  if constexpr (!Q8) {
 #pragma unroll
-      for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
-      store16_stream<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      if (row_ok && c < nchunk) {
+        float yf[V];
+        make_y(k, yf);
+        store16_stream<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
+      }
+    }
+  } else {
+    // y stays in registers from the amax pass to the encoding (NV * V floats).
+    __shared__ uint32_t red_max[kMaxWavesPerRow];
+    float yf[NV][V];
+    uint32_t am = 0;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      make_y(k, yf[k]);
+      if (row_ok && c < nchunk) {
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          am = umax(am, __builtin_bit_cast(uint32_t, yf[k][i]) & 0x7fffffffu);
+      }
+    }
+    am = row_max_abs_bits(am, tpr, grp, red_max);
+    const float scale = __builtin_bit_cast(float, am) / kE4M3Max;
+    const float inv = inverse_scale(scale);
+    if (row_ok && lt == 0) a.y_scale[row] = scale;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      if (row_ok && c < nchunk) {
+        uint32_t words[V / 4];
+#pragma unroll
+        for (int j = 0; j < V / 4; ++j) {
+          words[j] = e4m3x4(yf[k][4 * j] * inv, yf[k][4 * j + 1] * inv, yf[k][4 * j + 2] * inv,
+                            yf[k][4 * j + 3] * inv);
+        }
+        uint8_t* dst = static_cast<uint8_t*>(a.y) + row * a.ld_y + (int64_t)c * V;
+        if constexpr (V == 8) {
+          const u32x2 w2 = {words[0], words[1]};
+          __builtin_nontemporal_store(w2, reinterpret_cast<u32x2*>(dst));
+        } else {
+          __builtin_nontemporal_store(words[0], reinterpret_cast<uint32_t*>(dst));
+        }
+      }
     }
   }
 }
@@ -384,7 +499,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 // Forward, any dim / alignment: one row per workgroup, two passes over the row (the second
 // re-reads x and residual, normally from L2, and recomputes the identical fp32 h).
 // ------------------------------------------------------------------------------------------
-template <int DT, int WDT>
+template <int DT, int WDT, bool Q8>
 __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArgs a) {
   using C = Codec<DT>;
   using CW = Codec<WDT>;
@@ -406,11 +521,27 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
   const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
   if (threadIdx.x == 0 && a.inv_rms != nullptr) a.inv_rms[row] = r;
 
-  for (int j = threadIdx.x; j < a.dim; j += blockDim.x) {
+  auto y_at = [&](int j) {
     float hx = C::load1(a.x, row * a.ld_x + j);
     if (has_res) hx = hx + C::load1(a.res, row * a.ld_res + j);
     const float n = hx * r;
-    C::store1(a.y, row * a.ld_y + j, has_w ? n * CW::load1(a.w, j) : n);
+    return has_w ? n * CW::load1(a.w, j) : n;
+  };
+  if constexpr (!Q8) {
+    for (int j = threadIdx.x; j < a.dim; j += blockDim.x) C::store1(a.y, row * a.ld_y + j, y_at(j));
+  } else {
+    // fp8 epilogue (see fwd_vec_kernel): a third pass stores the codes.
+    __shared__ uint32_t red_max[kGenericBlock / kWave];
+    uint32_t am = 0;
+    for (int j = threadIdx.x; j < a.dim; j += blockDim.x)
+      am = umax(am, __builtin_bit_cast(uint32_t, y_at(j)) & 0x7fffffffu);
+    am = row_max_abs_bits(am, blockDim.x, 0, red_max);
+    const float scale = __builtin_bit_cast(float, am) / kE4M3Max;
+    const float inv = inverse_scale(scale);
+    if (threadIdx.x == 0) a.y_scale[row] = scale;
+    uint8_t* yq = static_cast<uint8_t*>(a.y) + row * a.ld_y;
+    for (int j = threadIdx.x; j < a.dim; j += blockDim.x)
+      yq[j] = (uint8_t)e4m3x1(y_at(j) * inv);
   }
 }
 
@@ -770,20 +901,20 @@ int elem_bytes_of(int32_t dt) {
 // ------------------------------------------------------------------------------------------
 // Typed launchers.
 // ------------------------------------------------------------------------------------------
-template <int DT, int WDT>
+template <int DT, int WDT, bool Q8>
 void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
   if (!p.vec) {
-    hipLaunchKernelGGL((fwd_generic_kernel<DT, WDT>), dim3((uint32_t)a.rows), dim3(p.block), 0,
-                       st, a);
+    hipLaunchKernelGGL((fwd_generic_kernel<DT, WDT, Q8>), dim3((uint32_t)a.rows), dim3(p.block),
+                       0, st, a);
     return;
   }
   const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups));
   const dim3 block(p.block);
   switch (p.nv) {
-    case 1: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 1>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 2>), grid, block, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 3>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 4>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 1, Q8>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 2, Q8>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 3, Q8>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 4, Q8>), grid, block, 0, st, a); break;
   }
 }
 
@@ -847,6 +978,76 @@ size_t workspace_bytes_for(int64_t rows, int64_t dim, int cus) {
   return vg_plan::bwd_workspace_bytes(rows, dim, cus, t.bwd_nv, t.bwd_block, t.bwd_waves_per_cu);
 }
 
+// Shared by the forward entry points.  y_scale != nullptr selects the fp8 epilogue: y then
+// holds one e4m3 byte per element and ld_y counts bytes.
+int32_t run_fwd(const char* what, const void* x, const void* residual, const void* weight,
+                void* y, float* y_scale, void* h, float* inv_rms, int64_t rows, int64_t dim,
+                int64_t ld_x, int64_t ld_res, int64_t ld_y, int64_t ld_h, int32_t dtype,
+                int32_t w_dtype, float eps, void* hip_stream) {
+  const bool q8 = y_scale != nullptr;
+  if (!types_ok(dtype, w_dtype))
+    return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
+                "%s: unsupported dtype/w_dtype pair (%d, %d): weight must be the activation "
+                "dtype or fp32",
+                what, (int)dtype, (int)w_dtype);
+  if (rows < 0 || dim <= 0 || dim > INT32_MAX)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: invalid shape rows=%lld dim=%lld", what,
+                (long long)rows, (long long)dim);
+  if (rows == 0) {
+    g_last_error[0] = '\0';
+    return 0;
+  }
+  if (x == nullptr || y == nullptr)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: x and y must not be NULL", what);
+  if (residual == nullptr) h = nullptr;  // h is x itself
+  if (ld_x < dim || ld_y < dim || (residual && ld_res < dim) || (h && ld_h < dim))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "%s: row strides must be >= dim (ld_x=%lld ld_res=%lld ld_y=%lld ld_h=%lld)",
+                what, (long long)ld_x, (long long)ld_res, (long long)ld_y, (long long)ld_h);
+  if (y == x || y == residual || (h && (h == x || h == residual || h == y)) ||
+      (q8 && ((const void*)y_scale == x || (const void*)y_scale == residual ||
+              (void*)y_scale == y || (h && (void*)y_scale == h))))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: outputs must not alias inputs", what);
+  if (rows > INT32_MAX)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: rows=%lld exceeds the grid limit", what,
+                (long long)rows);
+
+  const int eb = elem_bytes_of(dtype);
+  // The fp8 output moves 16 / eb bytes per 16-byte input chunk.
+  const bool y_aligned = q8 ? (((uintptr_t)y % (uintptr_t)(16 / eb)) == 0 && ld_y % (16 / eb) == 0)
+                            : (aligned16(y) && ld_ok(ld_y, eb));
+  const bool aligned = aligned16(x) && ld_ok(ld_x, eb) && y_aligned &&
+                       (!residual || (aligned16(residual) && ld_ok(ld_res, eb))) &&
+                       (!h || (aligned16(h) && ld_ok(ld_h, eb))) && (!weight || aligned16(weight));
+  const RowPlan p = plan_fwd(dim, eb, aligned);
+  if (!vg_plan::row_plan_valid(p, dim, eb))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: internal launch plan rejected (dim=%lld)",
+                what, (long long)dim);
+
+  FwdArgs a;
+  a.x = x;
+  a.res = residual;
+  a.w = weight;
+  a.y = y;
+  a.h = h;
+  a.inv_rms = inv_rms;
+  a.y_scale = y_scale;
+  a.rows = rows;
+  a.ld_x = ld_x;
+  a.ld_res = ld_res;
+  a.ld_y = ld_y;
+  a.ld_h = ld_h;
+  a.dim = (int32_t)dim;
+  a.tpr = p.tpr;
+  a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(hip_stream);
+  if (q8)
+    VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, true>(a, p, st)));
+  else
+    VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, false>(a, p, st)));
+  return check_launch(q8 ? "velograd_rmsnorm_residual_fwd_fp8" : "velograd_rmsnorm_residual_fwd");
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------------------------
@@ -869,58 +1070,18 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(const void* x, const void* re
                                                    int64_t ld_x, int64_t ld_res, int64_t ld_y,
                                                    int64_t ld_h, int32_t dtype, int32_t w_dtype,
                                                    float eps, void* hip_stream) {
-  if (!types_ok(dtype, w_dtype))
-    return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
-                "fwd: unsupported dtype/w_dtype pair (%d, %d): weight must be the activation "
-                "dtype or fp32",
-                (int)dtype, (int)w_dtype);
-  if (rows < 0 || dim <= 0 || dim > INT32_MAX)
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: invalid shape rows=%lld dim=%lld",
-                (long long)rows, (long long)dim);
-  if (rows == 0) {
-    g_last_error[0] = '\0';
-    return 0;
-  }
-  if (x == nullptr || y == nullptr)
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: x and y must not be NULL");
-  if (residual == nullptr) h = nullptr;  // h is x itself
-  if (ld_x < dim || ld_y < dim || (residual && ld_res < dim) || (h && ld_h < dim))
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
-                "fwd: row strides must be >= dim (ld_x=%lld ld_res=%lld ld_y=%lld ld_h=%lld)",
-                (long long)ld_x, (long long)ld_res, (long long)ld_y, (long long)ld_h);
-  if (y == x || y == residual || (h && (h == x || h == residual || h == y)))
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: outputs must not alias inputs");
-  if (rows > INT32_MAX)
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: rows=%lld exceeds the grid limit",
-                (long long)rows);
+  return run_fwd("fwd", x, residual, weight, y, nullptr, h, inv_rms, rows, dim, ld_x, ld_res,
+                 ld_y, ld_h, dtype, w_dtype, eps, hip_stream);
+}
 
-  const int eb = elem_bytes_of(dtype);
-  const bool aligned = aligned16(x) && aligned16(y) && ld_ok(ld_x, eb) && ld_ok(ld_y, eb) &&
-                       (!residual || (aligned16(residual) && ld_ok(ld_res, eb))) &&
-                       (!h || (aligned16(h) && ld_ok(ld_h, eb))) && (!weight || aligned16(weight));
-  const RowPlan p = plan_fwd(dim, eb, aligned);
-  if (!vg_plan::row_plan_valid(p, dim, eb))
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd: internal launch plan rejected (dim=%lld)",
-                (long long)dim);
-
-  FwdArgs a;
-  a.x = x;
-  a.res = residual;
-  a.w = weight;
-  a.y = y;
-  a.h = h;
-  a.inv_rms = inv_rms;
-  a.rows = rows;
-  a.ld_x = ld_x;
-  a.ld_res = ld_res;
-  a.ld_y = ld_y;
-  a.ld_h = ld_h;
-  a.dim = (int32_t)dim;
-  a.tpr = p.tpr;
-  a.eps = eps;
-  hipStream_t st = static_cast<hipStream_t>(hip_stream);
-  VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW>(a, p, st)));
-  return check_launch("velograd_rmsnorm_residual_fwd");
+VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_fp8(
+    const void* x, const void* residual, const void* weight, uint8_t* y_fp8, float* y_scale,
+    void* h, float* inv_rms, int64_t rows, int64_t dim, int64_t ld_x, int64_t ld_res,
+    int64_t ld_y, int64_t ld_h, int32_t dtype, int32_t w_dtype, float eps, void* hip_stream) {
+  if (rows > 0 && y_scale == nullptr)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd_fp8: y_scale must not be NULL");
+  return run_fwd("fwd_fp8", x, residual, weight, y_fp8, y_scale, h, inv_rms, rows, dim, ld_x,
+                 ld_res, ld_y, ld_h, dtype, w_dtype, eps, hip_stream);
 }
 
 VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(

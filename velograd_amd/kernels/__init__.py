@@ -29,6 +29,7 @@ Additions (keyword-only, off by default): `saved_is_h=True` lets the backward ta
 xhat (xhat is then formed in registers; same bytes moved), `dresidual_out=` receives a second
 copy of grad_x in a caller-owned buffer, and `grad_h=` adds the residual-stream gradient (the
 gradient reaching h from the next residual add) to grad_x in the same pass.
+`fused_rmsnorm_residual_forward_fp8` returns y as fp8 E4M3 codes with one scale per row.
 """
 
 from __future__ import annotations
@@ -45,6 +46,7 @@ __all__ = [
     "fused_rmsnorm_residual",
     "fused_rmsnorm_residual_forward",
     "fused_rmsnorm_residual_backward",
+    "fused_rmsnorm_residual_forward_fp8",
     "bwd_workspace_bytes",
 ]
 
@@ -170,10 +172,11 @@ def _forward_fast(x: torch.Tensor, residual: Optional[torch.Tensor],
 
 
 def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
-                    weight: Optional[torch.Tensor], eps: float):
-    fast = _forward_fast(x, residual, weight, eps)
-    if fast is not None:
-        return fast
+                    weight: Optional[torch.Tensor], eps: float, fp8: bool = False):
+    if not fp8:
+        fast = _forward_fast(x, residual, weight, eps)
+        if fast is not None:
+            return fast
     lib = _lib.load()
     device = x.device
     code = _dtype_code(x, "x")
@@ -192,28 +195,47 @@ def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
 
     x2 = _rows_view(x, "x")
     rows = x2.shape[0]
-    y = torch.empty(out_shape, dtype=x.dtype, device=device)
+    # fp8 codes are allocated as bytes and handed back viewed as float8_e4m3fn
+    y = torch.empty(out_shape, dtype=torch.uint8 if fp8 else x.dtype, device=device)
     h = torch.empty(out_shape, dtype=x.dtype, device=device) if residual is not None else x
-    inv_rms = torch.empty(tuple(out_shape[:-1]) + (1,), dtype=torch.float32, device=device)
-    if rows == 0:
+    stat_shape = tuple(out_shape[:-1]) + (1,)
+    inv_rms = torch.empty(stat_shape, dtype=torch.float32, device=device)
+    y_scale = torch.empty(stat_shape, dtype=torch.float32, device=device) if fp8 else None
+
+    def result():
+        if fp8:
+            return y.view(torch.float8_e4m3fn), y_scale, h, inv_rms
         return y, h, inv_rms
+
+    if rows == 0:
+        return result()
     if d == 0:
         # mean over an empty axis is NaN in NumPy; y and h are empty.
         inv_rms.fill_(float("nan"))
-        return y, h, inv_rms
+        if fp8:
+            y_scale.fill_(float("nan"))
+        return result()
 
     r2 = _rows_view(residual, "residual") if residual is not None else None
     y2 = y.view(-1, d)
     h2 = h.view(-1, d) if residual is not None else None
     with torch.cuda.device(device):
-        rc = lib.velograd_rmsnorm_residual_fwd(
-            x2.data_ptr(), _ptr(r2), _ptr(w),
-            y2.data_ptr(), _ptr(h2), inv_rms.data_ptr(),
-            rows, d,
-            _ld(x2), _ld(r2) if r2 is not None else d, d, d,
-            code, wcode, float(eps), _stream(device))
-    _lib.check(rc, "velograd_rmsnorm_residual_fwd")
-    return y, h, inv_rms
+        if fp8:
+            rc = lib.velograd_rmsnorm_residual_fwd_fp8(
+                x2.data_ptr(), _ptr(r2), _ptr(w),
+                y2.data_ptr(), y_scale.data_ptr(), _ptr(h2), inv_rms.data_ptr(),
+                rows, d,
+                _ld(x2), _ld(r2) if r2 is not None else d, d, d,
+                code, wcode, float(eps), _stream(device))
+        else:
+            rc = lib.velograd_rmsnorm_residual_fwd(
+                x2.data_ptr(), _ptr(r2), _ptr(w),
+                y2.data_ptr(), _ptr(h2), inv_rms.data_ptr(),
+                rows, d,
+                _ld(x2), _ld(r2) if r2 is not None else d, d, d,
+                code, wcode, float(eps), _stream(device))
+    _lib.check(rc, "velograd_rmsnorm_residual_fwd_fp8" if fp8 else "velograd_rmsnorm_residual_fwd")
+    return result()
 
 
 def _backward_device(grad_out: torch.Tensor, saved: torch.Tensor,
@@ -351,6 +373,21 @@ def fused_rmsnorm_residual_backward(grad_out: Any, normed_input: Any, weight: Op
     ghd = _host_to_device_f32(grad_h, device) if grad_h is not None else None
     dx, dw = _backward_device(gd, sd, wd, rd, saved_is_h, None, ghd)
     return _to_host(dx), _to_host(dw)
+
+
+def fused_rmsnorm_residual_forward_fp8(x: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                                       weight: Optional[torch.Tensor] = None, eps: float = 1e-6):
+    """The forward with y quantised to fp8 E4M3 for the next GEMM, in the same pass.
+
+    Returns (y_fp8, y_scale, h, inv_rms): y_fp8 is a float8_e4m3fn tensor shaped like x,
+    y_scale ([..., 1], float32) is amax(|y|) / 448 per row, the codes are e4m3(y * (1 /
+    y_scale)), and y ~= y_fp8.float() * y_scale; h and inv_rms as
+    fused_rmsnorm_residual_forward.  Rounding is to nearest even, saturating at +-448.  Device tensors only (an extension: the reference has no quantising forward; its
+    E4M3 format is include/velograd/kernels.h:29-37, 58-73).
+    """
+    if not _is_device_tensor(x):
+        raise TypeError("fused_rmsnorm_residual_forward_fp8 takes torch tensors on a ROCm device")
+    return _forward_device(x, residual, weight, eps, fp8=True)
 
 
 def fused_rmsnorm_residual(x: Any, residual: Optional[Any] = None, weight: Optional[Any] = None,
