@@ -68,6 +68,8 @@ def parse_args(argv=None):
                    help="CPU-baseline budget; 0 skips it")
     p.add_argument("--no-fp8", action="store_true",
                    help="skip timing the fp8-epilogue forward (reported under extra)")
+    p.add_argument("--no-rope", action="store_true",
+                   help="skip timing the fused RoPE kernel (reported under extra)")
     p.add_argument("--no-copy-ceiling", action="store_true",
                    help="skip the same-run stream-probe ceilings")
     return p.parse_args(argv)
@@ -218,6 +220,53 @@ def fp8_forward_timing(lib, sets, rows: int, d: int, s: int, code: int, eps: flo
             "fp8_fwd_gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
 
 
+def rope_timing(lib, tokens: int, stream, sets: int = 2) -> dict:
+    """Fused RoPE (velograd_rope) on a Llama-3-8B-like attention input of the same token
+    count: q [tokens, 32, 128] and k [tokens, 8, 128] bf16, theta 500000, one launch each per
+    step, rotating over `sets` buffer sets.  Bytes: q and k read once and written once."""
+    import torch
+
+    from velograd_amd import _lib
+
+    dev = torch.device("cuda", 0)
+    shapes = ((32, 128), (8, 128))
+    bufs = []
+    for _ in range(sets):
+        b = []
+        for heads, hd in shapes:
+            x = torch.randn(tokens, heads, hd, device=dev).to(torch.bfloat16)
+            b.append((x, torch.empty_like(x), heads, hd))
+        bufs.append(b)
+    fn = lib.velograd_rope
+    sp = stream.cuda_stream
+
+    def step(i):
+        rc = 0
+        for x, out, heads, hd in bufs[i % sets]:
+            rc |= fn(x.data_ptr(), out.data_ptr(), 1, tokens, heads, hd, hd, 500000.0, 0,
+                     _lib.DTYPE_BF16, sp)
+        return rc
+
+    for i in range(sets * 2):
+        _lib.check(step(i), "rope warm-up")
+    reps = 40
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    rc = 0
+    for i in range(reps):
+        rc |= step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    _lib.check(rc, "rope timed")
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    nbytes = sum(2 * tokens * h * d * 2 for h, d in shapes)
+    del bufs
+    return {"rope_qk_us_mean": round(us, 2), "rope_qk_bytes": nbytes,
+            "rope_qk_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5"}
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -351,6 +400,8 @@ def main(argv=None) -> int:
 
     if not args.no_fp8:
         extra.update(fp8_forward_timing(lib, sets, rows, d, s, code, eps, stream))
+    if not args.no_rope:
+        extra.update(rope_timing(lib, rows, stream))
 
     cpu = None
     if args.cpu_seconds > 0:

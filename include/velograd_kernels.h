@@ -131,6 +131,28 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
 VELOGRAD_API size_t velograd_rmsnorm_residual_bwd_workspace_bytes(int64_t rows, int64_t dim,
                                                                   int32_t device);
 
+/*
+ * Rotary position embedding, "rotate half" pairing, on one tensor (call once for q and once
+ * for k).  Replaces fused_rope_forward (python/velograd/kernels/fused.py:72-130), whose body
+ * this follows for a tensor laid out as [outer, seq, heads, dim]:
+ *   position of x[o, s, h, :] is s (fused.py:96-98); for j < rot_dim / 2,
+ *     freq_j = 1 / theta^(2j / rot_dim), angle = s * freq_j (fp32, fused.py:98-103),
+ *     (x_j, x_{j + rot_dim/2}) -> (x_j cos - x_{j+rot_dim/2} sin, x_j sin + x_{j+rot_dim/2} cos);
+ *   elements rot_dim .. dim-1 are copied (fused.py:119-120).
+ *
+ *   x, out   : [outer, seq, heads, dim] contiguous in `dtype`; out may be x itself (in place)
+ *              but must not otherwise overlap it.
+ *   rot_dim  : the reference's head_dim: even, 2 <= rot_dim <= dim, rot_dim <= 4096.
+ *   theta    : the frequency base (> 0).
+ *   inverse  : nonzero rotates by -angle: the backward (grad_x from grad_out), the rotary
+ *              backward rule of src/ops.rs:501-530 for this pairing.  No counterpart in the
+ *              fused reference, which has no backward.
+ */
+VELOGRAD_API int32_t velograd_rope(
+    const void* x, void* out,
+    int64_t outer, int64_t seq, int64_t heads, int64_t dim, int64_t rot_dim,
+    float theta, int32_t inverse, int32_t dtype, void* hip_stream);
+
 /* Text of the calling thread's last error ("" if none).  No counterpart in the reference. */
 VELOGRAD_API const char* velograd_kernels_last_error(void);
 

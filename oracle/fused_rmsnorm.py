@@ -166,3 +166,76 @@ def fused_rmsnorm_residual_forward_fp8(x: np.ndarray, residual: Optional[np.ndar
             y = y * weight
     codes, scale = quantize_rows_e4m3(y)
     return codes, scale, h, r
+
+
+# ---------------------------------------------------------------------------------------------
+# Fused RoPE (rotary position embedding), the reference's second fused kernel:
+#   python/velograd/kernels/fused.py:72-130 (fused_rope_forward) and the wrapper
+#   python/velograd/kernels/__init__.py:34-48 (fused_rope).  Pairs are (j, j + half) of each
+# head vector ("rotate half"), the position is the index along axis -3 (axis 0 for 2-D input),
+# and the last axis beyond head_dim passes through unchanged.
+# ---------------------------------------------------------------------------------------------
+def rope_tables(seq_len: int, head_dim: int, theta: float = 10000.0, dtype=np.float32):
+    """fused.py:98-103: (cos, sin) of shape [seq_len, head_dim // 2] in `dtype`."""
+    half = head_dim // 2
+    pos = np.arange(seq_len, dtype=dtype)                               # :98
+    dim_pairs = np.arange(half, dtype=dtype)                            # :99
+    freqs = 1.0 / (theta ** (2.0 * dim_pairs / head_dim))              # :100
+    angles = np.outer(pos, freqs)                                        # :101
+    return np.cos(angles), np.sin(angles)                                # :102-103
+
+
+def fused_rope_forward(q: np.ndarray, k: Optional[np.ndarray] = None,
+                       head_dim: Optional[int] = None, theta: float = 10000.0,
+                       inverse: bool = False):
+    """fused.py:72-130 op for op.  `inverse=True` rotates by -angle instead (the adjoint, i.e.
+    the backward: the reference's rotary backward rule, src/ops.rs:501-530, for this pairing)."""
+    orig_shape = q.shape
+    h_dim = head_dim or q.shape[-1]                                      # :83
+    half_dim = h_dim // 2                                                # :84
+    need_reshape = False
+    if q.ndim == 2 and q.shape[-1] > h_dim:                              # :88-94
+        need_reshape = True
+        num_heads = q.shape[-1] // h_dim
+        q = q.reshape(q.shape[0], num_heads, h_dim)
+        if k is not None and isinstance(k, np.ndarray) and k.ndim == 2:
+            k = k.reshape(k.shape[0], num_heads, h_dim)
+    seq_dim = -3 if q.ndim >= 3 else 0                                   # :96
+    seq_len = q.shape[seq_dim]                                           # :97
+    cos_vals, sin_vals = rope_tables(seq_len, h_dim, theta)              # float32, :98-103
+    if inverse:
+        sin_vals = -sin_vals
+    shape_pad = [1] * q.ndim                                             # :106-111
+    shape_pad[seq_dim] = seq_len
+    shape_pad[-1] = half_dim
+    cos_vals = cos_vals.reshape(shape_pad)
+    sin_vals = sin_vals.reshape(shape_pad)
+
+    def _apply_rope(t):                                                  # :113-121
+        x1 = t[..., :half_dim]
+        x2 = t[..., half_dim:h_dim]
+        rot_1 = x1 * cos_vals - x2 * sin_vals
+        rot_2 = x1 * sin_vals + x2 * cos_vals
+        res = np.concatenate([rot_1, rot_2], axis=-1)
+        if t.shape[-1] > h_dim:
+            res = np.concatenate([res, t[..., h_dim:]], axis=-1)
+        return res
+
+    q_rot = _apply_rope(q)                                               # :123
+    k_rot = _apply_rope(k) if (k is not None and isinstance(k, np.ndarray)) else None
+    if need_reshape:                                                     # :126-129
+        q_rot = q_rot.reshape(orig_shape)
+        if k_rot is not None:
+            k_rot = k_rot.reshape(orig_shape)
+    return q_rot, k_rot
+
+
+def fused_rope(x, k=None, head_dim: Optional[int] = None, base: float = 10000.0):
+    """kernels/__init__.py:34-48 for array-like inputs: float32 casts; q_rot, or (q_rot, k_rot)
+    when k is given."""
+    x_arr = np.asarray(x, dtype=np.float32)                              # :36
+    k_arr = np.asarray(k, dtype=np.float32) if k is not None else None  # :37
+    q_rot, k_rot = fused_rope_forward(x_arr, k_arr, head_dim=head_dim, theta=base)   # :39
+    if k is not None:                                                    # :46-48
+        return q_rot, k_rot
+    return q_rot

@@ -135,3 +135,64 @@ def to_device(a: np.ndarray, dtype: torch.dtype, device="cuda") -> torch.Tensor:
 def upcast(t: torch.Tensor) -> np.ndarray:
     """The values a reduced-precision tensor really holds, as fp32 numpy."""
     return t.detach().float().cpu().numpy()
+
+
+# ---------------------------------------------------------------------------------------------
+# Fused RoPE.  A float32 RoPE computes the angle pos * freq in float32, so a difference of a few
+# float32 ulps in freq (NumPy's float32 power is faithful, not correctly rounded) moves the angle
+# by a few ulps of |angle|, and the output by that many radians times |x1| + |x2|; cos and sin
+# add ~1.5 ulp each and the products and the sum a few more ulps of |x1| + |x2|.  The tolerance
+# for each rotated element of a pair (x1, x2) at angle a:
+#     |got - want| <= (ROPE_ANGLE_ULPS * 2^-24 * max(|a|, 1) + 2^-21) * (|x1| + |x2|)
+# Elements past head_dim are copied and must be exact.
+# ---------------------------------------------------------------------------------------------
+ROPE_ANGLE_ULPS = 16
+
+
+def rope_canonical(a: np.ndarray, head_dim: int) -> np.ndarray:
+    """View an input as [T, S, H, D] the way fused.py:86-96 reads it."""
+    a = np.asarray(a)
+    if a.ndim == 2:
+        if a.shape[-1] > head_dim:
+            return a.reshape(1, a.shape[0], a.shape[1] // head_dim, head_dim)
+        return a.reshape(1, a.shape[0], 1, a.shape[1])
+    return a.reshape(-1, *a.shape[-3:])
+
+
+def rope_angles(seq_len: int, head_dim: int, theta: float) -> np.ndarray:
+    """Exact (float64) angles pos * theta^(-2j/head_dim), shape [seq_len, head_dim // 2]."""
+    j = np.arange(head_dim // 2, dtype=np.float64)
+    return np.outer(np.arange(seq_len, dtype=np.float64), theta ** (-2.0 * j / head_dim))
+
+
+def rope_truth(x: np.ndarray, head_dim: int, theta: float, inverse: bool = False) -> np.ndarray:
+    """float64 rotate-half RoPE of a canonical [T, S, H, D] array, from the exact angles."""
+    x = np.asarray(x, dtype=np.float64)
+    half = head_dim // 2
+    ang = rope_angles(x.shape[1], head_dim, theta)[None, :, None, :]
+    c, s = np.cos(ang), np.sin(ang) * (-1.0 if inverse else 1.0)
+    x1, x2 = x[..., :half], x[..., half:head_dim]
+    return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c, x[..., head_dim:]], axis=-1)
+
+
+def rope_bound(x: np.ndarray, head_dim: int, theta: float) -> np.ndarray:
+    """Per-element tolerance for a canonical [T, S, H, D] input (see the comment above)."""
+    x = np.abs(np.asarray(x, dtype=np.float64))
+    half = head_dim // 2
+    ang = np.maximum(np.abs(rope_angles(x.shape[1], head_dim, theta)), 1.0)[None, :, None, :]
+    mag = x[..., :half] + x[..., half:head_dim]
+    b = (ROPE_ANGLE_ULPS * 2.0 ** -24 * ang + 2.0 ** -21) * mag
+    return np.concatenate([b, b, np.zeros_like(x[..., head_dim:])], axis=-1)
+
+
+def assert_rope_close(got: np.ndarray, want: np.ndarray, x: np.ndarray, head_dim: int,
+                      theta: float, extra: float = 0.0, what: str = "rope"):
+    """|got - want| <= rope_bound + extra * |want| elementwise (canonical arrays); `extra`
+    allows the rounding of a reduced-precision output."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    tol = rope_bound(x, head_dim, theta) + extra * np.abs(want)
+    err = np.abs(got - want)
+    bad = err > tol
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} elements out of tolerance; "
+                           f"worst excess {float((err - tol).max()):.3e}")

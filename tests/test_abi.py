@@ -150,3 +150,32 @@ def test_dtype_codes_match_header():
     for name, val in (("F32", _lib.DTYPE_F32), ("F16", _lib.DTYPE_F16), ("BF16", _lib.DTYPE_BF16)):
         assert re.search(rf"#define VELOGRAD_DTYPE_{name} {val}\b", text)
     assert _lib.TORCH_DTYPE_CODES[torch.bfloat16] == _lib.DTYPE_BF16
+
+
+def _rope(lib, **kw):
+    args = dict(x=16, out=32, outer=1, seq=4, heads=2, dim=64, rot_dim=64, theta=10000.0,
+                inverse=0, dtype=2, stream=None)
+    args.update(kw)
+    return lib.velograd_rope(*args.values())
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=3), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    (dict(seq=-1), _lib.ERR_INVALID_ARGUMENT, "invalid shape"),
+    (dict(rot_dim=63), _lib.ERR_INVALID_ARGUMENT, "must be even"),
+    (dict(rot_dim=0), _lib.ERR_INVALID_ARGUMENT, "must be even"),
+    (dict(rot_dim=66), _lib.ERR_INVALID_ARGUMENT, "<= dim"),
+    (dict(dim=8192, rot_dim=8192), _lib.ERR_INVALID_ARGUMENT, "<= 4096"),
+    (dict(x=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(theta=0.0), _lib.ERR_INVALID_ARGUMENT, "theta"),
+    (dict(theta=float("nan")), _lib.ERR_INVALID_ARGUMENT, "theta"),
+])
+def test_rope_argument_errors(lib, kw, code, msg):
+    # the message also shows that both translation units share the library's error state
+    assert _rope(lib, **kw) == code
+    assert msg in _lib.last_error() and "rope" in _lib.last_error()
+
+
+def test_rope_empty_is_a_no_op(lib):
+    assert _rope(lib, seq=0, x=None, out=None) == 0
+    assert _lib.last_error() == ""

@@ -130,3 +130,25 @@ def test_two_stacked_prenorm_blocks_chain_gradients():
                      (n2.weight.grad, W2.grad)):
         err = float((got.double().cpu() - ref).abs().max())
         assert err <= 1e-4 * float(ref.abs().max()), err
+
+
+def test_apply_rope_gradients_match_torch_autograd():
+    """apply_rope's backward (the inverse rotation) against float64 CPU autograd of the same
+    rotate-half formula (fused.py:113-121) on the exact angles."""
+    torch.manual_seed(4)
+    q = torch.randn(2, 64, 4, 32, device="cuda", requires_grad=True)
+    k = torch.randn(2, 64, 2, 32, device="cuda", requires_grad=True)
+    gq, gk = torch.randn_like(q), torch.randn_like(k)
+    q_rot, k_rot = vnn.apply_rope(q, k)
+    ((q_rot * gq).sum() + (k_rot * gk).sum()).backward()
+
+    def ref(x):
+        xd = x.detach().double().cpu().requires_grad_(True)
+        ang = torch.from_numpy(P.rope_angles(x.shape[1], 32, 10000.0))[None, :, None, :]
+        x1, x2 = xd[..., :16], xd[..., 16:]
+        return xd, torch.cat([x1 * ang.cos() - x2 * ang.sin(), x1 * ang.sin() + x2 * ang.cos()], -1)
+
+    (qd, qr), (kd, kr) = ref(q), ref(k)
+    ((qr * gq.double().cpu()).sum() + (kr * gk.double().cpu()).sum()).backward()
+    for got, want in ((q.grad, qd.grad), (k.grad, kd.grad)):
+        assert float((got.double().cpu() - want).abs().max()) <= 1e-5 * float(want.abs().max())

@@ -1,0 +1,133 @@
+"""GPU parity of the fused RoPE kernel (velograd_rope) against the oracle restatement of
+python/velograd/kernels/fused.py:72-130 on the same inputs.
+
+Tolerance (tests/_parity.py, stated there): per rotated element
+|got - want| <= (16 * 2^-24 * max(|angle|, 1) + 2^-21) * (|x1| + |x2|), i.e. a few float32 ulps of
+the angle (NumPy's float32 power is faithful, not correctly rounded, so freq and with it the
+angle may differ by ulps) plus a few ulps of the operands; reduced-precision outputs may also
+differ by their own rounding (half an ulp: 2^-8 relative for bf16, 2^-11 for fp16).  Elements past
+head_dim are copied exactly."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fused_rmsnorm as ora
+from tests import _parity as P
+from velograd_amd import _lib
+from velograd_amd import kernels as vk
+
+pytestmark = pytest.mark.gpu
+
+ROUNDING = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8 * 1.01, torch.float16: 2.0 ** -11 * 1.01}
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _check(got: torch.Tensor, x: torch.Tensor, hd: int, theta: float, inverse=False, what=""):
+    x32 = P.upcast(x)
+    want, _ = ora.fused_rope_forward(x32, None, head_dim=hd, theta=theta, inverse=inverse)
+    xc = P.rope_canonical(x32, hd)
+    P.assert_rope_close(P.rope_canonical(P.upcast(got), hd), P.rope_canonical(want, hd), xc, hd,
+                        theta, extra=ROUNDING[got.dtype], what=what)
+
+
+CASES = [
+    # (q shape, k shape or None, head_dim, theta, dtype)
+    ((512, 1024), None, 64, 10000.0, torch.float32),            # bench_vs_pytorch.py:57-59
+    ((33, 64), (33, 64), None, 10000.0, torch.bfloat16),        # 2-D, one head
+    ((2, 128, 8, 64), (2, 128, 2, 64), None, 10000.0, torch.bfloat16),   # GQA
+    ((3, 16, 96), None, 64, 10000.0, torch.float16),            # pass-through tail, vector path
+    ((1, 50, 3, 10), (1, 50, 5, 6), 6, 10000.0, torch.float32),  # scalar path (half = 3)
+    ((1, 32768, 2, 64), None, None, 10000.0, torch.float32),    # long positions
+    ((4096, 32, 128), (4096, 8, 128), None, 500000.0, torch.bfloat16),  # Llama-3-like
+]
+
+
+@pytest.mark.parametrize("qs,ks,hd,theta,dtype", CASES, ids=[str(c[0]) for c in CASES])
+def test_rope_matches_oracle(qs, ks, hd, theta, dtype):
+    _say(f"rope q{qs} k{ks} hd={hd} theta={theta} {dtype}")
+    rng = np.random.default_rng(sum(qs))
+    q = P.to_device(P.gaussian(rng, qs), dtype)
+    k = P.to_device(P.gaussian(rng, ks), dtype) if ks is not None else None
+    h_dim = hd or qs[-1]
+    q_rot, k_rot = vk.fused_rope_forward(q, k, head_dim=hd, theta=theta)
+    assert q_rot.shape == q.shape and q_rot.dtype == dtype
+    _check(q_rot, q, h_dim, theta, what="q")
+    if k is not None:
+        assert k_rot.shape == k.shape
+        _check(k_rot, k, h_dim, theta, what="k")
+    else:
+        assert k_rot is None
+
+
+def test_rope_reference_wrapper_case_host_arrays():
+    """The reference test's call (tests/test_exhaustive.py:126-128) with NumPy input: float32
+    ndarray out, computed on the GPU."""
+    x = P.gaussian(np.random.default_rng(1), (4, 16))
+    out = vk.fused_rope(x, head_dim=8)
+    assert isinstance(out, np.ndarray) and out.dtype == np.float32 and out.shape == (4, 16)
+    want = ora.fused_rope(x, head_dim=8)
+    P.assert_rope_close(P.rope_canonical(out, 8), P.rope_canonical(want, 8),
+                        P.rope_canonical(x, 8), 8, 10000.0)
+    q_rot, k_rot = vk.fused_rope(x, x * 2, head_dim=8)
+    assert np.array_equal(q_rot, out)
+    P.assert_rope_close(P.rope_canonical(k_rot, 8), P.rope_canonical(want * 2, 8),
+                        P.rope_canonical(x * 2, 8), 8, 10000.0)
+
+
+def test_rope_position_zero_exact_and_tail_copied():
+    rng = np.random.default_rng(2)
+    x = P.to_device(P.gaussian(rng, (2, 9, 4, 80)), torch.bfloat16)
+    y, _ = vk.fused_rope_forward(x, head_dim=64)
+    assert torch.equal(y[:, 0], x[:, 0])
+    assert torch.equal(y[..., 64:], x[..., 64:])
+
+
+def test_rope_backward_is_inverse_and_adjoint():
+    _say("rope backward")
+    rng = np.random.default_rng(3)
+    x = P.to_device(P.gaussian(rng, (2, 300, 4, 128)), torch.float32)
+    g = P.to_device(P.gaussian(rng, (2, 300, 4, 128)), torch.float32)
+    y, _ = vk.fused_rope_forward(x)
+    gx, _ = vk.fused_rope_backward(g)
+    _check(gx, g, 128, 10000.0, inverse=True, what="backward")
+    lhs = float((y.double() * g.double()).sum())
+    rhs = float((x.double() * gx.double()).sum())
+    assert abs(lhs - rhs) <= 1e-5 * float((x.double().abs() * gx.double().abs()).sum())
+    back, _ = vk.fused_rope_backward(y)
+    assert float((back - x).abs().max()) <= 1e-4
+
+
+def test_rope_in_place_through_the_c_abi():
+    rng = np.random.default_rng(4)
+    x = P.to_device(P.gaussian(rng, (1, 64, 8, 128)), torch.bfloat16)
+    want, _ = vk.fused_rope_forward(x)
+    buf = x.clone()
+    rc = _lib.load().velograd_rope(buf.data_ptr(), buf.data_ptr(), 1, 64, 8, 128, 128, 10000.0,
+                                   0, _lib.DTYPE_BF16, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "velograd_rope in place")
+    assert torch.equal(buf, want)
+
+
+def test_rope_layout_errors():
+    x = torch.zeros(4, 30, device="cuda")
+    with pytest.raises(ValueError):
+        vk.fused_rope_forward(x, head_dim=8)            # 30 is not a multiple of 8
+    with pytest.raises(ValueError):
+        vk.fused_rope_forward(x, head_dim=7)            # odd head_dim
+    with pytest.raises(ValueError):
+        vk.fused_rope_forward(torch.zeros(2, 5, 3, 16, device="cuda"),
+                              torch.zeros(2, 6, 3, 16, device="cuda"))   # k positions differ
+
+
+def test_rope_empty_and_deterministic():
+    e = torch.empty(0, 8, 64, device="cuda", dtype=torch.bfloat16)
+    assert vk.fused_rope_forward(e)[0].shape == e.shape
+    rng = np.random.default_rng(5)
+    x = P.to_device(P.gaussian(rng, (512, 16, 64)), torch.bfloat16)
+    assert torch.equal(vk.fused_rope_forward(x)[0], vk.fused_rope_forward(x)[0])

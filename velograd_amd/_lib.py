@@ -70,6 +70,13 @@ SIGNATURES = {
          _c_ptr],                           # hip_stream
     ),
     "velograd_rmsnorm_residual_bwd_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i32]),
+    "velograd_rope": (
+        _c_i32,
+        [_c_ptr, _c_ptr,                    # x, out
+         _c_i64, _c_i64, _c_i64, _c_i64,    # outer, seq, heads, dim
+         _c_i64, ctypes.c_float, _c_i32,    # rot_dim, theta, inverse
+         _c_i32, _c_ptr],                   # dtype, hip_stream
+    ),
     "velograd_kernels_last_error": (ctypes.c_char_p, []),
     "velograd_kernels_version": (ctypes.c_char_p, []),
 }

@@ -14,7 +14,8 @@ import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
-SRC = os.path.join(PKG_DIR, "csrc", "rmsnorm_residual.hip")
+# Translation units of the kernels library (one .so).
+SRCS = [os.path.join(PKG_DIR, "csrc", name) for name in ("rmsnorm_residual.hip", "rope.hip")]
 PROBE_SRC = os.path.join(PKG_DIR, "csrc", "stream_probe.hip")
 INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 CSRC_DIR = os.path.join(PKG_DIR, "csrc")
@@ -47,9 +48,9 @@ def find_hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP toolchain (ROCm) is required to build")
 
 
-def _hipcc(src: str, out: str, verbose: bool) -> None:
+def _hipcc(srcs, out: str, verbose: bool) -> None:
     tmp = out + ".tmp"
-    cmd = [find_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE_DIR, "-I", CSRC_DIR, src, "-o", tmp]
+    cmd = [find_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE_DIR, "-I", CSRC_DIR, *srcs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,8 +64,8 @@ def _hipcc(src: str, out: str, verbose: bool) -> None:
 def build_library(verbose: bool = False) -> str:
     """Compile the kernels (and the bench's stream probe) for gfx950; return the kernels' .so."""
     os.makedirs(LIB_DIR, exist_ok=True)
-    _hipcc(SRC, LIB_PATH, verbose)
-    _hipcc(PROBE_SRC, PROBE_LIB_PATH, verbose)
+    _hipcc(SRCS, LIB_PATH, verbose)
+    _hipcc([PROBE_SRC], PROBE_LIB_PATH, verbose)
     return LIB_PATH
 
 

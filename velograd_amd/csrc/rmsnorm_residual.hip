@@ -21,31 +21,14 @@
 // Row sums: DPP inside each 16-lane row of the wave, readlane across the four rows, LDS only
 // across the waves that share a row; every order is fixed, so results are bitwise reproducible.
 
-#include <hip/hip_runtime.h>
-
-#include <stdarg.h>
-#include <stddef.h>
-#include <stdint.h>
-#include <stdio.h>
-#include <stdlib.h>
-
-#include <atomic>
-
-#include "velograd_kernels.h"
-
-#define VG_HOST_DEVICE __host__ __device__
+#include "common.h"
 #include "fp8_e4m3.h"
-#include "launch_plan.h"
 
 #define VG_VERSION_STRING "velograd_amd 0.1.0 fused-rmsnorm-residual gfx950"
 
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
+using namespace vg;
 using vg_fp8::inverse_scale;
 using vg_fp8::kE4M3Max;
 using vg_plan::BwdPlan;
@@ -55,138 +38,6 @@ using vg_plan::kMaxWavesPerRow;
 using vg_plan::kWave;
 using vg_plan::max_block_for_nv;
 using vg_plan::RowPlan;
-
-// ------------------------------------------------------------------------------------------
-// Element codecs: 16 bytes <-> fp32 registers.
-// ------------------------------------------------------------------------------------------
-template <int DT>
-struct Codec;
-
-template <>
-struct Codec<VELOGRAD_DTYPE_F32> {
-  static constexpr int kBytes = 4;
-  static constexpr int kVec = 4;
-  __device__ static inline void unpack(const u32x4 v, float* f) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // Copy the element out first: hipcc 7.2 bit-casts an ext_vector element lvalue
-      // (`__builtin_bit_cast(float, v[i])`) as element 0 whatever i is.
-      const uint32_t u = v[i];
-      f[i] = __builtin_bit_cast(float, u);
-    }
-  }
-  __device__ static inline u32x4 pack(const float* f) {
-    u32x4 v;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __builtin_bit_cast(uint32_t, f[i]);
-    return v;
-  }
-  __device__ static inline float load1(const void* p, int64_t i) {
-    return static_cast<const float*>(p)[i];
-  }
-  __device__ static inline void store1(void* p, int64_t i, float f) {
-    static_cast<float*>(p)[i] = f;
-  }
-};
-
-template <>
-struct Codec<VELOGRAD_DTYPE_BF16> {
-  static constexpr int kBytes = 2;
-  static constexpr int kVec = 8;
-  __device__ static inline void unpack(const u32x4 v, float* f) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[2 * i] = __builtin_bit_cast(float, v[i] << 16);
-      f[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
-    }
-  }
-  __device__ static inline u32x4 pack(const float* f) {
-    u32x4 v;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bf16x2 p = {(__bf16)f[2 * i], (__bf16)f[2 * i + 1]};  // v_cvt_pk_bf16_f32, RNE
-      v[i] = __builtin_bit_cast(uint32_t, p);
-    }
-    return v;
-  }
-  __device__ static inline float load1(const void* p, int64_t i) {
-    const uint32_t u = static_cast<const uint16_t*>(p)[i];
-    return __builtin_bit_cast(float, u << 16);
-  }
-  __device__ static inline void store1(void* p, int64_t i, float f) {
-    static_cast<__bf16*>(p)[i] = (__bf16)f;
-  }
-};
-
-template <>
-struct Codec<VELOGRAD_DTYPE_F16> {
-  static constexpr int kBytes = 2;
-  static constexpr int kVec = 8;
-  __device__ static inline void unpack(const u32x4 v, float* f) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t u = v[i];  // scalar copy: see the fp32 codec
-      const f16x2 h = __builtin_bit_cast(f16x2, u);
-      f[2 * i] = (float)h[0];
-      f[2 * i + 1] = (float)h[1];
-    }
-  }
-  __device__ static inline u32x4 pack(const float* f) {
-    u32x4 v;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f16x2 p = {(_Float16)f[2 * i], (_Float16)f[2 * i + 1]};
-      v[i] = __builtin_bit_cast(uint32_t, p);
-    }
-    return v;
-  }
-  __device__ static inline float load1(const void* p, int64_t i) {
-    return (float)static_cast<const _Float16*>(p)[i];
-  }
-  __device__ static inline void store1(void* p, int64_t i, float f) {
-    static_cast<_Float16*>(p)[i] = (_Float16)f;
-  }
-};
-
-template <int DT>
-__device__ inline u32x4 load16(const void* base, int64_t elem) {
-  return *reinterpret_cast<const u32x4*>(static_cast<const char*>(base) +
-                                         elem * Codec<DT>::kBytes);
-}
-
-template <int DT>
-__device__ inline void store16(void* base, int64_t elem, const u32x4 v) {
-  *reinterpret_cast<u32x4*>(static_cast<char*>(base) + elem * Codec<DT>::kBytes) = v;
-}
-
-// Streamed activations are touched once per launch: non-temporal loads and stores keep them from
-// displacing reusable lines (weight, partial sums) in L2 and the MALL.  A stream-pattern probe
-// with the fwd (2 reads + 2 writes) and bwd (2 reads + 1 write) shapes measured +8..12% from the
-// non-temporal forms on MI355X.  Build with -DVG_STREAM_NT=0 to compare.
-#ifndef VG_STREAM_NT
-#define VG_STREAM_NT 1
-#endif
-
-template <int DT>
-__device__ inline u32x4 load16_stream(const void* base, int64_t elem) {
-  const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const char*>(base) +
-                                                  elem * Codec<DT>::kBytes);
-#if VG_STREAM_NT
-  return __builtin_nontemporal_load(p);
-#else
-  return *p;
-#endif
-}
-
-template <int DT>
-__device__ inline void store16_stream(void* base, int64_t elem, const u32x4 v) {
-  u32x4* p = reinterpret_cast<u32x4*>(static_cast<char*>(base) + elem * Codec<DT>::kBytes);
-#if VG_STREAM_NT
-  __builtin_nontemporal_store(v, p);
-#else
-  *p = v;
-#endif
-}
 
 // The weight values of one activation chunk (kVec(DT) columns), kept packed in registers: one
 // 16-byte vector when the weight has the activation dtype, kVec/4 vectors when it is fp32.
@@ -217,50 +68,6 @@ struct WeightChunk {
     for (int i = 0; i < kParts; ++i) Codec<WDT>::unpack(q[i], f + i * Codec<WDT>::kVec);
   }
 };
-
-// ------------------------------------------------------------------------------------------
-// Reductions.
-// ------------------------------------------------------------------------------------------
-template <int CTRL>
-__device__ inline float dpp_move(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Empty register barrier: the compiler must assume `v` changed here, so values it decoded from
-// `v` before this point are decoded again afterwards instead of being held in extra VGPRs
-// across the row reduction.  Emits no instruction.
-__device__ inline void forget(u32x4& v) { asm volatile("" : "+v"(v)); }
-
-// Sum over the 64 lanes of a wave; the result is wave-uniform.  Requires all lanes active.
-__device__ inline float wave_sum(float v) {
-  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_move<0x124>(v);  // row_ror:4
-  v += dpp_move<0x128>(v);  // row_ror:8  -> each lane holds its 16-lane row's sum
-  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-  return (r0 + r1) + (r2 + r3);
-}
-
-// Sum over the `tpr` threads of row group `grp` (threads grp*tpr .. grp*tpr+tpr-1, whole waves).
-// `red` holds one float per wave of the block; the caller alternates buffers between calls
-// that reuse it so one barrier per call suffices.
-__device__ inline float row_sum(float v, int tpr, int grp, float* red) {
-  v = wave_sum(v);
-  if (tpr > kWave) {
-    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
-    __syncthreads();
-    const int wpr = tpr / kWave;
-    const float* p = red + grp * wpr;
-    float t = p[0];
-    for (int i = 1; i < wpr; ++i) t += p[i];
-    v = t;
-  }
-  return v;
-}
 
 // Largest |value| over the `tpr` threads of row group `grp`, on the bit patterns of |value|
 // (sign cleared): for non-negative IEEE floats the unsigned order is the numeric order, and
@@ -812,50 +619,6 @@ __global__ __launch_bounds__(kReduceBlock) void dweight_reduce_kernel(const floa
   }
 }
 
-// ------------------------------------------------------------------------------------------
-// Host side: errors, device facts, launch plans.
-// ------------------------------------------------------------------------------------------
-thread_local char g_last_error[512] = "";
-
-int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-int32_t fail(int32_t code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-int32_t check_launch(const char* what) {
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess)
-    return fail((int32_t)e, "%s: launch failed: %s", what, hipGetErrorString(e));
-  g_last_error[0] = '\0';
-  return 0;
-}
-
-constexpr int kMaxDevices = 64;
-std::atomic<int> g_cu_count[kMaxDevices];
-
-int cu_count(int device) {
-  if (device < 0 || device >= kMaxDevices) return 0;
-  int v = g_cu_count[device].load(std::memory_order_relaxed);
-  if (v > 0) return v;
-  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
-      v <= 0)
-    return 0;
-  g_cu_count[device].store(v, std::memory_order_relaxed);
-  return v;
-}
-
-int env_int(const char* name, int dflt, int lo, int hi) {
-  const char* s = getenv(name);
-  if (s == nullptr || *s == '\0') return dflt;
-  const long v = strtol(s, nullptr, 10);
-  if (v < lo || v > hi) return dflt;
-  return (int)v;
-}
-
 // Launch-shape knobs, read once per process from the environment (for tuning sweeps; the
 // defaults are the measured best on MI355X).  Results do not depend on them except through the
 // dweight summation order, which stays fixed for a given setting.
@@ -886,17 +649,7 @@ BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cu
                            t.bwd_waves_per_cu);
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 bool ld_ok(int64_t ld, int elem_bytes) { return ((ld * elem_bytes) & 15) == 0; }
-
-int elem_bytes_of(int32_t dt) {
-  switch (dt) {
-    case VELOGRAD_DTYPE_F32: return 4;
-    case VELOGRAD_DTYPE_F16: return 2;
-    case VELOGRAD_DTYPE_BF16: return 2;
-    default: return 0;
-  }
-}
 
 // ------------------------------------------------------------------------------------------
 // Typed launchers.
@@ -994,7 +747,7 @@ int32_t run_fwd(const char* what, const void* x, const void* residual, const voi
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: invalid shape rows=%lld dim=%lld", what,
                 (long long)rows, (long long)dim);
   if (rows == 0) {
-    g_last_error[0] = '\0';
+    clear_error();
     return 0;
   }
   if (x == nullptr || y == nullptr)
@@ -1108,7 +861,7 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
                          dweight);
       return check_launch("velograd_rmsnorm_residual_bwd(dweight)");
     }
-    g_last_error[0] = '\0';
+    clear_error();
     return 0;
   }
   if (grad_y == nullptr || saved == nullptr || inv_rms == nullptr || dx == nullptr)

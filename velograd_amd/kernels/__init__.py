@@ -47,6 +47,9 @@ __all__ = [
     "fused_rmsnorm_residual_forward",
     "fused_rmsnorm_residual_backward",
     "fused_rmsnorm_residual_forward_fp8",
+    "fused_rope",
+    "fused_rope_forward",
+    "fused_rope_backward",
     "bwd_workspace_bytes",
 ]
 
@@ -388,6 +391,126 @@ def fused_rmsnorm_residual_forward_fp8(x: torch.Tensor, residual: Optional[torch
     if not _is_device_tensor(x):
         raise TypeError("fused_rmsnorm_residual_forward_fp8 takes torch tensors on a ROCm device")
     return _forward_device(x, residual, weight, eps, fp8=True)
+
+
+# ---------------------------------------------------------------------------------------------
+# Fused RoPE (python/velograd/kernels/fused.py:72-130, wrapper kernels/__init__.py:34-48)
+# ---------------------------------------------------------------------------------------------
+def _rope_q_layout(q_shape, h_dim: int):
+    """(outer, seq, heads, dim) of q as fused.py:83-97 reads it, and whether q is the 2-D
+    [seq, heads * head_dim] form that the reference reshapes into heads."""
+    if len(q_shape) < 2:
+        raise ValueError("fused_rope: q must have at least 2 dimensions ([seq, dim] or "
+                         "[..., seq, heads, dim])")
+    if h_dim < 2 or h_dim % 2 != 0:
+        raise ValueError(f"fused_rope: head_dim={h_dim} must be even and >= 2")
+    last = q_shape[-1]
+    if len(q_shape) == 2:
+        if last > h_dim:                                                   # fused.py:88-94
+            if last % h_dim != 0:
+                raise ValueError(f"fused_rope: last dimension {last} is not a multiple of "
+                                 f"head_dim={h_dim}")
+            return (1, q_shape[0], last // h_dim, h_dim), True
+        if last < h_dim:
+            raise ValueError(f"fused_rope: head_dim={h_dim} exceeds the last dimension {last}")
+        return (1, q_shape[0], 1, last), False
+    if last < h_dim:
+        raise ValueError(f"fused_rope: head_dim={h_dim} exceeds the last dimension {last}")
+    return (math.prod(q_shape[:-3]), q_shape[-3], q_shape[-2], last), False
+
+
+def _rope_k_layout(k_shape, q_shape, q_layout, q_split: bool, h_dim: int):
+    seq = q_layout[1]
+    if q_split:
+        # the reference reshapes k with q's head count and k_rot back to q's shape (:91-94,
+        # :126-129): only a k shaped like q is meaningful
+        if tuple(k_shape) != tuple(q_shape):
+            raise ValueError("fused_rope: with q of shape [seq, heads * head_dim], k must have "
+                             "q's shape")
+        return q_layout
+    if len(q_shape) == 2:
+        if len(k_shape) != 2 or k_shape[0] != seq:
+            raise ValueError(f"fused_rope: k must be [seq={seq}, dim] like q")
+        if k_shape[-1] < h_dim:
+            raise ValueError(f"fused_rope: head_dim={h_dim} exceeds k's last dimension")
+        return (1, seq, 1, k_shape[-1])
+    if len(k_shape) < 3 or k_shape[-3] != seq:
+        raise ValueError(f"fused_rope: k must be [..., seq={seq}, heads, dim] (positions on "
+                         f"axis -3, like q)")
+    if k_shape[-1] < h_dim:
+        raise ValueError(f"fused_rope: head_dim={h_dim} exceeds k's last dimension")
+    return (math.prod(k_shape[:-3]), k_shape[-3], k_shape[-2], k_shape[-1])
+
+
+def _rope_device(t: torch.Tensor, layout, h_dim: int, theta: float, inverse: bool,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    code = _dtype_code(t, "q/k")
+    src = t.contiguous()
+    dst = torch.empty_like(src) if out is None else out
+    outer, seq, heads, dim = layout
+    if src.numel() == 0:
+        return dst.view(t.shape)
+    with torch.cuda.device(src.device):
+        rc = _lib.load().velograd_rope(src.data_ptr(), dst.data_ptr(), outer, seq, heads, dim,
+                                       h_dim, float(theta), 1 if inverse else 0, code,
+                                       _stream(src.device))
+    _lib.check(rc, "velograd_rope")
+    return dst.view(t.shape)
+
+
+def _rope(q: Any, k: Optional[Any], head_dim: Optional[int], theta: float, inverse: bool):
+    on_device = _is_device_tensor(q)
+    if not on_device:
+        device = _require_gpu()
+        q_np = np.asarray(q.detach().cpu().numpy() if isinstance(q, torch.Tensor) else q,
+                          dtype=np.float32)
+        qd = torch.from_numpy(np.ascontiguousarray(q_np)).to(device)
+        kd = None
+        if isinstance(k, (np.ndarray, torch.Tensor)):       # fused.py:92,124 use k only if an array
+            k_np = k.detach().cpu().numpy() if isinstance(k, torch.Tensor) else k
+            kd = torch.from_numpy(np.ascontiguousarray(k_np, dtype=np.float32)).to(device)
+    else:
+        qd, kd = q, k
+        if kd is not None and (not isinstance(kd, torch.Tensor) or kd.device != qd.device):
+            raise ValueError("k must be a tensor on q's device")
+    h_dim = head_dim or qd.shape[-1]                                       # fused.py:83
+    q_layout, split = _rope_q_layout(tuple(qd.shape), h_dim)
+    k_layout = (_rope_k_layout(tuple(kd.shape), tuple(qd.shape), q_layout, split, h_dim)
+                if kd is not None else None)
+    q_rot = _rope_device(qd, q_layout, h_dim, theta, inverse)
+    k_rot = _rope_device(kd, k_layout, h_dim, theta, inverse) if kd is not None else None
+    if on_device:
+        return q_rot, k_rot
+    return _to_host(q_rot), _to_host(k_rot)
+
+
+def fused_rope_forward(q: Any, k: Optional[Any] = None, head_dim: Optional[int] = None,
+                       theta: float = 10000.0):
+    """Rotary position embedding of q (and k), "rotate half" pairing; (q_rot, k_rot) like
+    fused.py:72-130.  Positions run along axis -3 ([..., seq, heads, dim]) or axis 0 for 2-D
+    input, whose last axis is split into heads of head_dim when it is longer; the last axis past
+    head_dim passes through.  Device tensors keep their dtype; arrays are computed in float32
+    on the GPU and returned as float32 ndarrays (k only when it is an array, as the reference)."""
+    return _rope(q, k, head_dim, theta, inverse=False)
+
+
+def fused_rope_backward(grad_q: Any, grad_k: Optional[Any] = None,
+                        head_dim: Optional[int] = None, theta: float = 10000.0):
+    """Gradients of fused_rope_forward: the inverse rotation of grad_q (and grad_k).  An
+    extension: the reference's fused RoPE has no backward (its rotary backward rule is
+    src/ops.rs:501-530)."""
+    return _rope(grad_q, grad_k, head_dim, theta, inverse=True)
+
+
+def fused_rope(x: Any, k: Optional[Any] = None, head_dim: Optional[int] = None,
+               base: float = 10000.0):
+    """Wrapper like kernels/__init__.py:34-48: q_rot, or (q_rot, k_rot) when k is given."""
+    if not _is_device_tensor(x) and k is not None and not isinstance(k, (np.ndarray, torch.Tensor)):
+        k = np.asarray(k, dtype=np.float32)                                # :37
+    q_rot, k_rot = fused_rope_forward(x, k, head_dim=head_dim, theta=base)
+    if k is not None:
+        return q_rot, k_rot
+    return q_rot
 
 
 def fused_rmsnorm_residual(x: Any, residual: Optional[Any] = None, weight: Optional[Any] = None,

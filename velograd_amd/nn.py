@@ -13,6 +13,8 @@ gradient function (python/velograd/kernels/__init__.py:30-31).  Here:
   also floors mean(x^2) at 1e-12 before adding eps (`nn.py:349`); with the default eps that
   changes inv_rms by at most 5e-7 relative, and only for rows whose mean square is below 1e-12.
 * `FusedAddRMSNorm(dim, eps=1e-6)` — `(y, h) = module(x, residual)` for pre-norm blocks.
+* `FusedRoPEFunction` / `apply_rope(q, k, head_dim, theta)` — the fused RoPE kernel with its
+  inverse-rotation backward.
 
 All computation runs in the HIP kernels; there is no CPU path.
 """
@@ -25,7 +27,8 @@ import torch
 
 from . import kernels as _k
 
-__all__ = ["FusedRMSNormResidualFunction", "fused_add_rmsnorm", "RMSNorm", "FusedAddRMSNorm"]
+__all__ = ["FusedRMSNormResidualFunction", "fused_add_rmsnorm", "RMSNorm", "FusedAddRMSNorm",
+           "FusedRoPEFunction", "apply_rope"]
 
 
 class FusedRMSNormResidualFunction(torch.autograd.Function):
@@ -98,3 +101,26 @@ class FusedAddRMSNorm(torch.nn.Module):
 
     def extra_repr(self) -> str:
         return f"{self.dim}, eps={self.eps}"
+
+
+class FusedRoPEFunction(torch.autograd.Function):
+    """Differentiable fused RoPE of one tensor (fused.py:72-130 semantics); the backward is the
+    inverse rotation of the incoming gradient, in one kernel launch."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, head_dim: Optional[int], theta: float):
+        ctx.head_dim, ctx.theta = head_dim, theta
+        return _k.fused_rope_forward(x, None, head_dim=head_dim, theta=theta)[0]
+
+    @staticmethod
+    def backward(ctx, grad: torch.Tensor):
+        gx = _k.fused_rope_backward(grad, None, head_dim=ctx.head_dim, theta=ctx.theta)[0]
+        return gx, None, None
+
+
+def apply_rope(q: torch.Tensor, k: Optional[torch.Tensor] = None,
+               head_dim: Optional[int] = None, theta: float = 10000.0):
+    """Differentiable `(q_rot, k_rot)`; k_rot is None without k."""
+    q_rot = FusedRoPEFunction.apply(q, head_dim, theta)
+    k_rot = FusedRoPEFunction.apply(k, head_dim, theta) if k is not None else None
+    return q_rot, k_rot
