@@ -14,11 +14,12 @@
 // head), then streams the tokens' elements with 16-byte loads and stores, every element moving
 // through HBM once.  The kernel is HBM-bound: ~6 flops per element pair.
 //
-// Numerics: freq_j is theta^e evaluated in double and rounded to float (the correctly rounded
-// float32 power in all but vanishing cases; NumPy's float32 power, which the reference uses, is
-// faithful, within 1 ulp), then 1 / p in float32; the angle is the float32 product s * freq_j
-// as np.outer forms it; sincosf is ocml's (a few ulps); products and sums round as NumPy's
-// float32 ufuncs do (-ffp-contract=off).
+// Numerics: freq_j = 1 / powf(theta, e) in float32, as the reference forms it with NumPy's
+// float32 power (faithful, within 1 ulp; so is ocml's powf: the two may differ by an ulp or
+// two, which moves the angle by that many ulps of |angle|); the angle is the float32 product
+// s * freq_j as np.outer forms it; sincosf is ocml's (a few ulps); products and sums round as
+// NumPy's float32 ufuncs do (-ffp-contract=off).  A double-precision pow was measured to cost
+// 89 VGPRs (5 waves per SIMD) against 50 (8 waves) for powf.
 
 #include "common.h"
 
@@ -28,7 +29,7 @@ using namespace vg;
 
 constexpr int kRopeBlock = 256;
 constexpr int kRopeMaxHalf = 2048;       // rot_dim <= 4096
-constexpr int kRopeLdsFloats = 8192;     // freq[half] + cos/sin[tpb][half] <= 32 KiB
+constexpr int kRopeLdsFloats = 8192;     // bound on freq[half] + cos/sin[tpb][half]: 32 KiB
 static_assert(3 * kRopeMaxHalf <= kRopeLdsFloats, "one token's tables must fit the LDS array");
 constexpr int kRopeTargetElems = 4096;   // elements per workgroup the token grouping aims at
 
@@ -51,7 +52,7 @@ __device__ inline void rope_tables(const RopeArgs& a, int64_t tok0, int ntok, fl
                                    float* cs, float* sn) {
   for (int j = threadIdx.x; j < a.half; j += blockDim.x) {
     const float e = (2.0f * (float)j) / (float)(2 * a.half);          // fused.py:100
-    const float p = (float)pow((double)a.theta, (double)e);
+    const float p = powf(a.theta, e);
     freq[j] = 1.0f / p;
   }
   __syncthreads();
@@ -68,58 +69,115 @@ __device__ inline void rope_tables(const RopeArgs& a, int64_t tok0, int ntok, fl
   __syncthreads();
 }
 
+// Item `it` of a workgroup: token t, head h, chunk c of that head (chunks < rot_items are pairs
+// of rotated chunks, the rest pass-through chunks).
+struct RopeItem {
+  int t, c;
+  int64_t head0;  // element offset of the head vector
+};
+
+__device__ inline RopeItem rope_item(const RopeArgs& a, int64_t tok0, int it, int per_tok,
+                                     int per_head) {
+  RopeItem r;
+  r.t = it / per_tok;
+  const int rest = it - r.t * per_tok;
+  const int h = rest / per_head;
+  r.c = rest - h * per_head;
+  r.head0 = ((tok0 + r.t) * a.heads + h) * (int64_t)a.dim;
+  return r;
+}
+
 // VEC: 16-byte chunks (needs half and dim multiples of the chunk, 16-byte aligned tensors);
-// otherwise one element (pair) per item.
+// otherwise one element (pair) per item.  The first kPrefetch items of every thread are loaded
+// before the tables are built, so the table work overlaps their HBM latency.
+constexpr int kPrefetch = 2;
+
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kRopeBlock) void rope_kernel(const RopeArgs a) {
   using C = Codec<DT>;
   constexpr int V = VEC ? C::kVec : 1;
-  __shared__ float lds[kRopeLdsFloats];
+  extern __shared__ float lds[];  // freq[half], cos[tpb][half], sin[tpb][half]
   const int64_t tok0 = (int64_t)blockIdx.x * a.tpb;
   const int ntok = (int)((a.tokens - tok0) < a.tpb ? (a.tokens - tok0) : a.tpb);
   float* freq = lds;
   float* cs = lds + a.half;
   float* sn = cs + a.tpb * a.half;
-  rope_tables(a, tok0, ntok, freq, cs, sn);
 
   const int rot_items = a.half / V;                                     // per head
   const int tail_items = a.copy_tail ? (a.dim - 2 * a.half) / V : 0;   // per head
   const int per_head = rot_items + tail_items;
   const int per_tok = a.heads * per_head;
   const int n = ntok * per_tok;
-  for (int it = threadIdx.x; it < n; it += blockDim.x) {
-    const int t = it / per_tok;
-    const int r = it - t * per_tok;
-    const int h = r / per_head;
-    const int c = r - h * per_head;
-    const int64_t head0 = ((tok0 + t) * a.heads + h) * (int64_t)a.dim;
-    if (c < rot_items) {
-      const int j0 = c * V;
-      const float* cp = cs + t * a.half + j0;
-      const float* sp = sn + t * a.half + j0;
-      if constexpr (VEC) {
-        float x1[V], x2[V], r1[V], r2[V];
-        C::unpack(load16_stream<DT>(a.x, head0 + j0), x1);
-        C::unpack(load16_stream<DT>(a.x, head0 + a.half + j0), x2);
+
+  auto rotate_store = [&](const RopeItem& r, const u32x4 va, const u32x4 vb) {
+    const int j0 = r.c * V;
+    const float* cp = cs + r.t * a.half + j0;
+    const float* sp = sn + r.t * a.half + j0;
+    float x1[C::kVec], x2[C::kVec], r1[C::kVec], r2[C::kVec];
+    C::unpack(va, x1);
+    C::unpack(vb, x2);
 #pragma unroll
-        for (int i = 0; i < V; ++i) {
-          const float cv = cp[i], sv = sp[i];
-          r1[i] = x1[i] * cv - x2[i] * sv;                               // fused.py:116
-          r2[i] = x1[i] * sv + x2[i] * cv;                               // fused.py:117
+    for (int i = 0; i < C::kVec; ++i) {
+      const float cv = cp[i], sv = sp[i];
+      r1[i] = x1[i] * cv - x2[i] * sv;                                   // fused.py:116
+      r2[i] = x1[i] * sv + x2[i] * cv;                                   // fused.py:117
+    }
+    store16_stream<DT>(a.out, r.head0 + j0, C::pack(r1));
+    store16_stream<DT>(a.out, r.head0 + a.half + j0, C::pack(r2));
+  };
+
+  if constexpr (VEC) {
+    u32x4 pa[kPrefetch], pb[kPrefetch];
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) {
+      const int it = threadIdx.x + p * blockDim.x;
+      pa[p] = u32x4{0u, 0u, 0u, 0u};
+      pb[p] = u32x4{0u, 0u, 0u, 0u};
+      if (it < n) {
+        const RopeItem r = rope_item(a, tok0, it, per_tok, per_head);
+        if (r.c < rot_items) {
+          pa[p] = load16_stream<DT>(a.x, r.head0 + r.c * V);
+          pb[p] = load16_stream<DT>(a.x, r.head0 + a.half + r.c * V);
+        } else {
+          pa[p] = load16_stream<DT>(a.x, r.head0 + 2 * a.half + (int64_t)(r.c - rot_items) * V);
         }
-        store16_stream<DT>(a.out, head0 + j0, C::pack(r1));
-        store16_stream<DT>(a.out, head0 + a.half + j0, C::pack(r2));
-      } else {
-        const float x1 = C::load1(a.x, head0 + j0);
-        const float x2 = C::load1(a.x, head0 + a.half + j0);
-        C::store1(a.out, head0 + j0, x1 * cp[0] - x2 * sp[0]);
-        C::store1(a.out, head0 + a.half + j0, x1 * sp[0] + x2 * cp[0]);
       }
-    } else {
-      const int64_t e0 = head0 + 2 * a.half + (int64_t)(c - rot_items) * V;
-      if constexpr (VEC) {
-        store16_stream<DT>(a.out, e0, load16_stream<DT>(a.x, e0));
+    }
+    rope_tables(a, tok0, ntok, freq, cs, sn);
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) {
+      const int it = threadIdx.x + p * blockDim.x;
+      if (it < n) {
+        const RopeItem r = rope_item(a, tok0, it, per_tok, per_head);
+        if (r.c < rot_items)
+          rotate_store(r, pa[p], pb[p]);
+        else
+          store16_stream<DT>(a.out, r.head0 + 2 * a.half + (int64_t)(r.c - rot_items) * V, pa[p]);
+      }
+    }
+    for (int it = threadIdx.x + kPrefetch * blockDim.x; it < n; it += blockDim.x) {
+      const RopeItem r = rope_item(a, tok0, it, per_tok, per_head);
+      if (r.c < rot_items) {
+        rotate_store(r, load16_stream<DT>(a.x, r.head0 + r.c * V),
+                     load16_stream<DT>(a.x, r.head0 + a.half + r.c * V));
       } else {
+        const int64_t e0 = r.head0 + 2 * a.half + (int64_t)(r.c - rot_items) * V;
+        store16_stream<DT>(a.out, e0, load16_stream<DT>(a.x, e0));
+      }
+    }
+  } else {
+    rope_tables(a, tok0, ntok, freq, cs, sn);
+    for (int it = threadIdx.x; it < n; it += blockDim.x) {
+      const RopeItem r = rope_item(a, tok0, it, per_tok, per_head);
+      if (r.c < rot_items) {
+        const float* cp = cs + r.t * a.half + r.c;
+        const float* sp = sn + r.t * a.half + r.c;
+        const float x1 = C::load1(a.x, r.head0 + r.c);
+        const float x2 = C::load1(a.x, r.head0 + a.half + r.c);
+        C::store1(a.out, r.head0 + r.c, x1 * cp[0] - x2 * sp[0]);
+        C::store1(a.out, r.head0 + a.half + r.c, x1 * sp[0] + x2 * cp[0]);
+      } else {
+        const int64_t e0 = r.head0 + 2 * a.half + (r.c - rot_items);
         C::store1(a.out, e0, C::load1(a.x, e0));
       }
     }
@@ -129,10 +187,11 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(const RopeArgs a) {
 template <int DT>
 void launch_rope(const RopeArgs& a, bool vec, hipStream_t st) {
   const dim3 grid((uint32_t)((a.tokens + a.tpb - 1) / a.tpb));
+  const size_t lds = (size_t)(a.half + 2 * a.tpb * a.half) * sizeof(float);
   if (vec)
-    hipLaunchKernelGGL((rope_kernel<DT, true>), grid, dim3(kRopeBlock), 0, st, a);
+    hipLaunchKernelGGL((rope_kernel<DT, true>), grid, dim3(kRopeBlock), lds, st, a);
   else
-    hipLaunchKernelGGL((rope_kernel<DT, false>), grid, dim3(kRopeBlock), 0, st, a);
+    hipLaunchKernelGGL((rope_kernel<DT, false>), grid, dim3(kRopeBlock), lds, st, a);
 }
 
 }  // namespace
