@@ -68,6 +68,8 @@ def parse_args(argv=None):
                    help="CPU-baseline budget; 0 skips it")
     p.add_argument("--no-fp8", action="store_true",
                    help="skip timing the fp8-epilogue forward (reported under extra)")
+    p.add_argument("--no-decode", action="store_true",
+                   help="skip the config E decode-latency table (reported under extra)")
     p.add_argument("--no-rope", action="store_true",
                    help="skip timing the fused RoPE kernel (reported under extra)")
     p.add_argument("--no-copy-ceiling", action="store_true",
@@ -220,6 +222,90 @@ def fp8_forward_timing(lib, sets, rows: int, d: int, s: int, code: int, eps: flo
             "fp8_fwd_gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
 
 
+def decode_latency(lib, stream, calls: int = 1000) -> list:
+    """Config E: forward at decode shapes T in {1, 7, 64, 257} x D in {5120, 7168} bf16, where
+    launch latency, not bandwidth, sets the time.  Per shape: device us per call back to back
+    (HIP events around `calls` launches), median isolated latency (launch to completion, events
+    around one launch, 200 samples), median host us per call of the C ABI (ctypes) and of the
+    Python API, and device us per call when 32 calls are captured in a HIP graph and replayed."""
+    import torch
+
+    from velograd_amd import _lib
+    from velograd_amd import kernels as vk
+
+    dev = torch.device("cuda", 0)
+    out = []
+    fn = lib.velograd_rmsnorm_residual_fwd
+    for d in (5120, 7168):
+        for t in (1, 7, 64, 257):
+            x = torch.randn(t, d, device=dev).to(torch.bfloat16)
+            r = torch.randn(t, d, device=dev).to(torch.bfloat16)
+            w = (1 + 0.1 * torch.randn(d, device=dev)).to(torch.bfloat16)
+            y, h = torch.empty_like(x), torch.empty_like(x)
+            inv = torch.empty(t, device=dev)
+            args = (x.data_ptr(), r.data_ptr(), w.data_ptr(), y.data_ptr(), h.data_ptr(),
+                    inv.data_ptr(), t, d, d, d, d, d, _lib.DTYPE_BF16, _lib.DTYPE_BF16, 1e-6,
+                    stream.cuda_stream)
+            for _ in range(50):
+                fn(*args)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            rc = 0
+            for _ in range(calls):
+                rc |= fn(*args)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            _lib.check(rc, "decode calls")
+            dev_us = e0.elapsed_time(e1) * 1e3 / calls
+            iso = []
+            for _ in range(200):
+                e0.record(stream)
+                fn(*args)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                iso.append(e0.elapsed_time(e1) * 1e3)
+            host_c, host_py = [], []
+            for _ in range(calls):
+                t0 = time.perf_counter()
+                fn(*args)
+                host_c.append(time.perf_counter() - t0)
+            torch.cuda.synchronize()
+            for _ in range(calls):
+                t0 = time.perf_counter()
+                vk.fused_rmsnorm_residual_forward(x, r, w, 1e-6)
+                host_py.append(time.perf_counter() - t0)
+            torch.cuda.synchronize()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    vk.fused_rmsnorm_residual_forward(x, r, w, 1e-6)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(32):
+                    vk.fused_rmsnorm_residual_forward(x, r, w, 1e-6)
+            for _ in range(3):
+                g.replay()
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(30):
+                g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
+            out.append({"T": t, "D": d, "device_us_back_to_back": round(dev_us, 2),
+                        "isolated_us_median": round(med(iso), 2),
+                        "host_us_c_abi_median": round(med(host_c) * 1e6, 2),
+                        "host_us_python_api_median": round(med(host_py) * 1e6, 2),
+                        "graph_replay_us_per_call": round(e0.elapsed_time(e1) * 1e3 / 960, 2),
+                        "bytes": 8 * t * d + 2 * d + 4 * t})
+            del g
+    return out
+
+
 def rope_timing(lib, tokens: int, stream, sets: int = 2) -> dict:
     """Fused RoPE (velograd_rope) on a Llama-3-8B-like attention input of the same token
     count: q [tokens, 32, 128] and k [tokens, 8, 128] bf16, theta 500000, one launch each per
@@ -292,10 +378,19 @@ def main(argv=None) -> int:
     gen = torch.Generator(device=dev).manual_seed(0)
     ws_bytes = vk.bwd_workspace_bytes(rows, d, dev)
     sets = []
+    def act():
+        """x / residual: N(0, 1); config D: std 2 with 0.1% of entries scaled by 50."""
+        a = torch.randn(rows, d, device=dev, generator=gen)
+        if args.config == "D":
+            a *= 2.0
+            mask = torch.rand(rows, d, device=dev, generator=gen) < 1e-3
+            a[mask] *= 50.0
+        return a.to(dt)
+
     for _ in range(args.sets):
         b = {
-            "x": torch.randn(rows, d, device=dev, generator=gen).to(dt),
-            "res": torch.randn(rows, d, device=dev, generator=gen).to(dt),
+            "x": act(),
+            "res": act(),
             "w": (1 + 0.1 * torch.randn(d, device=dev, generator=gen)).to(dt),
             "y": torch.empty(rows, d, device=dev, dtype=dt),
             "h": torch.empty(rows, d, device=dev, dtype=dt),
@@ -398,10 +493,25 @@ def main(argv=None) -> int:
             extra["ceiling_step_gbs"] = round((fb + bb) / t_ideal / 1e9, 1)
             extra["frac_of_ceiling"] = round(value / extra["ceiling_step_gbs"], 4)
 
+    # Warm-MALL figure (informational): the same step repeated on one buffer set, whose
+    # 768 MiB exceed the 256 MiB MALL only partly.
+    torch.cuda.synchronize()
+    tw0 = time.perf_counter()
+    for _ in range(50):
+        rc = fwd_fn(*fwd_args[0])
+        if with_bwd:
+            rc |= bwd_fn(*bwd_args[0])
+    torch.cuda.synchronize()
+    extra["warm_one_set_step_us"] = round((time.perf_counter() - tw0) * 1e6 / 50, 2)
+    _lib.check(rc, "warm steps")
+    extra["warm_one_set_gbs"] = round((fb + bb) / (extra["warm_one_set_step_us"] * 1e-6) / 1e9, 1)
+
     if not args.no_fp8:
         extra.update(fp8_forward_timing(lib, sets, rows, d, s, code, eps, stream))
     if not args.no_rope:
         extra.update(rope_timing(lib, rows, stream))
+    if not args.no_decode:
+        extra["config_E_decode"] = decode_latency(lib, stream)
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -423,8 +533,10 @@ def main(argv=None) -> int:
         "config": {
             "workload": (f"config {args.config}: fused RMSNorm+residual "
                          f"{'fwd+bwd' if with_bwd else 'fwd'}, {rows}x{d} "
-                         f"{'bf16' if s == 2 else 'fp32'}, eps {eps}, x,residual,grad_y ~ "
-                         f"N(0,1), weight 1+0.1N(0,1), {args.sets} rotating buffer sets"),
+                         f"{'bf16' if s == 2 else 'fp32'}, eps {eps}, "
+                         + ("x,residual ~ N(0,2) with 0.1% x50 outliers, grad_y ~ N(0,1)"
+                            if args.config == "D" else "x,residual,grad_y ~ N(0,1)")
+                         + f", weight 1+0.1N(0,1), {args.sets} rotating buffer sets"),
             "rows": rows,
             "dim": d,
             "algorithmic_bytes_per_step": fb + bb,
