@@ -58,7 +58,7 @@ def bwd_bytes(rows: int, d: int, s: int) -> int:
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--steps", type=int, default=500)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", choices=sorted(CONFIGS), default="C")
     p.add_argument("--sets", type=int, default=4, help="rotating buffer sets (MALL hygiene)")
@@ -68,6 +68,8 @@ def parse_args(argv=None):
                    help="CPU-baseline budget; 0 skips it")
     p.add_argument("--no-fp8", action="store_true",
                    help="skip timing the fp8-epilogue forward (reported under extra)")
+    p.add_argument("--no-other-configs", action="store_true",
+                   help="skip the B/C/D summary lines (reported under extra)")
     p.add_argument("--no-decode", action="store_true",
                    help="skip the config E decode-latency table (reported under extra)")
     p.add_argument("--no-rope", action="store_true",
@@ -353,41 +355,35 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2) -> dict:
             "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5"}
 
 
-def main(argv=None) -> int:
-    args = parse_args(argv)
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus "
-              f"{args.gpus}", file=sys.stderr)
-        return 2
-
+def measure(lib, config: str, steps: int, warmup: int, nsets: int, event_every: int,
+            stream) -> dict:
+    """Time `steps` steps of `config` (forward, plus backward where the config has one) on
+    `nsets` rotating buffer sets; per-kernel HIP events on every `event_every`-th step."""
     import torch
 
     from velograd_amd import _lib
     from velograd_amd import kernels as vk
 
-    rows, d, eps, with_bwd = CONFIGS[args.config]
-    dt = torch.bfloat16 if args.config != "A" else torch.float32
+    rows, d, eps, with_bwd = CONFIGS[config]
+    dt = torch.bfloat16 if config != "A" else torch.float32
     s = 2 if dt == torch.bfloat16 else 4
     code = _lib.TORCH_DTYPE_CODES[dt]
     dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    lib = _lib.load()
-    stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
-
     gen = torch.Generator(device=dev).manual_seed(0)
     ws_bytes = vk.bwd_workspace_bytes(rows, d, dev)
-    sets = []
+
     def act():
         """x / residual: N(0, 1); config D: std 2 with 0.1% of entries scaled by 50."""
         a = torch.randn(rows, d, device=dev, generator=gen)
-        if args.config == "D":
+        if config == "D":
             a *= 2.0
             mask = torch.rand(rows, d, device=dev, generator=gen) < 1e-3
             a[mask] *= 50.0
         return a.to(dt)
 
-    for _ in range(args.sets):
+    sets = []
+    for _ in range(nsets):
         b = {
             "x": act(),
             "res": act(),
@@ -420,7 +416,7 @@ def main(argv=None) -> int:
         _lib.check(fwd_fn(*a), "fwd")
     torch.cuda.synchronize()
 
-    n = args.sets
+    n = nsets
     half = n // 2
 
     def step(k, evs=None):
@@ -435,20 +431,20 @@ def main(argv=None) -> int:
                 evs[2].record(stream)
         return rc
 
-    for k in range(args.warmup):
+    for k in range(warmup):
         _lib.check(step(k), "warm-up step")
     torch.cuda.synchronize()
 
     # Kernel durations come from HIP events recorded on the launch stream inside the timed
-    # region, on every `--event-every`-th step: each marker adds a little time to its step, so
+    # region, on every `event_every`-th step: each marker adds a little time to its step, so
     # sampling keeps the wall-clock figure close to an unmarked run.
-    every = max(1, args.event_every)
-    sampled = [k for k in range(args.steps) if k % every == 0]
+    every = max(1, event_every)
+    sampled = [k for k in range(steps) if k % every == 0]
     events = {k: [torch.cuda.Event(enable_timing=True) for _ in range(3)] for k in sampled}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     rc = 0
-    for k in range(args.steps):
+    for k in range(steps):
         rc |= step(k, events.get(k))
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -457,30 +453,84 @@ def main(argv=None) -> int:
 
     fwd_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
     mean_fwd_ms = sum(fwd_ms) / len(fwd_ms)
-    med_fwd_ms = fwd_ms[len(fwd_ms) // 2]
     fb = fwd_bytes(rows, d, s)
     bb = bwd_bytes(rows, d, s) if with_bwd else 0
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    ms_per_step = (t1 - t0) * 1e3 / steps
     value = (fb + bb) / (ms_per_step * 1e-3) / 1e9
-
-    extra = {
+    out = {
+        "value": value,
+        "ms_per_step": ms_per_step,
         "fwd_us_mean": round(mean_fwd_ms * 1e3, 2),
-        "fwd_us_median": round(med_fwd_ms * 1e3, 2),
+        "fwd_us_median": round(fwd_ms[len(fwd_ms) // 2] * 1e3, 2),
         "fwd_gbs": round(fb / (mean_fwd_ms * 1e-3) / 1e9, 1),
         "fwd_bytes": fb,
+        "kernel_event_samples": len(events),
     }
     if with_bwd:
         bwd_ms = sorted(e[1].elapsed_time(e[2]) for e in events)
         mean_bwd_ms = sum(bwd_ms) / len(bwd_ms)
-        extra.update({
+        out.update({
             "bwd_us_mean": round(mean_bwd_ms * 1e3, 2),
             "bwd_us_median": round(bwd_ms[len(bwd_ms) // 2] * 1e3, 2),
             "bwd_gbs": round(bb / (mean_bwd_ms * 1e-3) / 1e9, 1),
             "bwd_bytes": bb,
             "bwd_workspace_bytes": ws_bytes,
         })
-    extra["rows_per_s"] = round(rows / (ms_per_step * 1e-3), 1)
-    extra["pct_hbm_peak"] = round(100.0 * value / HBM_PEAK_GBS, 2)
+    out["rows_per_s"] = round(rows / (ms_per_step * 1e-3), 1)
+    out["pct_hbm_peak"] = round(100.0 * value / HBM_PEAK_GBS, 2)
+    out.update({"_sets": sets, "_fwd_args": fwd_args, "_bwd_args": bwd_args, "_s": s,
+                "_code": code})
+    return out
+
+
+def other_configs(lib, main_config: str, stream) -> dict:
+    """The other bandwidth configurations at modest step counts (B forward, D forward +
+    backward, C when it is not the headline), reported under extra."""
+    import torch
+
+    out = {}
+    for cfg, steps, nsets in (("B", 100, 4), ("C", 100, 4), ("D", 40, 2)):
+        if cfg == main_config:
+            continue
+        m = measure(lib, cfg, steps, 5, nsets, 5, stream)
+        for k in ("_sets", "_fwd_args", "_bwd_args", "_s", "_code"):
+            m.pop(k)
+        m["value"] = round(m["value"], 1)
+        m["ms_per_step"] = round(m["ms_per_step"], 4)
+        m["steps"], m["sets"] = steps, nsets
+        out[cfg] = m
+        del m
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus "
+              f"{args.gpus}", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from velograd_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    rows, d, eps, with_bwd = CONFIGS[args.config]
+    m = measure(lib, args.config, args.steps, args.warmup, args.sets, args.event_every, stream)
+    sets, fwd_args, bwd_args = m.pop("_sets"), m.pop("_fwd_args"), m.pop("_bwd_args")
+    fwd_fn = lib.velograd_rmsnorm_residual_fwd
+    bwd_fn = lib.velograd_rmsnorm_residual_bwd
+    s, code = m.pop("_s"), m.pop("_code")
+    dt = torch.bfloat16 if s == 2 else torch.float32
+    value, ms_per_step = m.pop("value"), m.pop("ms_per_step")
+    fb, bb = m["fwd_bytes"], m.get("bwd_bytes", 0)
+    mean_fwd_ms = m["fwd_us_mean"] * 1e-3
+    extra = m
 
     if not args.no_copy_ceiling:
         ceil = stream_ceilings(sets, rows * d * s, stream)
@@ -512,6 +562,10 @@ def main(argv=None) -> int:
         extra.update(rope_timing(lib, rows, stream))
     if not args.no_decode:
         extra["config_E_decode"] = decode_latency(lib, stream)
+    if not args.no_other_configs:
+        del sets, fwd_args, bwd_args
+        torch.cuda.empty_cache()
+        extra["other_configs"] = other_configs(lib, args.config, stream)
 
     cpu = None
     if args.cpu_seconds > 0:
