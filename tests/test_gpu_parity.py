@@ -1,5 +1,5 @@
 """GPU parity: the HIP kernels (through the C ABI, via velograd_amd.kernels) against the pinned
-CPU oracle on the same seeded inputs, on every BASELINE configuration and on the edge cases the
+CPU oracle on the same seeded inputs, on every benchmark configuration (A-E) and on the edge cases the
 reference's semantics define.  Tolerances are stated in tests/_parity.py."""
 
 import json
@@ -61,7 +61,8 @@ def test_known_answer_of_reference_rust_test():
 
 
 # ---------------------------------------------------------------------------------------------
-# BASELINE configurations.
+# Benchmark configurations A-E (shapes, dtypes, input distributions and eps of the headline
+# benchmark and its companions).
 # ---------------------------------------------------------------------------------------------
 def test_config_a_fp32_forward():
     """[4,128,768] fp32, x,res ~ N(0,1), weight 1+0.1N(0,1), eps 1e-6, seed 0."""
