@@ -25,6 +25,20 @@ How it is pinned (tests/test_oracle.py):
 Parity status: forward and backward are pinned; bit-exactness to the reference's own NumPy
 rounding sequence is not separately pinned (the reference module is not imported), which the
 stated tolerances make unnecessary.
+
+Beyond the reference's RMSNorm functions (pins in tests/test_fp8_codec.py and
+tests/test_rope_oracle.py):
+  * backward_with_residual_grad: torch autograd of the pre-norm block (tests/test_oracle.py);
+  * e4m3fn_decode / e4m3fn_encode / quantize_rows_e4m3 / fused_rmsnorm_residual_forward_fp8
+    (the fp8 output epilogue, format of include/velograd/kernels.h:29-37,58-73): torch's
+    float8_e4m3fn casts over every code and a dense set of values, the reference decoder's
+    values, round-trip and rounding bounds, and the per-row scale facts (largest element maps
+    to 448, dequantisation error bound);
+  * rope_tables / fused_rope_forward / fused_rope (fused.py:72-130, kernels/__init__.py:34-48):
+    float64 truth from the exact angles and torch's rotate-half form within an angle-scaled
+    tolerance, position 0 = identity, pair norms, the relative-position property, the adjoint
+    identity of the inverse rotation, and the reference test's own call.
+Each set of pins is shown to catch planted mistakes.  No function here is "parity unpinned".
 """
 
 from __future__ import annotations
