@@ -434,9 +434,11 @@ def _rope_k_layout(k_shape, q_shape, q_layout, q_split: bool, h_dim: int):
         if k_shape[-1] < h_dim:
             raise ValueError(f"fused_rope: head_dim={h_dim} exceeds k's last dimension")
         return (1, seq, 1, k_shape[-1])
-    if len(k_shape) < 3 or k_shape[-3] != seq:
-        raise ValueError(f"fused_rope: k must be [..., seq={seq}, heads, dim] (positions on "
-                         f"axis -3, like q)")
+    if len(k_shape) != len(q_shape) or k_shape[-3] != seq:
+        # the reference would broadcast other leading axes or a length-1 sequence axis
+        # against q's tables (fused.py:106-121); the device API takes k with q's positions
+        raise ValueError(f"fused_rope: k must be [..., seq={seq}, heads, dim] with q's number of "
+                         f"axes (positions on axis -3, like q)")
     if k_shape[-1] < h_dim:
         raise ValueError(f"fused_rope: head_dim={h_dim} exceeds k's last dimension")
     return (math.prod(k_shape[:-3]), k_shape[-3], k_shape[-2], k_shape[-1])
@@ -490,7 +492,11 @@ def fused_rope_forward(q: Any, k: Optional[Any] = None, head_dim: Optional[int] 
     fused.py:72-130.  Positions run along axis -3 ([..., seq, heads, dim]) or axis 0 for 2-D
     input, whose last axis is split into heads of head_dim when it is longer; the last axis past
     head_dim passes through.  Device tensors keep their dtype; arrays are computed in float32
-    on the GPU and returned as float32 ndarrays (k only when it is an array, as the reference)."""
+    on the GPU and returned as float32 ndarrays (k only when it is an array, as the reference).
+
+    Inputs the reference takes only through NumPy broadcasting raise ValueError here: an odd
+    head_dim or one longer than the last axis, and a k whose positions are not q's (another
+    sequence length, a length-1 sequence axis on one side, or another number of axes)."""
     return _rope(q, k, head_dim, theta, inverse=False)
 
 
