@@ -67,7 +67,7 @@ def parse_args(argv=None):
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU-baseline budget; 0 skips it")
     p.add_argument("--no-fp8", action="store_true",
-                   help="skip timing the fp8-epilogue forward (reported under extra)")
+                   help="skip timing the fp8 and MX-epilogue forwards (reported under extra)")
     p.add_argument("--no-other-configs", action="store_true",
                    help="skip the B/C/D summary lines (reported under extra)")
     p.add_argument("--no-decode", action="store_true",
@@ -222,6 +222,42 @@ def fp8_forward_timing(lib, sets, rows: int, d: int, s: int, code: int, eps: flo
     nbytes = 3 * rows * d * s + rows * d + d * s + 8 * rows
     return {"fp8_fwd_us_mean": round(us, 2), "fp8_fwd_bytes": nbytes,
             "fp8_fwd_gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+
+
+def mx_forward_timing(lib, sets, rows: int, d: int, s: int, code: int, eps: float,
+                      stream) -> dict:
+    """The forward with the MX epilogues (velograd_rmsnorm_residual_fwd_mx), MXFP8 and MXFP4,
+    on the same rotating buffer sets: y leaves as e4m3 bytes or e2m1 nibbles (written into each
+    set's y buffer) plus one E8M0 byte per 32 elements."""
+    import torch
+
+    from velograd_amd import _lib
+
+    fn = lib.velograd_rmsnorm_residual_fwd_mx
+    scales = [torch.empty(rows, d // 32, device=b["x"].device, dtype=torch.uint8) for b in sets]
+    out = {}
+    for name, fmt, ybytes in (("mxfp8", _lib.MX_E4M3, d), ("mxfp4", _lib.MX_E2M1, d // 2)):
+        args = [(b["x"].data_ptr(), b["res"].data_ptr(), b["w"].data_ptr(), b["y"].data_ptr(),
+                 sc.data_ptr(), b["h"].data_ptr(), b["inv"].data_ptr(), rows, d, d, d, ybytes,
+                 d // 32, d, code, code, fmt, eps, stream.cuda_stream)
+                for b, sc in zip(sets, scales)]
+        for a in args:
+            _lib.check(fn(*a), f"fwd_{name} warm-up")
+        reps = 40
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        rc = 0
+        for i in range(reps):
+            rc |= fn(*args[i % len(args)])
+        e1.record(stream)
+        torch.cuda.synchronize()
+        _lib.check(rc, f"fwd_{name} timed")
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = 3 * rows * d * s + rows * ybytes + rows * (d // 32) + d * s + 4 * rows
+        out.update({f"{name}_fwd_us_mean": round(us, 2), f"{name}_fwd_bytes": nbytes,
+                    f"{name}_fwd_gbs": round(nbytes / (us * 1e-6) / 1e9, 1)})
+    return out
 
 
 def decode_latency(lib, stream, calls: int = 1000) -> list:
@@ -558,6 +594,8 @@ def main(argv=None) -> int:
 
     if not args.no_fp8:
         extra.update(fp8_forward_timing(lib, sets, rows, d, s, code, eps, stream))
+        if d % 32 == 0:
+            extra.update(mx_forward_timing(lib, sets, rows, d, s, code, eps, stream))
     if not args.no_rope:
         extra.update(rope_timing(lib, rows, stream))
     if not args.no_decode:

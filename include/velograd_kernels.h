@@ -89,6 +89,38 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_fp8(
     int64_t ld_x, int64_t ld_res, int64_t ld_y, int64_t ld_h,
     int32_t dtype, int32_t w_dtype, float eps, void* hip_stream);
 
+/* Element formats of the MX (OCP Microscaling) forward. */
+#define VELOGRAD_MX_E4M3 0 /* MXFP8: fp8 E4M3 elements */
+#define VELOGRAD_MX_E2M1 1 /* MXFP4: fp4 E2M1 elements, two per byte */
+
+/*
+ * Forward with an MX output epilogue, the block-scaled layout of gfx950's scaled MFMA: h and
+ * inv_rms as velograd_rmsnorm_residual_fwd, while y leaves in blocks of 32 consecutive elements
+ * of a row that share one E8M0 scale 2^s:
+ *   amax = max |y| over the block (fp32 y, before any rounding)
+ *   s    = floor(log2(amax)) - emax, emax = 8 (E4M3) or 2 (E2M1), clamped to [-127, 127];
+ *          scale code s + 127; code 0 for an all-zero block; 0xFF (NaN) and zero element codes
+ *          for a block whose amax is not finite
+ *   element codes = round-to-nearest-even, saturating (+-448 / +-6) codes of y * 2^-s
+ * (OCP Microscaling Formats v1.0).  E2M1 nibbles are packed two per byte, the even element in
+ * the low nibble, and the scales are one byte per block: the layout the reference decodes with
+ * its E2M1 table (include/velograd/kernels.h:47-51, 97-101, 339-347).  No counterpart in the
+ * reference's NumPy path; it replaces "fused_rmsnorm_residual_forward (fused.py:28-46), then a
+ * separate MX quantisation pass".
+ *
+ *   dim       : a multiple of 32.
+ *   y_q       : [rows, dim] bytes (E4M3) or [rows, dim / 2] bytes (E2M1); ld_yq in bytes.
+ *   y_scales  : [rows, dim / 32] E8M0 bytes; ld_scales in bytes.
+ *   mx_format : VELOGRAD_MX_E4M3 or VELOGRAD_MX_E2M1.
+ * Other arguments as velograd_rmsnorm_residual_fwd.
+ */
+VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_mx(
+    const void* x, const void* residual, const void* weight,
+    uint8_t* y_q, uint8_t* y_scales, void* h, float* inv_rms,
+    int64_t rows, int64_t dim,
+    int64_t ld_x, int64_t ld_res, int64_t ld_yq, int64_t ld_scales, int64_t ld_h,
+    int32_t dtype, int32_t w_dtype, int32_t mx_format, float eps, void* hip_stream);
+
 /*
  * Backward of the forward above.
  * Replaces fused_rmsnorm_residual_backward (python/velograd/kernels/fused.py:48-66):

@@ -253,3 +253,100 @@ def fused_rope(x, k=None, head_dim: Optional[int] = None, base: float = 10000.0)
     if k is not None:                                                    # :46-48
         return q_rot, k_rot
     return q_rot
+
+
+# ---------------------------------------------------------------------------------------------
+# OCP Microscaling (MX) block quantisation of y: blocks of 32 consecutive elements of a row share
+# one E8M0 scale 2^s with s = floor(log2(amax)) - emax (8 for E4M3, 2 for E2M1), clamped to
+# [-127, 127]; elements are round-to-nearest-even, saturating codes of y / 2^s.  All-zero blocks
+# take scale code 0; blocks with a non-finite amax take the NaN scale 0xFF and zero codes.  The
+# reference's E2M1 table is include/velograd/kernels.h:47-51, its block decode :97-101, 339-347
+# (one scale per 32 elements, the even element in the low nibble).
+# ---------------------------------------------------------------------------------------------
+MX_BLOCK = 32
+MX_EMAX = {"e4m3": 8, "e2m1": 2}
+E2M1_VALUES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def e2m1_decode(nibbles: np.ndarray) -> np.ndarray:
+    """E2M1 nibble -> float32: (-1)^s * 2^(e-1) * (1 + m/2), subnormal 0.5 * m (bias 1)."""
+    n = np.asarray(nibbles).astype(np.int64) & 0xF
+    e = (n >> 1) & 3
+    m = n & 1
+    mag = np.where(e == 0, 0.5 * m, np.exp2(e - 1.0) * (1.0 + 0.5 * m))
+    return np.where((n >> 3) == 1, -mag, mag).astype(np.float32)
+
+
+def e2m1_encode(v: np.ndarray) -> np.ndarray:
+    """float32 -> E2M1 nibble: the nearest of the 8 magnitudes (ties to the even code),
+    saturating at 6; NaN -> 0.  A nearest-value search, not the device's comparison chain."""
+    v = np.asarray(v, dtype=np.float32)
+    with np.errstate(invalid="ignore"):
+        a = np.abs(v).astype(np.float64)
+    nan = np.isnan(a)
+    a = np.where(nan, 0.0, np.minimum(a, 6.0))
+    hi = np.clip(np.searchsorted(E2M1_VALUES, a, side="left"), 1, 7)
+    lo = hi - 1
+    d_lo, d_hi = a - E2M1_VALUES[lo], E2M1_VALUES[hi] - a
+    code = np.where(d_lo < d_hi, lo, np.where(d_hi < d_lo, hi, np.where(lo % 2 == 0, lo, hi)))
+    code = np.where(nan, 0, code)
+    return (code | (np.signbit(v).astype(np.int64) << 3)).astype(np.uint8)
+
+
+def e8m0_decode(codes: np.ndarray) -> np.ndarray:
+    """E8M0 scale code -> float64 2^(code - 127); 0xFF is NaN."""
+    c = np.asarray(codes).astype(np.int64)
+    return np.where(c == 0xFF, np.nan, np.exp2(c - 127.0))
+
+
+def mx_quantize_rows(y: np.ndarray, fmt: str):
+    """MX quantisation along the last axis (a multiple of 32).  Returns (codes, scales):
+    e4m3 codes [..., D] uint8; e2m1 nibbles packed two per byte [..., D/2] (even element in the
+    low nibble); scales [..., D/32] uint8 E8M0 codes."""
+    y = np.asarray(y, dtype=np.float32)
+    d = y.shape[-1]
+    assert d % MX_BLOCK == 0, "MX blocks need a last axis that is a multiple of 32"
+    blocks = y.reshape(y.shape[:-1] + (d // MX_BLOCK, MX_BLOCK))
+    with np.errstate(invalid="ignore"):
+        amax = np.max(np.abs(blocks), axis=-1)
+    finite = np.isfinite(amax)
+    pos = finite & (amax > 0)
+    _, ex = np.frexp(np.where(pos, amax, 1.0).astype(np.float64))  # amax = f * 2^ex, f in [.5,1)
+    s = np.where(pos, np.clip(ex - 1 - MX_EMAX[fmt], -127, 127), -127)
+    scales = np.where(finite, s + 127, 0xFF).astype(np.uint8)
+    factor = np.ldexp(np.float32(1.0), (-np.where(finite, s, 0)).astype(np.int32))[..., None]
+    with np.errstate(invalid="ignore", over="ignore"):
+        v = (blocks * factor.astype(np.float32)).astype(np.float32)
+    if fmt == "e4m3":
+        codes = e4m3fn_encode(v)
+    else:
+        codes = e2m1_encode(v)
+    codes = np.where(finite[..., None], codes, 0).astype(np.uint8).reshape(y.shape)
+    if fmt == "e2m1":
+        codes = (codes[..., 0::2] | (codes[..., 1::2] << 4)).astype(np.uint8)
+    return codes, scales
+
+
+def mx_dequantize_rows(codes: np.ndarray, scales: np.ndarray, fmt: str) -> np.ndarray:
+    """Inverse of mx_quantize_rows up to the element rounding (float64 values)."""
+    if fmt == "e2m1":
+        nib = np.stack([codes & 0xF, codes >> 4], axis=-1).reshape(codes.shape[:-1] + (-1,))
+        vals = e2m1_decode(nib).astype(np.float64)
+    else:
+        vals = e4m3fn_decode(codes).astype(np.float64)
+    sc = np.repeat(e8m0_decode(scales), MX_BLOCK, axis=-1)
+    return vals * sc
+
+
+def fused_rmsnorm_residual_forward_mx(x, residual=None, weight=None, eps: float = 1e-6,
+                                      fmt: str = "e4m3", inv_rms=None):
+    """fused.py:28-46 followed by mx_quantize_rows of y (given `inv_rms`, y is formed from it,
+    as in fused_rmsnorm_residual_forward_fp8).  Returns (codes, scales, h, inv_rms)."""
+    y, h, r = fused_rmsnorm_residual_forward(x, residual, weight, eps)
+    if inv_rms is not None:
+        r = np.asarray(inv_rms, dtype=h.dtype).reshape(r.shape)
+        y = h * r
+        if weight is not None:
+            y = y * weight
+    codes, scales = mx_quantize_rows(y, fmt)
+    return codes, scales, h, r

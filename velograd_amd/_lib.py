@@ -26,6 +26,9 @@ TORCH_DTYPE_CODES = {
     torch.bfloat16: DTYPE_BF16,
 }
 
+MX_E4M3 = 0
+MX_E2M1 = 1
+
 ERR_INVALID_ARGUMENT = -1
 ERR_UNSUPPORTED_DTYPE = -2
 ERR_WORKSPACE_TOO_SMALL = -3
@@ -56,6 +59,17 @@ SIGNATURES = {
          _c_i64, _c_i64, _c_i64, _c_i64,    # ld_x, ld_res, ld_y (bytes), ld_h
          _c_i32, _c_i32, ctypes.c_float,    # dtype, w_dtype, eps
          _c_ptr],                           # hip_stream
+    ),
+    "velograd_rmsnorm_residual_fwd_mx": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_ptr,            # x, residual, weight
+         _c_ptr, _c_ptr,                    # y_q, y_scales
+         _c_ptr, _c_ptr,                    # h, inv_rms
+         _c_i64, _c_i64,                    # rows, dim
+         _c_i64, _c_i64, _c_i64, _c_i64,    # ld_x, ld_res, ld_yq (bytes), ld_scales (bytes)
+         _c_i64,                            # ld_h
+         _c_i32, _c_i32, _c_i32,            # dtype, w_dtype, mx_format
+         ctypes.c_float, _c_ptr],           # eps, hip_stream
     ),
     "velograd_rmsnorm_residual_bwd": (
         _c_i32,

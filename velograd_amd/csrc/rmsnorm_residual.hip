@@ -23,6 +23,7 @@
 
 #include "common.h"
 #include "fp8_e4m3.h"
+#include "mx_formats.h"
 
 #define VG_VERSION_STRING "velograd_amd 0.1.0 fused-rmsnorm-residual gfx950"
 
@@ -131,6 +132,25 @@ __device__ inline uint32_t e4m3x1(float a) {
 #endif
 }
 
+// fp4 E2M1 nibbles on the device: gfx950's v_cvt_scalef32_pk_fp4_f32 converts two fp32 values
+// divided by a scale to E2M1, round to nearest even, saturating, the first value in the low
+// nibble of the selected byte (checked against the oracle's nearest-value encoder on every
+// midpoint and a dense sweep at scales 0.5..4).  The block factor 2^-s is applied by an exact
+// multiplication first and the instruction's scale is 1.  Build with -DVG_FP4_SOFT_ENCODE=1 to
+// use vg_mx::e2m1_encode (the comparison chain the CPU tests pin) instead.
+#ifndef VG_FP4_SOFT_ENCODE
+#define VG_FP4_SOFT_ENCODE 0
+#endif
+
+template <int SEL>
+__device__ inline uint32_t e2m1x2(uint32_t old, float a, float b) {
+#if VG_FP4_SOFT_ENCODE
+  return old | ((vg_mx::e2m1_encode(a) | (vg_mx::e2m1_encode(b) << 4)) << (8 * SEL));
+#else
+  return (uint32_t)__builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, a, b, 1.0f, SEL);
+#endif
+}
+
 // ------------------------------------------------------------------------------------------
 // Kernel arguments.
 // ------------------------------------------------------------------------------------------
@@ -142,6 +162,8 @@ struct FwdArgs {
   void* h;
   float* inv_rms;
   float* y_scale;   // fp8 epilogue: per-row dequantisation scale amax(|y|) / 448
+  uint8_t* mx_scale;  // MX epilogues: E8M0 scale codes, one per 32 elements of a row
+  int64_t ld_mx;      // row stride of mx_scale in bytes
   int64_t rows;
   int64_t ld_x, ld_res, ld_y, ld_h;
   int32_t dim;
@@ -165,13 +187,31 @@ struct BwdArgs {
   int32_t iters;  // rows visited per slot = ceil(rows / slots)
 };
 
+// Output modes of the forward kernels.
+constexpr int kOutDtype = 0;   // y in the activation dtype
+constexpr int kOutFp8Row = 1;  // y as e4m3 codes with one fp32 scale per row
+constexpr int kOutMxE4M3 = 2;  // MXFP8: e4m3 codes, one E8M0 scale per 32 elements
+constexpr int kOutMxE2M1 = 3;  // MXFP4: e2m1 nibbles (two per byte), one E8M0 scale per 32
+
+// Largest value over aligned groups of L lanes (L = 4 or 8), on every lane of the group.
+template <int L>
+__device__ inline uint32_t lane_group_max(uint32_t v) {
+  static_assert(L == 4 || L == 8, "MX blocks span 4 or 8 lanes");
+  v = umax(v, dpp_move_u32<0xB1>(v));     // quad_perm [1,0,3,2]
+  v = umax(v, dpp_move_u32<0x4E>(v));     // quad_perm [2,3,0,1]
+  if constexpr (L == 8) v = umax(v, dpp_move_u32<0x141>(v));  // row_half_mirror
+  return v;
+}
+
 // ------------------------------------------------------------------------------------------
 // Forward, register-resident row.
 // ------------------------------------------------------------------------------------------
-// Q8: the fp8 epilogue.  y is not stored in the activation dtype; a second row reduction finds
-// amax = max |y| over the row (fp32 y, before any rounding), the row's scale is amax / 448, and
-// y * (1 / scale) is stored as e4m3 codes: 8 bytes per bf16/fp16 chunk, 4 per fp32 chunk.
-template <int DT, int WDT, int NV, bool Q8>
+// OUT selects the epilogue.  kOutFp8Row: y is not stored in the activation dtype; a second row
+// reduction finds amax = max |y| over the row (fp32 y, before any rounding), the row's scale is
+// amax / 448, and y * (1 / scale) is stored as e4m3 codes: 8 bytes per bf16/fp16 chunk, 4 per
+// fp32 chunk.  kOutMxE4M3 / kOutMxE2M1: the 32 elements of an MX block are the chunks of 4
+// (bf16/fp16) or 8 (fp32) consecutive lanes, whose amax is reduced with DPP inside the group.
+template <int DT, int WDT, int NV, int OUT>
 __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const FwdArgs a) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
@@ -251,7 +291,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
     for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
   };
 
-  if constexpr (!Q8) {
+  if constexpr (OUT == kOutDtype) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = lt + k * tpr;
@@ -259,6 +299,58 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
         float yf[V];
         make_y(k, yf);
         store16_stream<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
+      }
+    }
+  } else if constexpr (OUT == kOutMxE4M3 || OUT == kOutMxE2M1) {
+    constexpr int kEmax = OUT == kOutMxE4M3 ? vg_mx::kEmaxE4M3 : vg_mx::kEmaxE2M1;
+    constexpr int kLanes = vg_mx::kBlock / V;  // lanes per MX block
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      float yf[V];
+      make_y(k, yf);
+      uint32_t am = 0;
+#pragma unroll
+      for (int i = 0; i < V; ++i) am = umax(am, __builtin_bit_cast(uint32_t, yf[i]) & 0x7fffffffu);
+      am = lane_group_max<kLanes>(am);  // every lane, before any divergence
+      if (row_ok && c < nchunk) {
+        const bool finite = am < 0x7f800000u;
+        const float f = finite ? vg_mx::inverse_scale(vg_mx::shared_exp(am, kEmax)) : 0.0f;
+        uint8_t* dst = static_cast<uint8_t*>(a.y) + row * a.ld_y;
+        if constexpr (OUT == kOutMxE4M3) {
+          uint32_t words[V / 4];
+#pragma unroll
+          for (int j = 0; j < V / 4; ++j) {
+            float q[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              q[t] = __builtin_fminf(__builtin_fmaxf(yf[4 * j + t] * f, -kE4M3Max), kE4M3Max);
+            words[j] = finite ? e4m3x4(q[0], q[1], q[2], q[3]) : 0u;
+          }
+          if constexpr (V == 8) {
+            const u32x2 w2 = {words[0], words[1]};
+            __builtin_nontemporal_store(w2, reinterpret_cast<u32x2*>(dst + (int64_t)c * V));
+          } else {
+            __builtin_nontemporal_store(words[0], reinterpret_cast<uint32_t*>(dst + (int64_t)c * V));
+          }
+        } else {
+          uint32_t word = 0;
+          word = e2m1x2<0>(word, yf[0] * f, yf[1] * f);
+          word = e2m1x2<1>(word, yf[2] * f, yf[3] * f);
+          if constexpr (V == 8) {
+            word = e2m1x2<2>(word, yf[4] * f, yf[5] * f);
+            word = e2m1x2<3>(word, yf[6] * f, yf[7] * f);
+          }
+          if (!finite) word = 0;
+          if constexpr (V == 8) {
+            __builtin_nontemporal_store(word, reinterpret_cast<uint32_t*>(dst + (int64_t)c * 4));
+          } else {
+            __builtin_nontemporal_store((uint16_t)word,
+                                        reinterpret_cast<uint16_t*>(dst + (int64_t)c * 2));
+          }
+        }
+        if (lt % kLanes == 0)
+          a.mx_scale[row * a.ld_mx + c / kLanes] = (uint8_t)vg_mx::scale_code(am, kEmax);
       }
     }
   } else {
@@ -306,7 +398,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 // Forward, any dim / alignment: one row per workgroup, two passes over the row (the second
 // re-reads x and residual, normally from L2, and recomputes the identical fp32 h).
 // ------------------------------------------------------------------------------------------
-template <int DT, int WDT, bool Q8>
+template <int DT, int WDT, int OUT>
 __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArgs a) {
   using C = Codec<DT>;
   using CW = Codec<WDT>;
@@ -334,8 +426,30 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
     const float n = hx * r;
     return has_w ? n * CW::load1(a.w, j) : n;
   };
-  if constexpr (!Q8) {
+  if constexpr (OUT == kOutDtype) {
     for (int j = threadIdx.x; j < a.dim; j += blockDim.x) C::store1(a.y, row * a.ld_y + j, y_at(j));
+  } else if constexpr (OUT == kOutMxE4M3 || OUT == kOutMxE2M1) {
+    // MX epilogue (see fwd_vec_kernel): a third pass, one 32-element block per thread.
+    constexpr int kEmax = OUT == kOutMxE4M3 ? vg_mx::kEmaxE4M3 : vg_mx::kEmaxE2M1;
+    uint8_t* yq = static_cast<uint8_t*>(a.y) + row * a.ld_y;
+    for (int b = threadIdx.x; b < a.dim / vg_mx::kBlock; b += blockDim.x) {
+      const int j0 = b * vg_mx::kBlock;
+      uint32_t am = 0;
+      for (int i = 0; i < vg_mx::kBlock; ++i)
+        am = umax(am, __builtin_bit_cast(uint32_t, y_at(j0 + i)) & 0x7fffffffu);
+      const bool finite = am < 0x7f800000u;
+      const float f = finite ? vg_mx::inverse_scale(vg_mx::shared_exp(am, kEmax)) : 0.0f;
+      for (int i = 0; i < vg_mx::kBlock; i += 2) {
+        const float v0 = y_at(j0 + i) * f, v1 = y_at(j0 + i + 1) * f;
+        if constexpr (OUT == kOutMxE4M3) {
+          yq[j0 + i] = finite ? (uint8_t)e4m3x1(__builtin_fminf(__builtin_fmaxf(v0, -kE4M3Max), kE4M3Max)) : 0;
+          yq[j0 + i + 1] = finite ? (uint8_t)e4m3x1(__builtin_fminf(__builtin_fmaxf(v1, -kE4M3Max), kE4M3Max)) : 0;
+        } else {
+          yq[(j0 + i) / 2] = finite ? (uint8_t)e2m1x2<0>(0u, v0, v1) : 0;
+        }
+      }
+      a.mx_scale[row * a.ld_mx + b] = (uint8_t)vg_mx::scale_code(am, kEmax);
+    }
   } else {
     // fp8 epilogue (see fwd_vec_kernel): a third pass stores the codes.
     __shared__ uint32_t red_max[kGenericBlock / kWave];
@@ -654,20 +768,20 @@ bool ld_ok(int64_t ld, int elem_bytes) { return ((ld * elem_bytes) & 15) == 0; }
 // ------------------------------------------------------------------------------------------
 // Typed launchers.
 // ------------------------------------------------------------------------------------------
-template <int DT, int WDT, bool Q8>
+template <int DT, int WDT, int OUT>
 void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
   if (!p.vec) {
-    hipLaunchKernelGGL((fwd_generic_kernel<DT, WDT, Q8>), dim3((uint32_t)a.rows), dim3(p.block),
+    hipLaunchKernelGGL((fwd_generic_kernel<DT, WDT, OUT>), dim3((uint32_t)a.rows), dim3(p.block),
                        0, st, a);
     return;
   }
   const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups));
   const dim3 block(p.block);
   switch (p.nv) {
-    case 1: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 1, Q8>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 2, Q8>), grid, block, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 3, Q8>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 4, Q8>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 1, OUT>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 2, OUT>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 3, OUT>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 4, OUT>), grid, block, 0, st, a); break;
   }
 }
 
@@ -731,13 +845,15 @@ size_t workspace_bytes_for(int64_t rows, int64_t dim, int cus) {
   return vg_plan::bwd_workspace_bytes(rows, dim, cus, t.bwd_nv, t.bwd_block, t.bwd_waves_per_cu);
 }
 
-// Shared by the forward entry points.  y_scale != nullptr selects the fp8 epilogue: y then
-// holds one e4m3 byte per element and ld_y counts bytes.
-int32_t run_fwd(const char* what, const void* x, const void* residual, const void* weight,
-                void* y, float* y_scale, void* h, float* inv_rms, int64_t rows, int64_t dim,
-                int64_t ld_x, int64_t ld_res, int64_t ld_y, int64_t ld_h, int32_t dtype,
-                int32_t w_dtype, float eps, void* hip_stream) {
-  const bool q8 = y_scale != nullptr;
+// Shared by the forward entry points.  `out` is the epilogue (kOut*): for kOutFp8Row y holds one
+// e4m3 byte per element and y_scale one fp32 per row; for the MX modes y holds e4m3 bytes or
+// e2m1 nibbles and mx_scale one E8M0 byte per 32 elements.  ld_y (and ld_mx) count bytes then.
+int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
+                const void* weight, void* y, float* y_scale, uint8_t* mx_scale, int64_t ld_mx,
+                void* h, float* inv_rms, int64_t rows, int64_t dim, int64_t ld_x,
+                int64_t ld_res, int64_t ld_y, int64_t ld_h, int32_t dtype, int32_t w_dtype,
+                float eps, void* hip_stream) {
+  const bool mx = out == kOutMxE4M3 || out == kOutMxE2M1;
   if (!types_ok(dtype, w_dtype))
     return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
                 "%s: unsupported dtype/w_dtype pair (%d, %d): weight must be the activation "
@@ -746,29 +862,47 @@ int32_t run_fwd(const char* what, const void* x, const void* residual, const voi
   if (rows < 0 || dim <= 0 || dim > INT32_MAX)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: invalid shape rows=%lld dim=%lld", what,
                 (long long)rows, (long long)dim);
+  if (mx && dim % vg_mx::kBlock != 0)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "%s: dim=%lld must be a multiple of the 32-element MX block", what,
+                (long long)dim);
   if (rows == 0) {
     clear_error();
     return 0;
   }
   if (x == nullptr || y == nullptr)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: x and y must not be NULL", what);
+  if (out == kOutFp8Row && y_scale == nullptr)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: y_scale must not be NULL", what);
+  if (mx && mx_scale == nullptr)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: scales must not be NULL", what);
   if (residual == nullptr) h = nullptr;  // h is x itself
-  if (ld_x < dim || ld_y < dim || (residual && ld_res < dim) || (h && ld_h < dim))
+  const int64_t y_row = out == kOutMxE2M1 ? dim / 2 : dim;  // y row length in its own units
+  if (ld_x < dim || ld_y < y_row || (residual && ld_res < dim) || (h && ld_h < dim) ||
+      (mx && ld_mx < dim / vg_mx::kBlock))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
-                "%s: row strides must be >= dim (ld_x=%lld ld_res=%lld ld_y=%lld ld_h=%lld)",
-                what, (long long)ld_x, (long long)ld_res, (long long)ld_y, (long long)ld_h);
+                "%s: row strides too small (ld_x=%lld ld_res=%lld ld_y=%lld ld_h=%lld "
+                "ld_scales=%lld for dim=%lld)",
+                what, (long long)ld_x, (long long)ld_res, (long long)ld_y, (long long)ld_h,
+                (long long)ld_mx, (long long)dim);
+  const void* extra_out = out == kOutFp8Row ? (const void*)y_scale : (const void*)mx_scale;
   if (y == x || y == residual || (h && (h == x || h == residual || h == y)) ||
-      (q8 && ((const void*)y_scale == x || (const void*)y_scale == residual ||
-              (void*)y_scale == y || (h && (void*)y_scale == h))))
+      (extra_out && (extra_out == x || extra_out == residual || extra_out == y ||
+                     (h && extra_out == h))))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: outputs must not alias inputs", what);
   if (rows > INT32_MAX)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: rows=%lld exceeds the grid limit", what,
                 (long long)rows);
 
   const int eb = elem_bytes_of(dtype);
-  // The fp8 output moves 16 / eb bytes per 16-byte input chunk.
-  const bool y_aligned = q8 ? (((uintptr_t)y % (uintptr_t)(16 / eb)) == 0 && ld_y % (16 / eb) == 0)
-                            : (aligned16(y) && ld_ok(ld_y, eb));
+  // Bytes of y per 16-byte input chunk: 16 (activation dtype), 16 / eb (e4m3), 8 / eb (e2m1).
+  bool y_aligned;
+  if (out == kOutDtype) {
+    y_aligned = aligned16(y) && ld_ok(ld_y, eb);
+  } else {
+    const int64_t cb = out == kOutMxE2M1 ? 8 / eb : 16 / eb;
+    y_aligned = ((uintptr_t)y % (uintptr_t)cb) == 0 && ld_y % cb == 0;
+  }
   const bool aligned = aligned16(x) && ld_ok(ld_x, eb) && y_aligned &&
                        (!residual || (aligned16(residual) && ld_ok(ld_res, eb))) &&
                        (!h || (aligned16(h) && ld_ok(ld_h, eb))) && (!weight || aligned16(weight));
@@ -785,6 +919,8 @@ int32_t run_fwd(const char* what, const void* x, const void* residual, const voi
   a.h = h;
   a.inv_rms = inv_rms;
   a.y_scale = y_scale;
+  a.mx_scale = mx_scale;
+  a.ld_mx = ld_mx;
   a.rows = rows;
   a.ld_x = ld_x;
   a.ld_res = ld_res;
@@ -794,11 +930,13 @@ int32_t run_fwd(const char* what, const void* x, const void* residual, const voi
   a.tpr = p.tpr;
   a.eps = eps;
   hipStream_t st = static_cast<hipStream_t>(hip_stream);
-  if (q8)
-    VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, true>(a, p, st)));
-  else
-    VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, false>(a, p, st)));
-  return check_launch(q8 ? "velograd_rmsnorm_residual_fwd_fp8" : "velograd_rmsnorm_residual_fwd");
+  switch (out) {
+    case kOutFp8Row: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutFp8Row>(a, p, st))); break;
+    case kOutMxE4M3: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutMxE4M3>(a, p, st))); break;
+    case kOutMxE2M1: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutMxE2M1>(a, p, st))); break;
+    default: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutDtype>(a, p, st))); break;
+  }
+  return check_launch(what);
 }
 
 }  // namespace
@@ -823,18 +961,32 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(const void* x, const void* re
                                                    int64_t ld_x, int64_t ld_res, int64_t ld_y,
                                                    int64_t ld_h, int32_t dtype, int32_t w_dtype,
                                                    float eps, void* hip_stream) {
-  return run_fwd("fwd", x, residual, weight, y, nullptr, h, inv_rms, rows, dim, ld_x, ld_res,
-                 ld_y, ld_h, dtype, w_dtype, eps, hip_stream);
+  return run_fwd("velograd_rmsnorm_residual_fwd", kOutDtype, x, residual, weight, y, nullptr,
+                 nullptr, 0, h, inv_rms, rows, dim, ld_x, ld_res, ld_y, ld_h, dtype, w_dtype,
+                 eps, hip_stream);
 }
 
 VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_fp8(
     const void* x, const void* residual, const void* weight, uint8_t* y_fp8, float* y_scale,
     void* h, float* inv_rms, int64_t rows, int64_t dim, int64_t ld_x, int64_t ld_res,
     int64_t ld_y, int64_t ld_h, int32_t dtype, int32_t w_dtype, float eps, void* hip_stream) {
-  if (rows > 0 && y_scale == nullptr)
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "fwd_fp8: y_scale must not be NULL");
-  return run_fwd("fwd_fp8", x, residual, weight, y_fp8, y_scale, h, inv_rms, rows, dim, ld_x,
-                 ld_res, ld_y, ld_h, dtype, w_dtype, eps, hip_stream);
+  return run_fwd("velograd_rmsnorm_residual_fwd_fp8", kOutFp8Row, x, residual, weight, y_fp8,
+                 y_scale, nullptr, 0, h, inv_rms, rows, dim, ld_x, ld_res, ld_y, ld_h, dtype,
+                 w_dtype, eps, hip_stream);
+}
+
+VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_mx(
+    const void* x, const void* residual, const void* weight, uint8_t* y_q, uint8_t* y_scales,
+    void* h, float* inv_rms, int64_t rows, int64_t dim, int64_t ld_x, int64_t ld_res,
+    int64_t ld_yq, int64_t ld_scales, int64_t ld_h, int32_t dtype, int32_t w_dtype,
+    int32_t mx_format, float eps, void* hip_stream) {
+  if (mx_format != VELOGRAD_MX_E4M3 && mx_format != VELOGRAD_MX_E2M1)
+    return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
+                "velograd_rmsnorm_residual_fwd_mx: unsupported mx_format %d", (int)mx_format);
+  return run_fwd("velograd_rmsnorm_residual_fwd_mx",
+                 mx_format == VELOGRAD_MX_E4M3 ? kOutMxE4M3 : kOutMxE2M1, x, residual, weight,
+                 y_q, nullptr, y_scales, ld_scales, h, inv_rms, rows, dim, ld_x, ld_res, ld_yq,
+                 ld_h, dtype, w_dtype, eps, hip_stream);
 }
 
 VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(

@@ -29,7 +29,8 @@ Additions (keyword-only, off by default): `saved_is_h=True` lets the backward ta
 xhat (xhat is then formed in registers; same bytes moved), `dresidual_out=` receives a second
 copy of grad_x in a caller-owned buffer, and `grad_h=` adds the residual-stream gradient (the
 gradient reaching h from the next residual add) to grad_x in the same pass.
-`fused_rmsnorm_residual_forward_fp8` returns y as fp8 E4M3 codes with one scale per row.
+`fused_rmsnorm_residual_forward_fp8` returns y as fp8 E4M3 codes with one scale per row, and
+`fused_rmsnorm_residual_forward_mx` as MXFP8 / MXFP4 blocks (one E8M0 scale per 32 elements).
 """
 
 from __future__ import annotations
@@ -47,6 +48,7 @@ __all__ = [
     "fused_rmsnorm_residual_forward",
     "fused_rmsnorm_residual_backward",
     "fused_rmsnorm_residual_forward_fp8",
+    "fused_rmsnorm_residual_forward_mx",
     "fused_rope",
     "fused_rope_forward",
     "fused_rope_backward",
@@ -175,8 +177,9 @@ def _forward_fast(x: torch.Tensor, residual: Optional[torch.Tensor],
 
 
 def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
-                    weight: Optional[torch.Tensor], eps: float, fp8: bool = False):
-    if not fp8:
+                    weight: Optional[torch.Tensor], eps: float, fp8: bool = False,
+                    mx: Optional[str] = None):
+    if not fp8 and mx is None:
         fast = _forward_fast(x, residual, weight, eps)
         if fast is not None:
             return fast
@@ -198,16 +201,25 @@ def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
 
     x2 = _rows_view(x, "x")
     rows = x2.shape[0]
-    # fp8 codes are allocated as bytes and handed back viewed as float8_e4m3fn
-    y = torch.empty(out_shape, dtype=torch.uint8 if fp8 else x.dtype, device=device)
+    if mx is not None and d % 32 != 0:
+        raise ValueError(f"MX blocks need a last dimension that is a multiple of 32, got {d}")
+    # fp8 / MX codes are allocated as bytes and handed back viewed as their torch dtypes
+    y_last = d // 2 if mx == "e2m1" else d
+    y = torch.empty(tuple(out_shape[:-1]) + (y_last,),
+                    dtype=torch.uint8 if (fp8 or mx) else x.dtype, device=device)
     h = torch.empty(out_shape, dtype=x.dtype, device=device) if residual is not None else x
     stat_shape = tuple(out_shape[:-1]) + (1,)
     inv_rms = torch.empty(stat_shape, dtype=torch.float32, device=device)
     y_scale = torch.empty(stat_shape, dtype=torch.float32, device=device) if fp8 else None
+    mx_scale = (torch.empty(tuple(out_shape[:-1]) + (d // 32,), dtype=torch.uint8, device=device)
+                if mx is not None else None)
 
     def result():
         if fp8:
             return y.view(torch.float8_e4m3fn), y_scale, h, inv_rms
+        if mx is not None:
+            yq = y.view(torch.float8_e4m3fn) if mx == "e4m3" else y.view(torch.float4_e2m1fn_x2)
+            return yq, mx_scale.view(torch.float8_e8m0fnu), h, inv_rms
         return y, h, inv_rms
 
     if rows == 0:
@@ -217,6 +229,20 @@ def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
         inv_rms.fill_(float("nan"))
         if fp8:
             y_scale.fill_(float("nan"))
+        return result()
+    if mx is not None:
+        r2 = _rows_view(residual, "residual") if residual is not None else None
+        y2 = y.view(-1, y_last)
+        h2 = h.view(-1, d) if residual is not None else None
+        with torch.cuda.device(device):
+            rc = lib.velograd_rmsnorm_residual_fwd_mx(
+                x2.data_ptr(), _ptr(r2), _ptr(w),
+                y2.data_ptr(), mx_scale.data_ptr(), _ptr(h2), inv_rms.data_ptr(),
+                rows, d,
+                _ld(x2), _ld(r2) if r2 is not None else d, y_last, d // 32, d,
+                code, wcode, _lib.MX_E4M3 if mx == "e4m3" else _lib.MX_E2M1, float(eps),
+                _stream(device))
+        _lib.check(rc, "velograd_rmsnorm_residual_fwd_mx")
         return result()
 
     r2 = _rows_view(residual, "residual") if residual is not None else None
@@ -517,6 +543,25 @@ def fused_rope(x: Any, k: Optional[Any] = None, head_dim: Optional[int] = None,
     if k is not None:
         return q_rot, k_rot
     return q_rot
+
+
+def fused_rmsnorm_residual_forward_mx(x: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                                      weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                                      fmt: str = "e4m3"):
+    """The forward with y quantised to an OCP MX block format, in the same pass.
+
+    fmt "e4m3" (MXFP8) or "e2m1" (MXFP4).  Returns (y_q, y_scales, h, inv_rms): y_q is a
+    float8_e4m3fn tensor shaped like x, or float4_e2m1fn_x2 with the last dimension halved (two
+    elements per byte, the even one in the low nibble); y_scales is float8_e8m0fnu [..., D/32],
+    one power-of-two scale per 32 consecutive elements of a row (2^(floor(log2(amax)) - emax)).
+    D must be a multiple of 32.  Device tensors only; the element formats are the reference's
+    (include/velograd/kernels.h:29-37, 47-51).
+    """
+    if not _is_device_tensor(x):
+        raise TypeError("fused_rmsnorm_residual_forward_mx takes torch tensors on a ROCm device")
+    if fmt not in ("e4m3", "e2m1"):
+        raise ValueError(f"fmt must be 'e4m3' or 'e2m1', got {fmt!r}")
+    return _forward_device(x, residual, weight, eps, mx=fmt)
 
 
 def fused_rmsnorm_residual(x: Any, residual: Optional[Any] = None, weight: Optional[Any] = None,
