@@ -179,3 +179,30 @@ def test_rope_argument_errors(lib, kw, code, msg):
 def test_rope_empty_is_a_no_op(lib):
     assert _rope(lib, seq=0, x=None, out=None) == 0
     assert _lib.last_error() == ""
+
+
+def _fwd_mx(lib, **kw):
+    args = dict(x=16, residual=None, weight=None, y=32, scales=112, h=None, inv_rms=None,
+                rows=4, dim=64, ld_x=64, ld_res=64, ld_y=64, ld_s=2, ld_h=64, dtype=2,
+                w_dtype=2, fmt=0, eps=1e-5, stream=None)
+    args.update(kw)
+    return lib.velograd_rmsnorm_residual_fwd_mx(*args.values())
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(fmt=2), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported mx_format"),
+    (dict(dtype=9), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    (dict(dim=48, ld_x=48, ld_y=48, ld_h=48), _lib.ERR_INVALID_ARGUMENT, "multiple of the 32"),
+    (dict(scales=None), _lib.ERR_INVALID_ARGUMENT, "scales must not be NULL"),
+    (dict(ld_s=1), _lib.ERR_INVALID_ARGUMENT, "row strides"),
+    (dict(fmt=1, ld_y=31), _lib.ERR_INVALID_ARGUMENT, "row strides"),
+    (dict(scales=16), _lib.ERR_INVALID_ARGUMENT, "alias"),
+])
+def test_fwd_mx_argument_errors(lib, kw, code, msg):
+    assert _fwd_mx(lib, **kw) == code
+    assert msg in _lib.last_error() and "fwd_mx" in _lib.last_error()
+
+
+def test_fwd_mx_e2m1_accepts_half_width_rows(lib):
+    # rows = 0 returns before any launch; the e2m1 row stride is dim / 2 bytes
+    assert _fwd_mx(lib, fmt=1, ld_y=32, rows=0) == 0
