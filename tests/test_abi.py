@@ -206,3 +206,26 @@ def test_fwd_mx_argument_errors(lib, kw, code, msg):
 def test_fwd_mx_e2m1_accepts_half_width_rows(lib):
     # rows = 0 returns before any launch; the e2m1 row stride is dim / 2 bytes
     assert _fwd_mx(lib, fmt=1, ld_y=32, rows=0) == 0
+
+
+def test_last_error_is_per_thread(lib):
+    """The error text lives in thread-local storage: a failing call on one thread does not
+    overwrite what another thread reads."""
+    import threading
+
+    seen = {}
+
+    def worker(name, kw):
+        rc = _fwd(lib, **kw)
+        seen[name] = (rc, _lib.last_error())
+
+    t1 = threading.Thread(target=worker, args=("a", dict(dtype=7)))
+    t1.start()
+    t1.join()
+    t2 = threading.Thread(target=worker, args=("b", dict(dim=0)))
+    t2.start()
+    t2.join()
+    assert seen["a"][0] == _lib.ERR_UNSUPPORTED_DTYPE and "unsupported dtype" in seen["a"][1]
+    assert seen["b"][0] == _lib.ERR_INVALID_ARGUMENT and "invalid shape" in seen["b"][1]
+    # this thread's own last error is untouched by the workers
+    assert _fwd(lib, rows=0, x=None, y=None) == 0 and _lib.last_error() == ""

@@ -50,3 +50,42 @@ def test_graph_replays_match_eager(dtype, rows, d):
         torch.cuda.synchronize()
         for name, got, want in zip(("y", "h", "inv_rms", "dx", "dweight"), outs, ref):
             assert torch.equal(got, want), f"replay {rep}: {name} differs from the eager call"
+
+
+def test_graph_replays_of_quantised_forwards_and_rope_match_eager():
+    """fp8, MXFP8, MXFP4 forwards and RoPE captured together, replayed with new inputs."""
+    torch.manual_seed(1)
+    dev = torch.device("cuda", 0)
+    rows, d = 300, 2048
+    x = torch.randn(rows, d, device=dev, dtype=torch.bfloat16)
+    r = torch.randn(rows, d, device=dev, dtype=torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(d, device=dev)).to(torch.bfloat16)
+    q = torch.randn(2, 64, 8, 128, device=dev, dtype=torch.bfloat16)
+
+    def calls():
+        out = list(vk.fused_rmsnorm_residual_forward_fp8(x, r, w, 1e-5))
+        out += list(vk.fused_rmsnorm_residual_forward_mx(x, r, w, 1e-5, fmt="e4m3"))
+        out += list(vk.fused_rmsnorm_residual_forward_mx(x, r, w, 1e-5, fmt="e2m1"))
+        out.append(vk.fused_rope_forward(q)[0])
+        return [t.view(torch.uint8) if t.element_size() == 1 else t for t in out]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            calls()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = calls()
+    for rep in range(3):
+        for t in (x, r, q):
+            t.copy_(torch.randn(t.shape, device=dev, dtype=t.dtype))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ref = calls()
+        torch.cuda.synchronize()
+        for i, (got, want) in enumerate(zip(outs, ref)):
+            assert torch.equal(got, want), f"replay {rep}: output {i} differs from the eager call"
