@@ -54,6 +54,21 @@ def test_golden_vectors_fp32(case):
     assert (dw is None and dw2 is None) or torch.equal(dw, dw2)
 
 
+def test_reference_wrapper_call_of_test_exhaustive():
+    """The reference suite's only call on this path (tests/test_exhaustive.py:116-123):
+    fused_rmsnorm_residual(randn(4,16), randn(4,16), randn(16), eps=1e-5), there checked for its
+    shape only; here with NumPy inputs (a float32 ndarray comes back, computed on the GPU) and
+    against the oracle's values."""
+    rng = np.random.default_rng(116)
+    x, res, w = (P.gaussian(rng, s) for s in ((4, 16), (4, 16), (16,)))
+    out = vk.fused_rmsnorm_residual(x, res, w, eps=1e-5)
+    assert isinstance(out, np.ndarray) and out.dtype == np.float32 and out.shape == (4, 16)
+    assert P.rel_err(out, ora.fused_rmsnorm_residual(x, res, w, eps=1e-5)) <= P.FP32_REL_TOL
+    # lists are accepted as the wrapper's np.asarray accepts them (kernels/__init__.py:21-27)
+    out_l = vk.fused_rmsnorm_residual(x.tolist(), res.tolist(), w.tolist(), eps=1e-5)
+    assert np.array_equal(out_l, out)
+
+
 def test_known_answer_of_reference_rust_test():
     x = torch.tensor([[1.0, 2.0, 3.0, 4.0]], device="cuda")
     y = vk.fused_rmsnorm_residual(x, None, torch.ones(4, device="cuda"), eps=1e-5)
