@@ -29,6 +29,13 @@ stated tolerances make unnecessary.
 Beyond the reference's RMSNorm functions (pins in tests/test_fp8_codec.py and
 tests/test_rope_oracle.py):
   * backward_with_residual_grad: torch autograd of the pre-norm block (tests/test_oracle.py);
+  * rmsnorm_module_forward / rmsnorm_module_backward (the reference module velograd.nn.RMSNorm,
+    python/velograd/nn.py:338-383, with its 1e-12 floor on the mean square;
+    tests/test_rmsnorm_module_oracle.py): the reference test's own ground-truth loop
+    (tests/test_velograd_v41_enterprise_verification.py:221-229), the Rust known answer, torch's
+    rms_norm and autograd where the floor is inactive, closed forms where it is active (eps = 0
+    zero and tiny rows, the boundary), Python's max on NaN and Inf, and the reference's gradcheck
+    rule on its own input;
   * e4m3fn_decode / e4m3fn_encode / quantize_rows_e4m3 / fused_rmsnorm_residual_forward_fp8
     (the fp8 output epilogue, format of include/velograd/kernels.h:29-37,58-73): torch's
     float8_e4m3fn casts over every code and a dense set of values, the reference decoder's
@@ -101,6 +108,47 @@ def fused_rmsnorm_residual(x, residual=None, weight=None, eps: float = 1e-6) -> 
     w_arr = None if weight is None else np.asarray(weight, dtype=np.float32)   # :25-27
     normed, _, _ = fused_rmsnorm_residual_forward(x_arr, res_arr, w_arr, eps)   # :29
     return normed                                                               # :32
+
+
+# ---------------------------------------------------------------------------------------------
+# The reference's module `velograd.nn.RMSNorm` (python/velograd/nn.py:328-389): residual-free,
+# mean square floored at 1e-12, computed in Python floats (float64), row by row.
+# ---------------------------------------------------------------------------------------------
+MODULE_MIN_MEAN_SQ = 1e-12                                                      # nn.py:349
+
+
+def rmsnorm_module_forward(x, weight=None, eps: float = 1e-6,
+                           min_mean_sq: float = MODULE_MIN_MEAN_SQ):
+    """nn.py:338-355 in float64: returns (y, inv_rms [..., 1])."""
+    x = np.asarray(x, dtype=np.float64)
+    dim = x.shape[-1]
+    # nn.py:349 sum(x ** 2 for x in row) / dim, summed left to right (cumsum is sequential)
+    mean_sq = np.cumsum(x ** 2, axis=-1)[..., -1:] / dim
+    # nn.py:349 max(1e-12, mean_sq): Python's max keeps its first argument unless a later one
+    # compares greater, so a NaN mean square becomes the floor
+    mean_sq = np.where(mean_sq > min_mean_sq, mean_sq, min_mean_sq)
+    rms = np.sqrt(mean_sq + eps)                                                # nn.py:350
+    inv_rms = 1.0 / rms                                                         # nn.py:351
+    y = x * inv_rms                                                             # nn.py:355
+    if weight is not None:
+        y = y * np.asarray(weight, dtype=np.float64).reshape(-1)
+    return y, inv_rms
+
+
+def rmsnorm_module_backward(grad, x, weight, inv_rms):
+    """nn.py:357-383 in float64: returns (grad_x, grad_weight [dim] or None)."""
+    g = np.asarray(grad, dtype=np.float64)
+    x = np.asarray(x, dtype=np.float64)
+    inv = np.asarray(inv_rms, dtype=np.float64)
+    dim = x.shape[-1]
+    w = np.ones(dim) if weight is None else np.asarray(weight, dtype=np.float64).reshape(-1)
+    grad_w = None
+    if weight is not None:                                                      # nn.py:361-367
+        grad_w = np.sum((g * x * inv).reshape(-1, dim), axis=0)
+    sum_dy_w_x = np.sum(g * w * x, axis=-1, keepdims=True)                      # nn.py:376-378
+    dy_w = g * w                                                                # nn.py:381
+    grad_x = inv * (dy_w - x * (inv ** 2) * sum_dy_w_x / dim)                   # nn.py:382
+    return grad_x, grad_w
 
 
 # ---------------------------------------------------------------------------------------------

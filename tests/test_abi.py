@@ -86,6 +86,33 @@ def test_fwd_zero_rows_is_a_no_op(lib):
     assert _lib.last_error() == ""
 
 
+def _rmsnorm_fwd(lib, **kw):
+    args = dict(x=16, weight=None, y=32, inv_rms=None, rows=4, dim=64, ld_x=64, ld_y=64,
+                dtype=2, w_dtype=2, eps=1e-6, min_mean_sq=1e-12, stream=None)
+    args.update(kw)
+    return lib.velograd_rmsnorm_fwd(*args.values())
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(min_mean_sq=-1e-12), _lib.ERR_INVALID_ARGUMENT, "min_mean_sq"),
+    (dict(min_mean_sq=float("nan")), _lib.ERR_INVALID_ARGUMENT, "min_mean_sq"),
+    (dict(min_mean_sq=float("inf")), _lib.ERR_INVALID_ARGUMENT, "min_mean_sq"),
+    (dict(dtype=7), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    (dict(dim=0), _lib.ERR_INVALID_ARGUMENT, "invalid shape"),
+    (dict(x=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(ld_y=63), _lib.ERR_INVALID_ARGUMENT, "row strides"),
+    (dict(y=16), _lib.ERR_INVALID_ARGUMENT, "alias"),
+])
+def test_rmsnorm_fwd_argument_errors(lib, kw, code, msg):
+    assert _rmsnorm_fwd(lib, **kw) == code
+    assert msg in _lib.last_error() and "velograd_rmsnorm_fwd" in _lib.last_error()
+
+
+def test_rmsnorm_fwd_zero_rows_is_a_no_op(lib):
+    assert _rmsnorm_fwd(lib, rows=0, x=None, y=None) == 0
+    assert _lib.last_error() == ""
+
+
 def _fwd_fp8(lib, **kw):
     args = dict(x=16, residual=None, weight=None, y=32, y_scale=112, h=None, inv_rms=None,
                 rows=4, dim=64, ld_x=64, ld_res=64, ld_y=64, ld_h=64, dtype=2, w_dtype=2,

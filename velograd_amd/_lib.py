@@ -50,6 +50,14 @@ SIGNATURES = {
          _c_i32, _c_i32, ctypes.c_float,    # dtype, w_dtype, eps
          _c_ptr],                           # hip_stream
     ),
+    "velograd_rmsnorm_fwd": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr,    # x, weight, y, inv_rms
+         _c_i64, _c_i64, _c_i64, _c_i64,    # rows, dim, ld_x, ld_y
+         _c_i32, _c_i32,                    # dtype, w_dtype
+         ctypes.c_float, ctypes.c_float,    # eps, min_mean_sq
+         _c_ptr],                           # hip_stream
+    ),
     "velograd_rmsnorm_residual_fwd_fp8": (
         _c_i32,
         [_c_ptr, _c_ptr, _c_ptr,            # x, residual, weight

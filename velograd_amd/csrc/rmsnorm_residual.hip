@@ -2,6 +2,8 @@
 //
 // Math (reference: python/velograd/kernels/fused.py:28-66):
 //   forward   h = x + residual;  inv_rms = 1 / sqrt(mean(h^2) + eps);  y = (h * inv_rms) * w
+//             (the residual-free module form, python/velograd/nn.py:338-355, first floors
+//             mean(h^2) at a minimum: see floor_mean_sq)
 //   backward  gw = g * w;  m = mean(gw * xhat);  dx = inv_rms * (gw - xhat * m)
 //             dweight = sum over rows of g * xhat,  with xhat = h * inv_rms
 // Every operation is fp32 and rounds where the NumPy reference rounds (this file is built with
@@ -151,6 +153,14 @@ __device__ inline uint32_t e2m1x2(uint32_t old, float a, float b) {
 #endif
 }
 
+// The reference module's `mean_sq = max(1e-12, sum(x ** 2) / dim)` (python/velograd/nn.py:349),
+// for a floor given > 0.  Python's max keeps its first argument unless the second compares
+// greater, so a NaN mean square becomes the floor there, and here.  floor == 0 (the fused
+// functions, which have no clamp, fused.py:41-42) leaves mean_sq untouched, NaN included.
+__device__ __forceinline__ float floor_mean_sq(float mean_sq, float floor) {
+  return (floor > 0.0f && !(mean_sq > floor)) ? floor : mean_sq;
+}
+
 // ------------------------------------------------------------------------------------------
 // Kernel arguments.
 // ------------------------------------------------------------------------------------------
@@ -169,6 +179,7 @@ struct FwdArgs {
   int32_t dim;
   int32_t tpr;
   float eps;
+  float ms_floor;   // > 0: floor on mean(h^2) before eps (the reference module's clamp)
 };
 
 struct BwdArgs {
@@ -272,7 +283,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
   }
 
   ss = row_sum(ss, tpr, grp, red);
-  const float mean_sq = ss / (float)a.dim;
+  const float mean_sq = floor_mean_sq(ss / (float)a.dim, a.ms_floor);
   const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
   if (row_ok && lt == 0 && a.inv_rms != nullptr) a.inv_rms[row] = r;
 
@@ -416,7 +427,7 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
     ss += hx * hx;
   }
   ss = row_sum(ss, blockDim.x, 0, red);
-  const float mean_sq = ss / (float)a.dim;
+  const float mean_sq = floor_mean_sq(ss / (float)a.dim, a.ms_floor);
   const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
   if (threadIdx.x == 0 && a.inv_rms != nullptr) a.inv_rms[row] = r;
 
@@ -852,7 +863,7 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
                 const void* weight, void* y, float* y_scale, uint8_t* mx_scale, int64_t ld_mx,
                 void* h, float* inv_rms, int64_t rows, int64_t dim, int64_t ld_x,
                 int64_t ld_res, int64_t ld_y, int64_t ld_h, int32_t dtype, int32_t w_dtype,
-                float eps, void* hip_stream) {
+                float eps, float ms_floor, void* hip_stream) {
   const bool mx = out == kOutMxE4M3 || out == kOutMxE2M1;
   if (!types_ok(dtype, w_dtype))
     return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
@@ -862,6 +873,9 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
   if (rows < 0 || dim <= 0 || dim > INT32_MAX)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: invalid shape rows=%lld dim=%lld", what,
                 (long long)rows, (long long)dim);
+  if (!(ms_floor >= 0.0f) || !__builtin_isfinite(ms_floor))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "%s: min_mean_sq=%g must be finite and >= 0", what, (double)ms_floor);
   if (mx && dim % vg_mx::kBlock != 0)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
                 "%s: dim=%lld must be a multiple of the 32-element MX block", what,
@@ -929,6 +943,7 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
   a.dim = (int32_t)dim;
   a.tpr = p.tpr;
   a.eps = eps;
+  a.ms_floor = ms_floor;
   hipStream_t st = static_cast<hipStream_t>(hip_stream);
   switch (out) {
     case kOutFp8Row: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutFp8Row>(a, p, st))); break;
@@ -963,7 +978,17 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(const void* x, const void* re
                                                    float eps, void* hip_stream) {
   return run_fwd("velograd_rmsnorm_residual_fwd", kOutDtype, x, residual, weight, y, nullptr,
                  nullptr, 0, h, inv_rms, rows, dim, ld_x, ld_res, ld_y, ld_h, dtype, w_dtype,
-                 eps, hip_stream);
+                 eps, 0.0f, hip_stream);
+}
+
+VELOGRAD_API int32_t velograd_rmsnorm_fwd(const void* x, const void* weight, void* y,
+                                          float* inv_rms, int64_t rows, int64_t dim,
+                                          int64_t ld_x, int64_t ld_y, int32_t dtype,
+                                          int32_t w_dtype, float eps, float min_mean_sq,
+                                          void* hip_stream) {
+  return run_fwd("velograd_rmsnorm_fwd", kOutDtype, x, nullptr, weight, y, nullptr, nullptr, 0,
+                 nullptr, inv_rms, rows, dim, ld_x, dim, ld_y, dim, dtype, w_dtype, eps,
+                 min_mean_sq, hip_stream);
 }
 
 VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_fp8(
@@ -972,7 +997,7 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_fp8(
     int64_t ld_y, int64_t ld_h, int32_t dtype, int32_t w_dtype, float eps, void* hip_stream) {
   return run_fwd("velograd_rmsnorm_residual_fwd_fp8", kOutFp8Row, x, residual, weight, y_fp8,
                  y_scale, nullptr, 0, h, inv_rms, rows, dim, ld_x, ld_res, ld_y, ld_h, dtype,
-                 w_dtype, eps, hip_stream);
+                 w_dtype, eps, 0.0f, hip_stream);
 }
 
 VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_mx(
@@ -986,7 +1011,7 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_mx(
   return run_fwd("velograd_rmsnorm_residual_fwd_mx",
                  mx_format == VELOGRAD_MX_E4M3 ? kOutMxE4M3 : kOutMxE2M1, x, residual, weight,
                  y_q, nullptr, y_scales, ld_scales, h, inv_rms, rows, dim, ld_x, ld_res, ld_yq,
-                 ld_h, dtype, w_dtype, eps, hip_stream);
+                 ld_h, dtype, w_dtype, eps, 0.0f, hip_stream);
 }
 
 VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(

@@ -31,6 +31,8 @@ copy of grad_x in a caller-owned buffer, and `grad_h=` adds the residual-stream 
 gradient reaching h from the next residual add) to grad_x in the same pass.
 `fused_rmsnorm_residual_forward_fp8` returns y as fp8 E4M3 codes with one scale per row, and
 `fused_rmsnorm_residual_forward_mx` as MXFP8 / MXFP4 blocks (one E8M0 scale per 32 elements).
+`rmsnorm_forward` is the residual-free form of the reference's module (nn.py:338-355), with its
+floor on the mean square.
 """
 
 from __future__ import annotations
@@ -49,6 +51,7 @@ __all__ = [
     "fused_rmsnorm_residual_backward",
     "fused_rmsnorm_residual_forward_fp8",
     "fused_rmsnorm_residual_forward_mx",
+    "rmsnorm_forward",
     "fused_rope",
     "fused_rope_forward",
     "fused_rope_backward",
@@ -411,8 +414,9 @@ def fused_rmsnorm_residual_forward_fp8(x: torch.Tensor, residual: Optional[torch
     Returns (y_fp8, y_scale, h, inv_rms): y_fp8 is a float8_e4m3fn tensor shaped like x,
     y_scale ([..., 1], float32) is amax(|y|) / 448 per row, the codes are e4m3(y * (1 /
     y_scale)), and y ~= y_fp8.float() * y_scale; h and inv_rms as
-    fused_rmsnorm_residual_forward.  Rounding is to nearest even, saturating at +-448.  Device tensors only (an extension: the reference has no quantising forward; its
-    E4M3 format is include/velograd/kernels.h:29-37, 58-73).
+    fused_rmsnorm_residual_forward.  Rounding is to nearest even, saturating at +-448.
+    Device tensors only (an extension: the reference has no quantising forward; its E4M3
+    format is include/velograd/kernels.h:29-37, 58-73).
     """
     if not _is_device_tensor(x):
         raise TypeError("fused_rmsnorm_residual_forward_fp8 takes torch tensors on a ROCm device")
@@ -562,6 +566,43 @@ def fused_rmsnorm_residual_forward_mx(x: torch.Tensor, residual: Optional[torch.
     if fmt not in ("e4m3", "e2m1"):
         raise ValueError(f"fmt must be 'e4m3' or 'e2m1', got {fmt!r}")
     return _forward_device(x, residual, weight, eps, mx=fmt)
+
+
+def rmsnorm_forward(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                    min_mean_sq: float = 1e-12) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Residual-free RMSNorm as the reference module computes it (python/velograd/nn.py:338-355).
+
+    mean_sq = max(min_mean_sq, mean(x^2)) per row (the reference floors at 1e-12, nn.py:349; as
+    Python's max does, a NaN mean square becomes the floor), inv_rms = 1 / sqrt(mean_sq + eps),
+    y = x * inv_rms * weight.  Returns (y, inv_rms) with y in x's dtype and inv_rms float32
+    [..., 1].  min_mean_sq = 0 is fused_rmsnorm_residual_forward without a residual.  Device
+    tensors only; the module's backward is fused_rmsnorm_residual_backward(g, x, weight,
+    inv_rms, saved_is_h=True).
+    """
+    if not _is_device_tensor(x):
+        raise TypeError("rmsnorm_forward takes torch tensors on a ROCm device")
+    min_mean_sq = float(min_mean_sq)
+    if not (math.isfinite(min_mean_sq) and min_mean_sq >= 0.0):
+        raise ValueError(f"min_mean_sq must be finite and >= 0, got {min_mean_sq}")
+    lib = _lib.load()
+    device = x.device
+    code = _dtype_code(x, "x")
+    if x.dim() == 0 or x.shape[-1] == 0:
+        raise ValueError("rmsnorm_forward needs a non-empty last dimension")
+    d = x.shape[-1]
+    w, wcode = _prep_weight(weight, d, x.dtype, device)
+    x2 = _rows_view(x, "x")
+    rows = x2.shape[0]
+    y = torch.empty(x.shape, dtype=x.dtype, device=device)
+    inv_rms = torch.empty(tuple(x.shape[:-1]) + (1,), dtype=torch.float32, device=device)
+    if rows == 0:
+        return y, inv_rms
+    with torch.cuda.device(device):
+        rc = lib.velograd_rmsnorm_fwd(x2.data_ptr(), _ptr(w), y.data_ptr(), inv_rms.data_ptr(),
+                                      rows, d, _ld(x2), d, code, wcode, float(eps), min_mean_sq,
+                                      _stream(device))
+    _lib.check(rc, "velograd_rmsnorm_fwd")
+    return y, inv_rms
 
 
 def fused_rmsnorm_residual(x: Any, residual: Optional[Any] = None, weight: Optional[Any] = None,

@@ -8,10 +8,10 @@ gradient function (python/velograd/kernels/__init__.py:30-31).  Here:
   `(h, inv_rms)`; backward runs the fused backward once, adding the gradient that reaches `h`
   from its other consumer (the next residual add) in the same pass, and returns
   dx = dresidual and dweight.
-* `RMSNorm(dim, eps=1e-6)` — the reference module's constructor and call
-  (`nn.py:330-337`): y = x * inv_rms * weight with weight initialised to ones.  The reference
-  also floors mean(x^2) at 1e-12 before adding eps (`nn.py:349`); with the default eps that
-  changes inv_rms by at most 5e-7 relative, and only for rows whose mean square is below 1e-12.
+* `RMSNormFunction` / `RMSNorm(dim, eps=1e-6)` — the reference module's constructor and call
+  (`nn.py:330-355`): mean(x^2) floored at 1e-12 (`nn.py:349`), inv_rms = 1/sqrt(mean_sq + eps),
+  y = x * inv_rms * weight with weight initialised to ones; its backward is the reference's
+  analytic one (`nn.py:357-383`), the fused backward with the saved input as h.
 * `FusedAddRMSNorm(dim, eps=1e-6)` — `(y, h) = module(x, residual)` for pre-norm blocks.
 * `FusedRoPEFunction` / `apply_rope(q, k, head_dim, theta)` — the fused RoPE kernel with its
   inverse-rotation backward.
@@ -27,8 +27,11 @@ import torch
 
 from . import kernels as _k
 
-__all__ = ["FusedRMSNormResidualFunction", "fused_add_rmsnorm", "RMSNorm", "FusedAddRMSNorm",
-           "FusedRoPEFunction", "apply_rope"]
+__all__ = ["FusedRMSNormResidualFunction", "fused_add_rmsnorm", "RMSNormFunction", "rms_norm",
+           "RMSNorm", "FusedAddRMSNorm", "FusedRoPEFunction", "apply_rope"]
+
+# nn.py:349: mean_sq = max(1e-12, sum(x ** 2 for x in row) / dim)
+REFERENCE_MIN_MEAN_SQ = 1e-12
 
 
 class FusedRMSNormResidualFunction(torch.autograd.Function):
@@ -70,8 +73,42 @@ def fused_add_rmsnorm(x: torch.Tensor, residual: Optional[torch.Tensor] = None,
     return FusedRMSNormResidualFunction.apply(x, residual, weight, eps)
 
 
+class RMSNormFunction(torch.autograd.Function):
+    """y = RMSNorm(x) * weight as the reference module computes it (nn.py:338-355, mean square
+    floored at `min_mean_sq`); differentiable in x and weight with the module's analytic
+    backward (nn.py:357-383): gw = g * w, dx = inv_rms * (gw - xhat * mean(gw * xhat)),
+    dweight = sum over rows of g * xhat, xhat = x * inv_rms.  Like the reference, the backward
+    treats inv_rms as 1/sqrt(mean(x^2) + eps) also where the floor applied."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, weight: Optional[torch.Tensor], eps: float,
+                min_mean_sq: float):
+        y, inv_rms = _k.rmsnorm_forward(x, weight, eps, min_mean_sq)
+        ctx.save_for_backward(x, weight, inv_rms)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y: torch.Tensor):
+        x, weight, inv_rms = ctx.saved_tensors
+        need_x, need_w, _, _ = ctx.needs_input_grad
+        dx, dweight = _k.fused_rmsnorm_residual_backward(
+            grad_y.contiguous(), x, weight, inv_rms, saved_is_h=True)
+        if dweight is not None and weight is not None and dweight.dtype != weight.dtype:
+            dweight = dweight.to(weight.dtype)
+        return (dx if need_x else None,
+                dweight.view_as(weight) if (need_w and dweight is not None) else None,
+                None, None)
+
+
+def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+             min_mean_sq: float = REFERENCE_MIN_MEAN_SQ) -> torch.Tensor:
+    """Differentiable RMSNorm with the reference module's semantics (nn.py:338-383)."""
+    return RMSNormFunction.apply(x, weight, eps, min_mean_sq)
+
+
 class RMSNorm(torch.nn.Module):
-    """Drop-in for the reference's `velograd.nn.RMSNorm(dim, eps=1e-6)` (nn.py:328-389)."""
+    """Drop-in for the reference's `velograd.nn.RMSNorm(dim, eps=1e-6)` (nn.py:328-389): the
+    mean square is floored at 1e-12 before eps, as the reference's forward does (nn.py:349)."""
 
     def __init__(self, dim: int, eps: float = 1e-6, device=None, dtype=None):
         super().__init__()
@@ -80,7 +117,7 @@ class RMSNorm(torch.nn.Module):
         self.weight = torch.nn.Parameter(torch.ones(dim, device=device, dtype=dtype))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return fused_add_rmsnorm(x, None, self.weight, self.eps)[0]
+        return rms_norm(x, self.weight, self.eps, REFERENCE_MIN_MEAN_SQ)
 
     def extra_repr(self) -> str:
         return f"{self.dim}, eps={self.eps}"
