@@ -1,0 +1,108 @@
+"""Tensors of more than 2^31 elements (64-bit offsets in every kernel): 262147 x 8192 bf16, 4.3 GB
+per tensor.  The rows next to the 2^31-element boundary and the last row are checked against
+the oracle at the usual tolerances; the full-size dweight against a float64 column sum computed
+by torch on the device in row blocks.  Peak device memory about 40 GB of the 288 GB."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fused_rmsnorm as ora
+from tests import _parity as P
+from velograd_amd import kernels as vk
+
+pytestmark = pytest.mark.gpu
+
+ROWS, D = 262147, 8192                  # 2,147,508,224 elements > 2^31
+CHECK_ROWS = [0, 1, 262143, 262144, 262145, ROWS - 1]   # 2^31 / 8192 = 262144
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def big():
+    assert ROWS * D > 2 ** 31
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(ROWS, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    res = torch.randn(ROWS, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    w = (1 + 0.1 * torch.randn(D, device="cuda", generator=gen)).to(torch.bfloat16)
+    yield x, res, w
+    del x, res
+    torch.cuda.empty_cache()
+
+
+def _rows(t):
+    return t[CHECK_ROWS].float().cpu().numpy()
+
+
+def test_forward_backward_beyond_2_pow_31_elements(big):
+    x, res, w = big
+    _say(f"large fwd/bwd {ROWS}x{D} bf16")
+    y, h, inv = vk.fused_rmsnorm_residual_forward(x, res, w, 1e-5)
+    w32 = P.upcast(w)
+    ry, rh, rinv = ora.fused_rmsnorm_residual_forward(_rows(x), _rows(res), w32, 1e-5)
+    P.assert_within_ulp(y[CHECK_ROWS], ry, 1, "y")
+    P.assert_within_ulp(h[CHECK_ROWS], rh, 0, "h")
+    assert P.rel_err(_rows(inv), rinv) <= P.FP32_REL_TOL
+    del y
+
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    g = torch.randn(ROWS, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True)
+    g32, h32, inv32 = _rows(g), _rows(h), _rows(inv)
+    rdx, _ = ora.backward_from_h(g32, h32, w32, inv32)
+    P.dx_check(dx[CHECK_ROWS], rdx, g32 * w32, h32 * inv32, inv32, "dx")
+    # dweight = sum over all rows of g * h * inv_rms, float64, 16384-row blocks
+    ref = torch.zeros(D, dtype=torch.float64, device="cuda")
+    for r0 in range(0, ROWS, 16384):
+        sl = slice(r0, min(ROWS, r0 + 16384))
+        ref += (g[sl].double() * (h[sl].double() * inv[sl].double())).sum(0)
+    P.assert_dweight(dw.double().cpu().numpy(), ref.cpu().numpy())
+    torch.cuda.synchronize()
+
+
+def test_quantised_forwards_beyond_2_pow_31_bytes(big):
+    x, res, w = big
+    w32 = P.upcast(w)
+    x32, r32 = _rows(x), _rows(res)
+    _say(f"large fp8 {ROWS}x{D}")
+    y8, ys, _, inv = vk.fused_rmsnorm_residual_forward_fp8(x, res, w, 1e-5)
+    gi = _rows(inv)
+    codes, scales, _, _ = ora.fused_rmsnorm_residual_forward_fp8(x32, r32, w32, 1e-5, inv_rms=gi)
+    assert np.array_equal(y8[CHECK_ROWS].view(torch.uint8).cpu().numpy(), codes)
+    assert np.array_equal(_rows(ys), scales)
+    del y8, ys
+    _say(f"large mxfp8 {ROWS}x{D}")
+    yq, sc, _, inv = vk.fused_rmsnorm_residual_forward_mx(x, res, w, 1e-5, fmt="e4m3")
+    gi = _rows(inv)
+    codes, scales, _, _ = ora.fused_rmsnorm_residual_forward_mx(x32, r32, w32, 1e-5, fmt="e4m3",
+                                                                inv_rms=gi)
+    assert np.array_equal(yq[CHECK_ROWS].view(torch.uint8).cpu().numpy(), codes)
+    assert np.array_equal(sc[CHECK_ROWS].view(torch.uint8).cpu().numpy(), scales)
+    torch.cuda.synchronize()
+
+
+def test_rope_beyond_2_pow_31_elements():
+    seq, heads, hd = 65537, 256, 128     # 2,147,516,416 elements
+    _say(f"large rope [1, {seq}, {heads}, {hd}]")
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    q = torch.randn(1, seq, heads, hd, device="cuda", dtype=torch.bfloat16, generator=gen)
+    out, _ = vk.fused_rope_forward(q, theta=10000.0)
+    pos = [0, 1, 65535, 65536, seq - 1]  # 2^31 / (256 * 128) = 65536
+    got = out[0, pos].double().cpu().numpy()
+    xs = q[0, pos].double().cpu().numpy()
+    # float64 truth and the float32 tolerance of tests/_parity.py at each position's angles,
+    # plus half a bf16 ulp for the output rounding
+    half = hd // 2
+    ang = np.asarray(pos, np.float64)[:, None] * 10000.0 ** (-2.0 * np.arange(half) / hd)
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    x1, x2 = xs[..., :half], xs[..., half:]
+    want = np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], axis=-1)
+    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 * np.maximum(np.abs(ang), 1.0)[:, None, :] + 2.0 ** -21) \
+        * (np.abs(x1) + np.abs(x2))
+    tol = np.concatenate([b, b], axis=-1) + 2.0 ** -8 * 1.01 * np.abs(want)
+    assert np.all(np.abs(got - want) <= tol)
+    del q, out
+    torch.cuda.synchronize()
