@@ -74,6 +74,8 @@ def parse_args(argv=None):
                    help="skip the config E decode-latency table (reported under extra)")
     p.add_argument("--no-rope", action="store_true",
                    help="skip timing the fused RoPE kernel (reported under extra)")
+    p.add_argument("--no-torch-baseline", action="store_true",
+                   help="skip the PyTorch eager comparison and the reference benchmark's shapes")
     p.add_argument("--no-copy-ceiling", action="store_true",
                    help="skip the same-run stream-probe ceilings")
     return p.parse_args(argv)
@@ -124,6 +126,21 @@ def cpu_baseline(rows: int, d: int, eps: float, budget_s: float, with_bwd: bool)
             break
     med = sorted(times)[len(times) // 2]
     rows_per_s = sample_rows / med
+
+    # the shapes of the reference's own benchmark (benchmarks/bench_vs_pytorch.py:43-72), fp32
+    xb = rng.standard_normal((512, 4096), dtype=np.float32)
+    wb = rng.standard_normal(4096, dtype=np.float32)
+    qb = rng.standard_normal((512, 1024), dtype=np.float32)
+    ref_shapes = {}
+    for name, fn in (("rmsnorm_512x4096_fp32_ms", lambda: ora.fused_rmsnorm_residual(xb, None, wb, 1e-5)),
+                     ("rope_512x1024_hd64_fp32_ms", lambda: ora.fused_rope(qb, head_dim=64))):
+        fn()
+        tt = []
+        for _ in range(7):
+            t0 = time.perf_counter()
+            fn()
+            tt.append(time.perf_counter() - t0)
+        ref_shapes[name] = round(sorted(tt)[3] * 1e3, 3)
     per_row = (fwd_bytes(rows, d, 2) + (bwd_bytes(rows, d, 2) if with_bwd else 0)) / rows
     return {
         "value": round(rows_per_s * per_row / 1e9, 4),
@@ -139,6 +156,7 @@ def cpu_baseline(rows: int, d: int, eps: float, budget_s: float, with_bwd: bool)
         "host_cpu": lscpu_model(),
         "os_cpu_count": os.cpu_count(),
         "affinity_cpus": len(os.sched_getaffinity(0)),
+        "reference_benchmark_shapes": ref_shapes,
     }
 
 
@@ -519,6 +537,85 @@ def measure(lib, config: str, steps: int, warmup: int, nsets: int, event_every: 
     return out
 
 
+def torch_eager_timing(sets, rows: int, d: int, s: int, eps: float, with_bwd: bool, stream,
+                       steps: int = 40) -> dict:
+    """The same step in PyTorch eager operations on the same GPU and buffers, for comparison
+    (the reference's own benchmark compares against PyTorch, benchmarks/bench_vs_pytorch.py):
+    h = x + residual; y = F.rms_norm(h, (D,), weight, eps); autograd backward of y with grad_y
+    -> dx (= dresidual) and dweight.  Same rotating buffer sets; wall clock per step.
+    Informational, under extra."""
+    import torch
+    import torch.nn.functional as F
+
+    n = len(sets)
+
+    def step(k):
+        b = sets[k % n]
+        x = b["x"].detach().requires_grad_(True)
+        w = b["w"].detach().requires_grad_(True)
+        h = x + b["res"]
+        y = F.rms_norm(h, (d,), w, eps)
+        if with_bwd:
+            torch.autograd.grad(y, (x, w), grad_outputs=b["g"])
+
+    for k in range(5):
+        step(k)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        step(k)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) * 1e6 / steps
+    total = fwd_bytes(rows, d, s) + (bwd_bytes(rows, d, s) if with_bwd else 0)
+    return {"torch_eager_step_us": round(us, 2),
+            "torch_eager_gbs": round(total / (us * 1e-6) / 1e9, 1),
+            "torch_eager_ops": "x + residual; F.rms_norm; autograd.grad(y, (x, weight))",
+            "torch_version": torch.__version__}
+
+
+def reference_benchmark_shapes(stream, calls: int = 500) -> dict:
+    """Device and host time per call at the shapes the reference's own benchmark uses
+    (benchmarks/bench_vs_pytorch.py:43-72): fused_rmsnorm_residual(x, None, weight, 1e-5) on
+    512 x 4096 fp32 with weight ~ N(0,1), and fused_rope(x, head_dim=64) on 2-D x [512, 1024]
+    fp32, both through the Python API on device tensors."""
+    import torch
+
+    from velograd_amd import kernels as vk
+
+    dev = torch.device("cuda", 0)
+    x = torch.randn(512, 4096, device=dev)
+    w = torch.randn(4096, device=dev)
+    q = torch.randn(512, 1024, device=dev)
+    out = {}
+    for name, fn in (("rmsnorm_512x4096_fp32", lambda: vk.fused_rmsnorm_residual(x, None, w, 1e-5)),
+                     ("rope_512x1024_hd64_fp32", lambda: vk.fused_rope(q, head_dim=64))):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        host = []
+        e0.record(stream)
+        for _ in range(calls):
+            t0 = time.perf_counter()
+            fn()
+            host.append(time.perf_counter() - t0)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        back_to_back = e0.elapsed_time(e1) * 1e3 / calls
+        iso = []
+        for _ in range(100):
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            iso.append(e0.elapsed_time(e1) * 1e3)
+        # back to back, the launches come no faster than the Python API issues them
+        out[name] = {"device_us_per_call_back_to_back": round(back_to_back, 2),
+                     "isolated_us_median": round(sorted(iso)[50], 2),
+                     "host_us_python_api_median": round(sorted(host)[calls // 2] * 1e6, 2)}
+    return out
+
+
 def other_configs(lib, main_config: str, stream) -> dict:
     """The other bandwidth configurations at modest step counts (B forward, D forward +
     backward, C when it is not the headline), reported under extra."""
@@ -598,6 +695,11 @@ def main(argv=None) -> int:
             extra.update(mx_forward_timing(lib, sets, rows, d, s, code, eps, stream))
     if not args.no_rope:
         extra.update(rope_timing(lib, rows, stream))
+    if not args.no_torch_baseline:
+        extra.update(torch_eager_timing(sets, rows, d, s, eps, with_bwd, stream))
+        extra["speedup_vs_torch_eager"] = round(
+            extra["torch_eager_step_us"] / (ms_per_step * 1e3), 3)
+        extra["reference_benchmark_shapes"] = reference_benchmark_shapes(stream)
     if not args.no_decode:
         extra["config_E_decode"] = decode_latency(lib, stream)
     if not args.no_other_configs:
