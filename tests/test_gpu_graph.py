@@ -89,3 +89,26 @@ def test_graph_replays_of_quantised_forwards_and_rope_match_eager():
         torch.cuda.synchronize()
         for i, (got, want) in enumerate(zip(outs, ref)):
             assert torch.equal(got, want), f"replay {rep}: output {i} differs from the eager call"
+
+
+def test_launch_stream_is_torchs_current_stream():
+    """The library launches on torch's current stream: the default one, a side stream made
+    current, and the capture stream inside torch.cuda.graph."""
+    from velograd_amd.kernels import _stream
+
+    dev = torch.device("cuda", 0)
+    assert _stream(dev) == torch.cuda.current_stream(dev).cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert _stream(dev) == side.cuda_stream == torch.cuda.current_stream(dev).cuda_stream
+        x = torch.randn(64, 4096, device=dev, dtype=torch.bfloat16)
+        y, _, _ = vk.fused_rmsnorm_residual_forward(x, None, None, 1e-5)
+    side.synchronize()
+    ref, _, _ = vk.fused_rmsnorm_residual_forward(x, None, None, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+    g = torch.cuda.CUDAGraph()
+    seen = []
+    with torch.cuda.graph(g):
+        seen.append((_stream(dev), torch.cuda.current_stream(dev).cuda_stream))
+    assert seen[0][0] == seen[0][1]
