@@ -65,19 +65,22 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(
     int32_t dtype, int32_t w_dtype, float eps, void* hip_stream);
 
 /*
- * Residual-free RMSNorm with a floor on the mean square: the reference's module
- * `velograd.nn.RMSNorm.forward` (python/velograd/nn.py:338-355):
- *   mean_sq = max(min_mean_sq, mean(x^2));  inv_rms = 1 / sqrt(mean_sq + eps);
- *   y = (x * inv_rms) * w
+ * RMSNorm with a floor on the mean square, as the reference's module computes it
+ * (`velograd.nn.RMSNorm.forward`, python/velograd/nn.py:338-355), optionally after the residual
+ * add its model performs first (`h = x + attn_out; ffn_norm(h)`, models/llama.py:52-54):
+ *   h = x + residual (residual may be NULL: h is x);  mean_sq = max(min_mean_sq, mean(h^2));
+ *   inv_rms = 1 / sqrt(mean_sq + eps);  y = (h * inv_rms) * w
  * The reference floors at 1e-12 (nn.py:349).  As in Python's max, a NaN mean square becomes the
  * floor (the NaN elements of y stay NaN, the others stay finite).  min_mean_sq must be finite and
- * >= 0; 0 gives velograd_rmsnorm_residual_fwd with residual = NULL exactly.  The module's
- * backward (nn.py:357-383) is velograd_rmsnorm_residual_bwd with saved = x, saved_is_h = 1.
+ * >= 0; 0 gives velograd_rmsnorm_residual_fwd exactly.  The module's backward (nn.py:357-383) is
+ * velograd_rmsnorm_residual_bwd with saved = h, saved_is_h = 1.
  * Arguments as velograd_rmsnorm_residual_fwd.
  */
 VELOGRAD_API int32_t velograd_rmsnorm_fwd(
-    const void* x, const void* weight, void* y, float* inv_rms,
-    int64_t rows, int64_t dim, int64_t ld_x, int64_t ld_y,
+    const void* x, const void* residual, const void* weight,
+    void* y, void* h, float* inv_rms,
+    int64_t rows, int64_t dim,
+    int64_t ld_x, int64_t ld_res, int64_t ld_y, int64_t ld_h,
     int32_t dtype, int32_t w_dtype, float eps, float min_mean_sq, void* hip_stream);
 
 /*

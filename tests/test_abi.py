@@ -87,8 +87,9 @@ def test_fwd_zero_rows_is_a_no_op(lib):
 
 
 def _rmsnorm_fwd(lib, **kw):
-    args = dict(x=16, weight=None, y=32, inv_rms=None, rows=4, dim=64, ld_x=64, ld_y=64,
-                dtype=2, w_dtype=2, eps=1e-6, min_mean_sq=1e-12, stream=None)
+    args = dict(x=16, residual=None, weight=None, y=32, h=None, inv_rms=None, rows=4, dim=64,
+                ld_x=64, ld_res=64, ld_y=64, ld_h=64, dtype=2, w_dtype=2, eps=1e-6,
+                min_mean_sq=1e-12, stream=None)
     args.update(kw)
     return lib.velograd_rmsnorm_fwd(*args.values())
 
@@ -102,6 +103,8 @@ def _rmsnorm_fwd(lib, **kw):
     (dict(x=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
     (dict(ld_y=63), _lib.ERR_INVALID_ARGUMENT, "row strides"),
     (dict(y=16), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(residual=48, h=48), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(residual=48, h=80, ld_res=32), _lib.ERR_INVALID_ARGUMENT, "row strides"),
 ])
 def test_rmsnorm_fwd_argument_errors(lib, kw, code, msg):
     assert _rmsnorm_fwd(lib, **kw) == code

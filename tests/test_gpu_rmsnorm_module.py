@@ -163,3 +163,63 @@ def test_min_mean_sq_is_validated():
         vk.rmsnorm_forward(x, None, 1e-6, min_mean_sq=float("nan"))
     with pytest.raises(TypeError):
         vk.rmsnorm_forward(x.cpu(), None)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
+def test_residual_add_then_module_norm(dtype):
+    """The reference model's `h = x + attn_out; ffn_norm(h)` (models/llama.py:52-54) in one pass:
+    fused_rmsnorm_residual_forward(..., min_mean_sq=1e-12) against the module oracle applied to
+    the fp32 sum; rows where h is zero (x = -residual) or tiny stay finite at eps = 0."""
+    rng = np.random.default_rng(11)
+    d = 4096
+    xs = P.gaussian(rng, (40, d))
+    rs = P.gaussian(rng, (40, d))
+    rs[0] = -xs[0]                     # h = 0
+    xs[1], rs[1] = 1e-8, 0.0           # tiny h
+    xs[2, 7] = np.nan                  # NaN mean square -> the floor
+    x, r = P.to_device(xs, dtype), P.to_device(rs, dtype)
+    w = P.to_device(P.weight_vec(rng, d), dtype)
+    for eps in (1e-6, 0.0):
+        y, h, inv = vk.fused_rmsnorm_residual_forward(x, r, w, eps, min_mean_sq=1e-12)
+        h32 = P.upcast(x) + P.upcast(r)
+        if dtype == torch.float32:
+            assert np.array_equal(P.upcast(h), h32, equal_nan=True)
+        else:
+            P.assert_within_ulp(h, h32, 0, "h")
+        with np.errstate(all="ignore"):
+            ry, rinv = ora.rmsnorm_module_forward(h32.astype(np.float64), P.upcast(w).astype(
+                np.float64), eps)
+        _assert_close_nan_aware(P.upcast(inv), rinv, "inv_rms")
+        if dtype == torch.float32:
+            _assert_close_nan_aware(P.upcast(y), ry, "y")
+        else:
+            P.assert_within_ulp(y, ry.astype(np.float32), 1, "y")
+        assert np.all(np.isfinite(P.upcast(inv)))
+        # without the floor (fused.py) the zero row at eps = 0 has inv_rms = inf
+        _, _, inv0 = vk.fused_rmsnorm_residual_forward(x, r, w, eps)
+        assert np.isinf(P.upcast(inv0)[0, 0]) == (eps == 0.0)
+
+
+def test_fused_add_module_floors_and_backpropagates():
+    d = 1024
+    mod = vnn.FusedAddRMSNorm(d, eps=0.0).cuda()
+    assert mod.min_mean_sq == 1e-12
+    x = torch.randn(3, d, device="cuda", requires_grad=True)
+    r = (-x.detach()).clone().requires_grad_(True)       # h = 0 on every row
+    y, h = mod(x, r)
+    assert torch.equal(y.detach(), torch.zeros_like(y))
+    (y.sum() + h.sum()).backward()
+    # dx = dres = inv_rms * g * w + grad_h = 1e6 + 1 per element
+    assert torch.isfinite(x.grad).all() and torch.equal(x.grad, r.grad)
+    assert torch.allclose(x.grad, torch.full_like(x.grad, 1e6 + 1), rtol=1e-6)
+    # floor off: fused.py semantics, inf * 0 = NaN
+    y0, _ = vnn.fused_add_rmsnorm(x.detach(), r.detach(), mod.weight.detach(), 0.0)
+    assert torch.isnan(y0).all()
+
+
+def test_min_mean_sq_host_arrays():
+    xs = np.zeros((2, 64), dtype=np.float32)
+    y, h, inv = vk.fused_rmsnorm_residual_forward(xs, None, None, 0.0, min_mean_sq=1e-12)
+    assert isinstance(y, np.ndarray) and np.all(y == 0) and np.allclose(inv, 1e6, rtol=1e-6)
+    with pytest.raises(ValueError):
+        vk.fused_rmsnorm_residual_forward(xs, None, None, 0.0, min_mean_sq=-1.0)

@@ -52,8 +52,10 @@ SIGNATURES = {
     ),
     "velograd_rmsnorm_fwd": (
         _c_i32,
-        [_c_ptr, _c_ptr, _c_ptr, _c_ptr,    # x, weight, y, inv_rms
-         _c_i64, _c_i64, _c_i64, _c_i64,    # rows, dim, ld_x, ld_y
+        [_c_ptr, _c_ptr, _c_ptr,            # x, residual, weight
+         _c_ptr, _c_ptr, _c_ptr,            # y, h, inv_rms
+         _c_i64, _c_i64,                    # rows, dim
+         _c_i64, _c_i64, _c_i64, _c_i64,    # ld_x, ld_res, ld_y, ld_h
          _c_i32, _c_i32,                    # dtype, w_dtype
          ctypes.c_float, ctypes.c_float,    # eps, min_mean_sq
          _c_ptr],                           # hip_stream

@@ -981,13 +981,14 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd(const void* x, const void* re
                  eps, 0.0f, hip_stream);
 }
 
-VELOGRAD_API int32_t velograd_rmsnorm_fwd(const void* x, const void* weight, void* y,
-                                          float* inv_rms, int64_t rows, int64_t dim,
-                                          int64_t ld_x, int64_t ld_y, int32_t dtype,
-                                          int32_t w_dtype, float eps, float min_mean_sq,
-                                          void* hip_stream) {
-  return run_fwd("velograd_rmsnorm_fwd", kOutDtype, x, nullptr, weight, y, nullptr, nullptr, 0,
-                 nullptr, inv_rms, rows, dim, ld_x, dim, ld_y, dim, dtype, w_dtype, eps,
+VELOGRAD_API int32_t velograd_rmsnorm_fwd(const void* x, const void* residual,
+                                          const void* weight, void* y, void* h, float* inv_rms,
+                                          int64_t rows, int64_t dim, int64_t ld_x,
+                                          int64_t ld_res, int64_t ld_y, int64_t ld_h,
+                                          int32_t dtype, int32_t w_dtype, float eps,
+                                          float min_mean_sq, void* hip_stream) {
+  return run_fwd("velograd_rmsnorm_fwd", kOutDtype, x, residual, weight, y, nullptr, nullptr, 0,
+                 h, inv_rms, rows, dim, ld_x, ld_res, ld_y, ld_h, dtype, w_dtype, eps,
                  min_mean_sq, hip_stream);
 }
 

@@ -151,7 +151,7 @@ def bwd_workspace_bytes(rows: int, dim: int, device: Optional[torch.device] = No
 # Device paths
 # ---------------------------------------------------------------------------------------------
 def _forward_fast(x: torch.Tensor, residual: Optional[torch.Tensor],
-                  weight: Optional[torch.Tensor], eps: float):
+                  weight: Optional[torch.Tensor], eps: float, min_mean_sq: float = 0.0):
     """The common case without views or copies, for launch-latency-bound (decode) calls:
     contiguous tensors of one dtype on the current device, weight [D] in that dtype or fp32.
     Returns None when the call does not qualify (the general path then handles it)."""
@@ -180,20 +180,35 @@ def _forward_fast(x: torch.Tensor, residual: Optional[torch.Tensor],
     y = torch.empty_like(x)
     h = torch.empty_like(x) if residual is not None else x
     inv_rms = torch.empty(x.shape[:-1] + (1,), dtype=torch.float32, device=dev)
-    rc = _lib.load().velograd_rmsnorm_residual_fwd(
-        x.data_ptr(), None if residual is None else residual.data_ptr(),
-        None if weight is None else weight.data_ptr(),
-        y.data_ptr(), None if residual is None else h.data_ptr(), inv_rms.data_ptr(),
-        rows, d, d, d, d, d, code, wcode, float(eps), _stream(dev))
-    _lib.check(rc, "velograd_rmsnorm_residual_fwd")
+    lib = _lib.load()
+    args = (x.data_ptr(), None if residual is None else residual.data_ptr(),
+            None if weight is None else weight.data_ptr(),
+            y.data_ptr(), None if residual is None else h.data_ptr(), inv_rms.data_ptr(),
+            rows, d, d, d, d, d, code, wcode, float(eps))
+    if min_mean_sq > 0.0:
+        _lib.check(lib.velograd_rmsnorm_fwd(*args, min_mean_sq, _stream(dev)),
+                   "velograd_rmsnorm_fwd")
+    else:
+        _lib.check(lib.velograd_rmsnorm_residual_fwd(*args, _stream(dev)),
+                   "velograd_rmsnorm_residual_fwd")
     return y, h, inv_rms
+
+
+def _check_min_mean_sq(min_mean_sq: float) -> float:
+    min_mean_sq = float(min_mean_sq)
+    if not (math.isfinite(min_mean_sq) and min_mean_sq >= 0.0):
+        raise ValueError(f"min_mean_sq must be finite and >= 0, got {min_mean_sq}")
+    return min_mean_sq
 
 
 def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
                     weight: Optional[torch.Tensor], eps: float, fp8: bool = False,
-                    mx: Optional[str] = None):
+                    mx: Optional[str] = None, min_mean_sq: float = 0.0):
+    min_mean_sq = _check_min_mean_sq(min_mean_sq)
+    if min_mean_sq > 0.0 and (fp8 or mx is not None):
+        raise ValueError("min_mean_sq applies to the forward with y in the input dtype only")
     if not fp8 and mx is None:
-        fast = _forward_fast(x, residual, weight, eps)
+        fast = _forward_fast(x, residual, weight, eps, min_mean_sq)
         if fast is not None:
             return fast
     lib = _lib.load()
@@ -270,13 +285,17 @@ def _forward_device(x: torch.Tensor, residual: Optional[torch.Tensor],
                 _ld(x2), _ld(r2) if r2 is not None else d, d, d,
                 code, wcode, float(eps), _stream(device))
         else:
-            rc = lib.velograd_rmsnorm_residual_fwd(
-                x2.data_ptr(), _ptr(r2), _ptr(w),
-                y2.data_ptr(), _ptr(h2), inv_rms.data_ptr(),
-                rows, d,
-                _ld(x2), _ld(r2) if r2 is not None else d, d, d,
-                code, wcode, float(eps), _stream(device))
-    _lib.check(rc, "velograd_rmsnorm_residual_fwd_fp8" if fp8 else "velograd_rmsnorm_residual_fwd")
+            args = (x2.data_ptr(), _ptr(r2), _ptr(w),
+                    y2.data_ptr(), _ptr(h2), inv_rms.data_ptr(),
+                    rows, d,
+                    _ld(x2), _ld(r2) if r2 is not None else d, d, d,
+                    code, wcode, float(eps))
+            if min_mean_sq > 0.0:
+                rc = lib.velograd_rmsnorm_fwd(*args, min_mean_sq, _stream(device))
+            else:
+                rc = lib.velograd_rmsnorm_residual_fwd(*args, _stream(device))
+    _lib.check(rc, "velograd_rmsnorm_residual_fwd_fp8" if fp8 else
+               ("velograd_rmsnorm_fwd" if min_mean_sq > 0.0 else "velograd_rmsnorm_residual_fwd"))
     return result()
 
 
@@ -372,20 +391,24 @@ def _to_host(t: Optional[torch.Tensor]) -> Optional[np.ndarray]:
 # Public API
 # ---------------------------------------------------------------------------------------------
 def fused_rmsnorm_residual_forward(x: Any, residual: Optional[Any] = None,
-                                   weight: Optional[Any] = None, eps: float = 1e-6):
+                                   weight: Optional[Any] = None, eps: float = 1e-6, *,
+                                   min_mean_sq: float = 0.0):
     """(x + residual) -> RMS-normalise over the last axis -> scale by weight.
 
-    Returns (normed_output, combined_residual, inv_rms) like fused.py:28-46.
+    Returns (normed_output, combined_residual, inv_rms) like fused.py:28-46.  `min_mean_sq`
+    (an extension, keyword only) floors mean(h^2) before eps as the reference's module does
+    (nn.py:349 uses 1e-12; a NaN mean square becomes the floor, as with Python's max); the
+    default 0 is fused.py's unclamped statistic.
     """
     if _is_device_tensor(x):
-        return _forward_device(x, residual, weight, eps)
+        return _forward_device(x, residual, weight, eps, min_mean_sq=min_mean_sq)
     device = _require_gpu()
     xd = _host_to_device_f32(x, device)
     rd = _host_to_device_f32(residual, device) if residual is not None else None
     wd = _host_to_device_f32(weight, device) if weight is not None else None
     if wd is not None and wd.numel() != xd.shape[-1]:
         raise ValueError(f"weight has {wd.numel()} elements, expected {xd.shape[-1]}")
-    y, h, inv_rms = _forward_device(xd, rd, wd, eps)
+    y, h, inv_rms = _forward_device(xd, rd, wd, eps, min_mean_sq=min_mean_sq)
     y_np = _to_host(y)
     # With residual=None the reference returns its (float32) x as h.
     h_np = _to_host(h) if residual is not None else np.asarray(x, dtype=np.float32)
@@ -591,27 +614,9 @@ def rmsnorm_forward(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps:
     """
     if not _is_device_tensor(x):
         raise TypeError("rmsnorm_forward takes torch tensors on a ROCm device")
-    min_mean_sq = float(min_mean_sq)
-    if not (math.isfinite(min_mean_sq) and min_mean_sq >= 0.0):
-        raise ValueError(f"min_mean_sq must be finite and >= 0, got {min_mean_sq}")
-    lib = _lib.load()
-    device = x.device
-    code = _dtype_code(x, "x")
     if x.dim() == 0 or x.shape[-1] == 0:
         raise ValueError("rmsnorm_forward needs a non-empty last dimension")
-    d = x.shape[-1]
-    w, wcode = _prep_weight(weight, d, x.dtype, device)
-    x2 = _rows_view(x, "x")
-    rows = x2.shape[0]
-    y = torch.empty(x.shape, dtype=x.dtype, device=device)
-    inv_rms = torch.empty(tuple(x.shape[:-1]) + (1,), dtype=torch.float32, device=device)
-    if rows == 0:
-        return y, inv_rms
-    with torch.cuda.device(device):
-        rc = lib.velograd_rmsnorm_fwd(x2.data_ptr(), _ptr(w), y.data_ptr(), inv_rms.data_ptr(),
-                                      rows, d, _ld(x2), d, code, wcode, float(eps), min_mean_sq,
-                                      _stream(device))
-    _lib.check(rc, "velograd_rmsnorm_fwd")
+    y, _, inv_rms = _forward_device(x, None, weight, eps, min_mean_sq=min_mean_sq)
     return y, inv_rms
 
 

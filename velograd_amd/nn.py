@@ -12,7 +12,9 @@ gradient function (python/velograd/kernels/__init__.py:30-31).  Here:
   (`nn.py:330-355`): mean(x^2) floored at 1e-12 (`nn.py:349`), inv_rms = 1/sqrt(mean_sq + eps),
   y = x * inv_rms * weight with weight initialised to ones; its backward is the reference's
   analytic one (`nn.py:357-383`), the fused backward with the saved input as h.
-* `FusedAddRMSNorm(dim, eps=1e-6)` — `(y, h) = module(x, residual)` for pre-norm blocks.
+* `FusedAddRMSNorm(dim, eps=1e-6)` — `(y, h) = module(x, residual)` for pre-norm blocks: the
+  reference model's `h = x + attn_out; ffn_norm(h)` (`models/llama.py:52-54`) in one pass, with
+  the module's floor on the mean square.
 * `FusedRoPEFunction` / `apply_rope(q, k, head_dim, theta)` — the fused RoPE kernel with its
   inverse-rotation backward.
 
@@ -39,8 +41,9 @@ class FusedRMSNormResidualFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, residual: Optional[torch.Tensor],
-                weight: Optional[torch.Tensor], eps: float):
-        y, h, inv_rms = _k.fused_rmsnorm_residual_forward(x, residual, weight, eps)
+                weight: Optional[torch.Tensor], eps: float, min_mean_sq: float = 0.0):
+        y, h, inv_rms = _k.fused_rmsnorm_residual_forward(x, residual, weight, eps,
+                                                          min_mean_sq=min_mean_sq)
         if residual is None:
             h = x.view_as(x)  # a distinct output object that aliases x (fused.py:39)
         ctx.save_for_backward(h, weight, inv_rms)
@@ -57,20 +60,22 @@ class FusedRMSNormResidualFunction(torch.autograd.Function):
         dx, dweight = _k.fused_rmsnorm_residual_backward(
             grad_y.contiguous(), h, weight, inv_rms, saved_is_h=True,
             grad_h=None if grad_h is None else grad_h.contiguous())
-        need_x, need_res, need_w, _ = ctx.needs_input_grad
+        need_x, need_res, need_w = ctx.needs_input_grad[:3]
         if dweight is not None and weight is not None and dweight.dtype != weight.dtype:
             dweight = dweight.to(weight.dtype)
         return (dx if need_x else None,
                 dx if (need_res and ctx.has_residual) else None,
                 dweight.view_as(weight) if (need_w and dweight is not None) else None,
-                None)
+                None, None)
 
 
 def fused_add_rmsnorm(x: torch.Tensor, residual: Optional[torch.Tensor] = None,
-                      weight: Optional[torch.Tensor] = None,
-                      eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Differentiable `(y, h)`: h = x + residual, y = RMSNorm(h) * weight."""
-    return FusedRMSNormResidualFunction.apply(x, residual, weight, eps)
+                      weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                      min_mean_sq: float = 0.0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Differentiable `(y, h)`: h = x + residual, y = RMSNorm(h) * weight.  The statistic is
+    fused.py's (min_mean_sq = 0) unless a floor on mean(h^2) is given (the reference module's
+    is 1e-12, nn.py:349)."""
+    return FusedRMSNormResidualFunction.apply(x, residual, weight, eps, min_mean_sq)
 
 
 class RMSNormFunction(torch.autograd.Function):
@@ -124,20 +129,25 @@ class RMSNorm(torch.nn.Module):
 
 
 class FusedAddRMSNorm(torch.nn.Module):
-    """Pre-norm block helper: `(y, h) = module(x, residual)` with h = x + residual."""
+    """Pre-norm block helper: `(y, h) = module(x, residual)` with h = x + residual and y the
+    reference module's RMSNorm of h, in one pass: the reference's model computes
+    `h = x + attn_out; ffn_norm(h)` (models/llama.py:52-54) with `ffn_norm` an `nn.RMSNorm`, so
+    the mean square is floored at `min_mean_sq` (1e-12, nn.py:349) unless told otherwise."""
 
-    def __init__(self, dim: int, eps: float = 1e-6, device=None, dtype=None):
+    def __init__(self, dim: int, eps: float = 1e-6, device=None, dtype=None,
+                 min_mean_sq: float = REFERENCE_MIN_MEAN_SQ):
         super().__init__()
         self.dim = dim
         self.eps = eps
+        self.min_mean_sq = min_mean_sq
         self.weight = torch.nn.Parameter(torch.ones(dim, device=device, dtype=dtype))
 
     def forward(self, x: torch.Tensor,
                 residual: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
-        return fused_add_rmsnorm(x, residual, self.weight, self.eps)
+        return fused_add_rmsnorm(x, residual, self.weight, self.eps, self.min_mean_sq)
 
     def extra_repr(self) -> str:
-        return f"{self.dim}, eps={self.eps}"
+        return f"{self.dim}, eps={self.eps}, min_mean_sq={self.min_mean_sq}"
 
 
 class FusedRoPEFunction(torch.autograd.Function):
