@@ -386,7 +386,7 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2) -> dict:
         rc = 0
         for x, out, heads, hd in bufs[i % sets]:
             rc |= fn(x.data_ptr(), out.data_ptr(), 1, tokens, heads, hd, hd, 500000.0, 0,
-                     _lib.DTYPE_BF16, sp)
+                     _lib.ROPE_HALF, _lib.DTYPE_BF16, sp)
         return rc
 
     for i in range(sets * 2):
@@ -404,9 +404,38 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2) -> dict:
     us = e0.elapsed_time(e1) * 1e3 / reps
     nbytes = sum(2 * tokens * h * d * 2 for h, d in shapes)
     del bufs
+
+    # The reference model's RoPE (functional.py:287-315): interleaved pairs over the whole
+    # hidden vector of the normalised attention input, [tokens, 4096] bf16, base 10000.
+    hid = 4096
+    ibufs = [(torch.randn(tokens, hid, device=dev).to(torch.bfloat16),
+              torch.empty(tokens, hid, device=dev, dtype=torch.bfloat16)) for _ in range(sets)]
+
+    def istep(i):
+        x, out = ibufs[i % sets]
+        return fn(x.data_ptr(), out.data_ptr(), 1, tokens, 1, hid, hid, 10000.0, 0,
+                  _lib.ROPE_INTERLEAVED, _lib.DTYPE_BF16, sp)
+
+    for i in range(sets * 2):
+        _lib.check(istep(i), "interleaved rope warm-up")
+    torch.cuda.synchronize()
+    e0.record(stream)
+    rc = 0
+    for i in range(reps):
+        rc |= istep(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    _lib.check(rc, "interleaved rope timed")
+    ius = e0.elapsed_time(e1) * 1e3 / reps
+    ibytes = 2 * tokens * hid * 2
+    del ibufs
     return {"rope_qk_us_mean": round(us, 2), "rope_qk_bytes": nbytes,
             "rope_qk_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5"}
+            "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5",
+            "rope_interleaved_us_mean": round(ius, 2), "rope_interleaved_bytes": ibytes,
+            "rope_interleaved_gbs": round(ibytes / (ius * 1e-6) / 1e9, 1),
+            "rope_interleaved_workload": f"x [{tokens},{hid}] bf16, pairs (2i, 2i+1) over the "
+                                         f"hidden vector, base 1e4 (functional.apply_rotary_emb)"}
 
 
 def measure(lib, config: str, steps: int, warmup: int, nsets: int, event_every: int,

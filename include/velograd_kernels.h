@@ -182,27 +182,37 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
 VELOGRAD_API size_t velograd_rmsnorm_residual_bwd_workspace_bytes(int64_t rows, int64_t dim,
                                                                   int32_t device);
 
+/* Pairings of a head vector's elements for velograd_rope. */
+#define VELOGRAD_ROPE_HALF 0        /* (j, j + rot_dim/2): fused.py, fused_kernels.cu */
+#define VELOGRAD_ROPE_INTERLEAVED 1 /* (2j, 2j + 1): functional.apply_rotary_emb, ops.rs */
+
 /*
- * Rotary position embedding, "rotate half" pairing, on one tensor (call once for q and once
- * for k).  Replaces fused_rope_forward (python/velograd/kernels/fused.py:72-130), whose body
- * this follows for a tensor laid out as [outer, seq, heads, dim]:
- *   position of x[o, s, h, :] is s (fused.py:96-98); for j < rot_dim / 2,
- *     freq_j = 1 / theta^(2j / rot_dim), angle = s * freq_j (fp32, fused.py:98-103),
- *     (x_j, x_{j + rot_dim/2}) -> (x_j cos - x_{j+rot_dim/2} sin, x_j sin + x_{j+rot_dim/2} cos);
- *   elements rot_dim .. dim-1 are copied (fused.py:119-120).
+ * Rotary position embedding on one tensor (call once for q and once for k), laid out as
+ * [outer, seq, heads, dim]; the position of x[o, s, h, :] is s.  For j < rot_dim / 2,
+ *   freq_j = 1 / theta^(2j / rot_dim), angle = s * freq_j (fp32), and the pair (a, b) of j
+ *   becomes (a cos - b sin, a sin + b cos); elements rot_dim .. dim-1 are copied.
+ * pairing VELOGRAD_ROPE_HALF: (a, b) = (x_j, x_{j + rot_dim/2}).  Replaces fused_rope_forward
+ *   (python/velograd/kernels/fused.py:72-130; positions fused.py:96-98, angles :98-103, copied
+ *   tail :119-120) and the reference's CUDA kernel (src/cuda/fused_kernels.cu:145-181).
+ * pairing VELOGRAD_ROPE_INTERLEAVED: (a, b) = (x_{2j}, x_{2j+1}).  Replaces
+ *   apply_rotary_emb (python/velograd/functional.py:287-315, the RoPE the reference's LLaMA
+ *   model applies, models/llama.py:49; there x is [..., seq, dim]: heads = 1, rot_dim = dim)
+ *   and rotary_pos_embedding_forward (src/ops.rs:465-499).
  *
  *   x, out   : [outer, seq, heads, dim] contiguous in `dtype`; out may be x itself (in place)
  *              but must not otherwise overlap it.
- *   rot_dim  : the reference's head_dim: even, 2 <= rot_dim <= dim, rot_dim <= 4096.
+ *   rot_dim  : the rotated width (the reference's head_dim): even, 2 <= rot_dim <= dim,
+ *              rot_dim <= 8192.
  *   theta    : the frequency base (> 0).
  *   inverse  : nonzero rotates by -angle: the backward (grad_x from grad_out), the rotary
- *              backward rule of src/ops.rs:501-530 for this pairing.  No counterpart in the
- *              fused reference, which has no backward.
+ *              backward of src/ops.rs:501-530 and functional.py:316-345.
+ *   pairing  : VELOGRAD_ROPE_HALF or VELOGRAD_ROPE_INTERLEAVED.
  */
 VELOGRAD_API int32_t velograd_rope(
     const void* x, void* out,
-    int64_t outer, int64_t seq, int64_t heads, int64_t dim, int64_t rot_dim,
-    float theta, int32_t inverse, int32_t dtype, void* hip_stream);
+    int64_t outer, int64_t seq, int64_t heads, int64_t dim,
+    int64_t rot_dim, float theta, int32_t inverse, int32_t pairing,
+    int32_t dtype, void* hip_stream);
 
 /* Text of the calling thread's last error ("" if none).  No counterpart in the reference. */
 VELOGRAD_API const char* velograd_kernels_last_error(void);

@@ -303,6 +303,26 @@ def fused_rope(x, k=None, head_dim: Optional[int] = None, base: float = 10000.0)
     return q_rot
 
 
+def apply_rotary_emb(x, base: float = 10000.0, inverse: bool = False) -> np.ndarray:
+    """python/velograd/functional.py:287-315 (forward) and :316-345 (inverse = the backward's
+    rotation) in float64, the precision of the reference's Python floats: interleaved pairs
+    (x_2i, x_2i+1) of the last axis, position = index along axis -2."""
+    x = np.asarray(x, dtype=np.float64)
+    seq_len, dim = x.shape[-2], x.shape[-1]                              # :289-290
+    assert dim % 2 == 0, "Dimension must be even for RoPE pairs"         # :291
+    i = np.arange(dim // 2, dtype=np.float64)
+    theta = 1.0 / (base ** ((2.0 * i) / float(dim)))                     # :302
+    angle = np.arange(seq_len, dtype=np.float64)[:, None] * theta        # :303
+    cos_val, sin_val = np.cos(angle), np.sin(angle)                      # :304-305
+    if inverse:
+        sin_val = -sin_val
+    x0, x1 = x[..., 0::2], x[..., 1::2]                                  # :307-311
+    out = np.empty_like(x)
+    out[..., 0::2] = x0 * cos_val - x1 * sin_val                         # :313
+    out[..., 1::2] = x0 * sin_val + x1 * cos_val                         # :314
+    return out
+
+
 # ---------------------------------------------------------------------------------------------
 # OCP Microscaling (MX) block quantisation of y: blocks of 32 consecutive elements of a row share
 # one E8M0 scale 2^s with s = floor(log2(amax)) - emax (8 for E4M3, 2 for E2M1), clamped to

@@ -180,11 +180,14 @@ def test_dtype_codes_match_header():
     for name, val in (("F32", _lib.DTYPE_F32), ("F16", _lib.DTYPE_F16), ("BF16", _lib.DTYPE_BF16)):
         assert re.search(rf"#define VELOGRAD_DTYPE_{name} {val}\b", text)
     assert _lib.TORCH_DTYPE_CODES[torch.bfloat16] == _lib.DTYPE_BF16
+    for name, val in (("MX_E4M3", _lib.MX_E4M3), ("MX_E2M1", _lib.MX_E2M1),
+                      ("ROPE_HALF", _lib.ROPE_HALF), ("ROPE_INTERLEAVED", _lib.ROPE_INTERLEAVED)):
+        assert re.search(rf"#define VELOGRAD_{name} {val}\b", text), name
 
 
 def _rope(lib, **kw):
     args = dict(x=16, out=32, outer=1, seq=4, heads=2, dim=64, rot_dim=64, theta=10000.0,
-                inverse=0, dtype=2, stream=None)
+                inverse=0, pairing=0, dtype=2, stream=None)
     args.update(kw)
     return lib.velograd_rope(*args.values())
 
@@ -195,9 +198,11 @@ def _rope(lib, **kw):
     (dict(rot_dim=63), _lib.ERR_INVALID_ARGUMENT, "must be even"),
     (dict(rot_dim=0), _lib.ERR_INVALID_ARGUMENT, "must be even"),
     (dict(rot_dim=66), _lib.ERR_INVALID_ARGUMENT, "<= dim"),
-    (dict(dim=8192, rot_dim=8192), _lib.ERR_INVALID_ARGUMENT, "<= 4096"),
+    (dict(dim=16384, rot_dim=16384), _lib.ERR_INVALID_ARGUMENT, "<= 8192"),
     (dict(x=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
     (dict(theta=0.0), _lib.ERR_INVALID_ARGUMENT, "theta"),
+    (dict(pairing=2), _lib.ERR_INVALID_ARGUMENT, "pairing"),
+    (dict(pairing=-1), _lib.ERR_INVALID_ARGUMENT, "pairing"),
     (dict(theta=float("nan")), _lib.ERR_INVALID_ARGUMENT, "theta"),
 ])
 def test_rope_argument_errors(lib, kw, code, msg):

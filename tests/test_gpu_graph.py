@@ -111,4 +111,8 @@ def test_launch_stream_is_torchs_current_stream():
     seen = []
     with torch.cuda.graph(g):
         seen.append((_stream(dev), torch.cuda.current_stream(dev).cuda_stream))
+        yg, _, _ = vk.fused_rmsnorm_residual_forward(x, None, None, 1e-5)
     assert seen[0][0] == seen[0][1]
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(yg, ref)

@@ -18,6 +18,7 @@ from oracle import fused_rmsnorm as ora
 from tests import _parity as P
 from velograd_amd import _lib
 from velograd_amd import kernels as vk
+from velograd_amd import nn as vnn
 
 pytestmark = pytest.mark.gpu
 
@@ -109,7 +110,8 @@ def test_rope_in_place_through_the_c_abi():
     want, _ = vk.fused_rope_forward(x)
     buf = x.clone()
     rc = _lib.load().velograd_rope(buf.data_ptr(), buf.data_ptr(), 1, 64, 8, 128, 128, 10000.0,
-                                   0, _lib.DTYPE_BF16, torch.cuda.current_stream().cuda_stream)
+                                   0, _lib.ROPE_HALF, _lib.DTYPE_BF16,
+                                   torch.cuda.current_stream().cuda_stream)
     _lib.check(rc, "velograd_rope in place")
     assert torch.equal(buf, want)
 
@@ -131,3 +133,76 @@ def test_rope_empty_and_deterministic():
     rng = np.random.default_rng(5)
     x = P.to_device(P.gaussian(rng, (512, 16, 64)), torch.bfloat16)
     assert torch.equal(vk.fused_rope_forward(x)[0], vk.fused_rope_forward(x)[0])
+
+
+# ---------------------------------------------------------------------------------------------
+# Interleaved pairs: the reference model's apply_rotary_emb (functional.py:287-345)
+# ---------------------------------------------------------------------------------------------
+def _interleaved_bound(x: np.ndarray, base: float) -> np.ndarray:
+    """The angle-scaled float32 tolerance of tests/_parity.py for pairs (x_2i, x_2i+1)."""
+    x = np.abs(np.asarray(x, np.float64))
+    seq, dim = x.shape[-2], x.shape[-1]
+    ang = np.arange(seq)[:, None] * base ** (-2.0 * np.arange(dim // 2) / dim)
+    mag = x[..., 0::2] + x[..., 1::2]
+    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 * np.maximum(ang, 1.0) + 2.0 ** -21) * mag
+    out = np.empty_like(x)
+    out[..., 0::2] = b
+    out[..., 1::2] = b
+    return out
+
+
+INTERLEAVED_CASES = [(torch.float32, (37, 64)), (torch.bfloat16, (2, 128, 4096)),
+                     (torch.float16, (3, 50, 256)), (torch.bfloat16, (1, 64, 8192)),
+                     (torch.float32, (3, 5, 6)), (torch.bfloat16, (2, 9, 12)),
+                     (torch.float32, (2, 9, 12)), (torch.float32, (4, 2, 3, 40))]
+
+
+@pytest.mark.parametrize("dtype,shape", INTERLEAVED_CASES,
+                         ids=[f"{str(d).split('.')[-1]}-{'x'.join(map(str, s))}"
+                              for d, s in INTERLEAVED_CASES])
+@pytest.mark.parametrize("base", [10000.0, 500000.0])
+def test_interleaved_rope_matches_oracle(dtype, shape, base):
+    _say(f"rope interleaved {dtype} {shape} base {base}")
+    rng = np.random.default_rng(len(shape) + shape[-1])
+    x = P.to_device(P.gaussian(rng, shape), dtype)
+    x64 = P.upcast(x).astype(np.float64)
+    for inverse in (False, True):
+        got = vk.fused_rope_interleaved(x, base, inverse=inverse)
+        assert got.dtype == dtype and got.shape == x.shape
+        want = ora.apply_rotary_emb(x64, base, inverse=inverse)
+        tol = _interleaved_bound(x64, base) + ROUNDING[dtype] * np.abs(want)
+        err = np.abs(P.upcast(got).astype(np.float64) - want)
+        assert np.all(err <= tol), (inverse, float((err - tol).max()))
+    # position 0 of every leading index is the identity (bit-exact)
+    assert torch.equal(vk.fused_rope_interleaved(x, base)[..., 0, :], x[..., 0, :])
+
+
+def test_interleaved_rope_round_trip_and_autograd():
+    rng = np.random.default_rng(9)
+    x32 = P.gaussian(rng, (2, 33, 256))
+    x = torch.from_numpy(x32).cuda().requires_grad_(True)
+    y = vnn.apply_rotary_emb(x, 10000.0)
+    g = torch.from_numpy(P.gaussian(rng, (2, 33, 256))).cuda()
+    y.backward(g)
+    # torch float64 autograd of the complex formulation on the CPU
+    t = torch.from_numpy(x32.astype(np.float64)).requires_grad_(True)
+    z = torch.view_as_complex(t.reshape(2, 33, 128, 2))
+    inv_freq = 10000.0 ** (-torch.arange(0, 256, 2, dtype=torch.float64) / 256)
+    ang = torch.arange(33, dtype=torch.float64)[:, None] * inv_freq[None, :]
+    ref = torch.view_as_real(z * torch.polar(torch.ones_like(ang), ang)).reshape(2, 33, 256)
+    ref.backward(g.double().cpu())
+    assert float((y.detach().double().cpu() - ref.detach()).abs().max()) < 2e-4
+    assert float((x.grad.double().cpu() - t.grad).abs().max()) < 2e-4
+    back = vk.fused_rope_interleaved(y.detach(), 10000.0, inverse=True)
+    assert float((back - x.detach()).abs().max()) < 1e-4
+
+
+def test_interleaved_rope_errors():
+    with pytest.raises(ValueError):
+        vk.fused_rope_interleaved(torch.zeros(4, 7, device="cuda"))      # odd dim
+    with pytest.raises(ValueError):
+        vk.fused_rope_interleaved(torch.zeros(8, device="cuda"))         # no seq axis
+    with pytest.raises(ValueError):
+        vk.fused_rope_interleaved(torch.zeros(2, 16384, device="cuda"))  # wider than 8192
+    with pytest.raises(TypeError):
+        vk.fused_rope_interleaved(np.zeros((4, 8), np.float32))

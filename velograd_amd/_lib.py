@@ -29,6 +29,9 @@ TORCH_DTYPE_CODES = {
 MX_E4M3 = 0
 MX_E2M1 = 1
 
+ROPE_HALF = 0
+ROPE_INTERLEAVED = 1
+
 ERR_INVALID_ARGUMENT = -1
 ERR_UNSUPPORTED_DTYPE = -2
 ERR_WORKSPACE_TOO_SMALL = -3
@@ -99,7 +102,7 @@ SIGNATURES = {
         [_c_ptr, _c_ptr,                    # x, out
          _c_i64, _c_i64, _c_i64, _c_i64,    # outer, seq, heads, dim
          _c_i64, ctypes.c_float, _c_i32,    # rot_dim, theta, inverse
-         _c_i32, _c_ptr],                   # dtype, hip_stream
+         _c_i32, _c_i32, _c_ptr],           # pairing, dtype, hip_stream
     ),
     "velograd_kernels_last_error": (ctypes.c_char_p, []),
     "velograd_kernels_version": (ctypes.c_char_p, []),

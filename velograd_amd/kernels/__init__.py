@@ -55,6 +55,7 @@ __all__ = [
     "fused_rope",
     "fused_rope_forward",
     "fused_rope_backward",
+    "fused_rope_interleaved",
     "bwd_workspace_bytes",
 ]
 
@@ -508,7 +509,8 @@ def _rope_k_layout(k_shape, q_shape, q_layout, q_split: bool, h_dim: int):
 
 
 def _rope_device(t: torch.Tensor, layout, h_dim: int, theta: float, inverse: bool,
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 out: Optional[torch.Tensor] = None,
+                 pairing: int = _lib.ROPE_HALF) -> torch.Tensor:
     code = _dtype_code(t, "q/k")
     src = t.contiguous()
     dst = torch.empty_like(src) if out is None else out
@@ -517,8 +519,8 @@ def _rope_device(t: torch.Tensor, layout, h_dim: int, theta: float, inverse: boo
         return dst.view(t.shape)
     with torch.cuda.device(src.device):
         rc = _lib.load().velograd_rope(src.data_ptr(), dst.data_ptr(), outer, seq, heads, dim,
-                                       h_dim, float(theta), 1 if inverse else 0, code,
-                                       _stream(src.device))
+                                       h_dim, float(theta), 1 if inverse else 0, pairing,
+                                       code, _stream(src.device))
     _lib.check(rc, "velograd_rope")
     return dst.view(t.shape)
 
@@ -580,6 +582,28 @@ def fused_rope(x: Any, k: Optional[Any] = None, head_dim: Optional[int] = None,
     if k is not None:
         return q_rot, k_rot
     return q_rot
+
+
+def fused_rope_interleaved(x: torch.Tensor, base: float = 10000.0,
+                           inverse: bool = False) -> torch.Tensor:
+    """RoPE with interleaved pairs, as the reference's model applies it: apply_rotary_emb
+    (python/velograd/functional.py:287-315; models/llama.py:49 rotates the normalised attention
+    input with it) and src/ops.rs:465-499.  x is [..., seq, dim]: positions run along axis -2,
+    the pairs (x_2i, x_2i+1) of the whole last axis rotate by pos * base^(-2i / dim).
+    `inverse=True` rotates back: the backward (functional.py:316-345, ops.rs:501-530).  Returns
+    a new tensor in x's dtype; device tensors only, dim even and at most 8192."""
+    if not _is_device_tensor(x):
+        raise TypeError("fused_rope_interleaved takes torch tensors on a ROCm device")
+    if x.dim() < 2:
+        raise ValueError("fused_rope_interleaved: x must be [..., seq, dim]")
+    seq, dim = x.shape[-2], x.shape[-1]
+    if dim % 2 != 0:
+        raise ValueError(f"fused_rope_interleaved: dim={dim} must be even (RoPE pairs)")
+    if dim == 0:
+        return torch.empty_like(x)
+    outer = math.prod(x.shape[:-2])
+    return _rope_device(x, (outer, seq, 1, dim), dim, base, inverse,
+                        pairing=_lib.ROPE_INTERLEAVED)
 
 
 def fused_rmsnorm_residual_forward_mx(x: torch.Tensor, residual: Optional[torch.Tensor] = None,

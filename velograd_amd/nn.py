@@ -17,6 +17,9 @@ gradient function (python/velograd/kernels/__init__.py:30-31).  Here:
   the module's floor on the mean square.
 * `FusedRoPEFunction` / `apply_rope(q, k, head_dim, theta)` — the fused RoPE kernel with its
   inverse-rotation backward.
+* `RotaryEmbFunction` / `apply_rotary_emb(x, base)` — the reference model's RoPE
+  (`functional.py:287-345`, interleaved pairs over the whole last axis, positions on axis -2)
+  on the same kernel, with its inverse-rotation backward.
 
 All computation runs in the HIP kernels; there is no CPU path.
 """
@@ -30,7 +33,8 @@ import torch
 from . import kernels as _k
 
 __all__ = ["FusedRMSNormResidualFunction", "fused_add_rmsnorm", "RMSNormFunction", "rms_norm",
-           "RMSNorm", "FusedAddRMSNorm", "FusedRoPEFunction", "apply_rope"]
+           "RMSNorm", "FusedAddRMSNorm", "FusedRoPEFunction", "apply_rope",
+           "RotaryEmbFunction", "apply_rotary_emb"]
 
 # nn.py:349: mean_sq = max(1e-12, sum(x ** 2 for x in row) / dim)
 REFERENCE_MIN_MEAN_SQ = 1e-12
@@ -171,3 +175,23 @@ def apply_rope(q: torch.Tensor, k: Optional[torch.Tensor] = None,
     q_rot = FusedRoPEFunction.apply(q, head_dim, theta)
     k_rot = FusedRoPEFunction.apply(k, head_dim, theta) if k is not None else None
     return q_rot, k_rot
+
+
+class RotaryEmbFunction(torch.autograd.Function):
+    """The reference's differentiable `apply_rotary_emb` (functional.py:287-345): forward and
+    backward (the inverse rotation, functional.py:316-345) are one kernel launch each."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, base: float):
+        ctx.base = base
+        return _k.fused_rope_interleaved(x, base)
+
+    @staticmethod
+    def backward(ctx, grad: torch.Tensor):
+        return _k.fused_rope_interleaved(grad.contiguous(), ctx.base, inverse=True), None
+
+
+def apply_rotary_emb(x: torch.Tensor, base: float = 10000.0) -> torch.Tensor:
+    """Drop-in for `velograd.functional.apply_rotary_emb(x, base=10000.0)`
+    (functional.py:287): interleaved-pair RoPE over x's last axis, positions along axis -2."""
+    return RotaryEmbFunction.apply(x, base)
