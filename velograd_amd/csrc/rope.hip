@@ -225,13 +225,16 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(const RopeArgs a) {
 // heads to amortise rope_kernel's tables, whose sincosf per (position, pair) bound that kernel
 // by VALU at a quarter of the copy speed.  The angles come out closer to the reference's
 // double-precision ones (functional.py:302-305) than a float32 angle does.  kRopeDepth loads
-// stay in flight per thread; they are issued before the double-precision set-up.
+// stay in flight per thread; they are issued before the double-precision set-up.  The kernel is
+// latency-bound on its loads, so the launch bounds ask for 4 waves per SIMD (128 VGPRs, no
+// spills; 138 VGPRs and 3 waves ran 10% slower).
 constexpr int kRopeRun = 32;
 constexpr int kRopeDepth = 4;
 
 template <int DT>
-__global__ __launch_bounds__(kRopeBlock) void rope_run_kernel(const RopeArgs a, int64_t col_blocks,
-                                                              int64_t groups) {
+__global__ __launch_bounds__(kRopeBlock, 4) void rope_run_kernel(const RopeArgs a,
+                                                                 int64_t col_blocks,
+                                                                 int64_t groups) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
   constexpr int P = V / 2;
