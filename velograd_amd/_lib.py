@@ -136,6 +136,29 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+_fast = None
+_fast_tried = False
+
+
+def fastpath():
+    """The optional pybind11 fast path (`velograd_amd._fastpath`, built next to the library by
+    velograd_amd.build) for launch-bound forward calls, or None when it is not built or when
+    VELOGRAD_NO_FASTPATH=1.  Loaded once, after the kernels library."""
+    global _fast, _fast_tried
+    if not _fast_tried:
+        load()
+        with _lock:
+            if not _fast_tried:
+                if os.environ.get("VELOGRAD_NO_FASTPATH", "0") != "1":
+                    try:
+                        from . import _fastpath as fp
+                        _fast = fp
+                    except ImportError:
+                        _fast = None
+                _fast_tried = True
+    return _fast
+
+
 def last_error() -> str:
     msg = load().velograd_kernels_last_error()
     return msg.decode("utf-8", "replace") if msg else ""

@@ -26,6 +26,11 @@ PROBE_LIB_PATH = os.path.join(LIB_DIR, "libvelograd_stream_probe.so")
 
 OFFLOAD_ARCH = "gfx950"
 
+# Host-only pybind11 binding of the forward's fast path to torch tensors (a CPython extension
+# module next to the package's Python files).  Optional at run time: without it the ctypes path
+# runs the same kernels.
+FASTPATH_SRC = os.path.join(PKG_DIR, "csrc", "torch_fastpath.cpp")
+
 HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
@@ -61,11 +66,50 @@ def _hipcc(srcs, out: str, verbose: bool) -> None:
     os.replace(tmp, out)
 
 
+def fastpath_path() -> str:
+    import sysconfig
+    return os.path.join(PKG_DIR, "_fastpath" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_fastpath(verbose: bool = False) -> str:
+    """Compile the torch-tensor fast path against the installed torch (host C++, g++)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    out = fastpath_path()
+    tmp = out + ".tmp"
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC",
+           "-fvisibility=hidden", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-DTORCH_EXTENSION_NAME=_fastpath", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           "-I", INCLUDE_DIR, "-I", sysconfig.get_paths()["include"]]
+    for inc in cpp_extension.include_paths(device_type="cuda"):
+        cmd += ["-I", inc]
+    cmd += [FASTPATH_SRC, "-o", tmp,
+            "-L", LIB_DIR, "-lvelograd_kernels", "-Wl,-rpath,$ORIGIN/lib",
+            "-L", torch_lib, "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+            "-ltorch_hip", f"-Wl,-rpath,{torch_lib}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(
+            "fast-path build failed (exit %d):\n%s\n%s" % (proc.returncode, proc.stdout, proc.stderr))
+    os.replace(tmp, out)
+    return out
+
+
 def build_library(verbose: bool = False) -> str:
-    """Compile the kernels (and the bench's stream probe) for gfx950; return the kernels' .so."""
+    """Compile the kernels (and the bench's stream probe) for gfx950, then the torch-tensor
+    fast path; return the kernels' .so."""
     os.makedirs(LIB_DIR, exist_ok=True)
     _hipcc(SRCS, LIB_PATH, verbose)
     _hipcc([PROBE_SRC], PROBE_LIB_PATH, verbose)
+    build_fastpath(verbose)
     return LIB_PATH
 
 

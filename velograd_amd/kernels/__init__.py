@@ -156,6 +156,15 @@ def _forward_fast(x: torch.Tensor, residual: Optional[torch.Tensor],
     """The common case without views or copies, for launch-latency-bound (decode) calls:
     contiguous tensors of one dtype on the current device, weight [D] in that dtype or fp32.
     Returns None when the call does not qualify (the general path then handles it)."""
+    fp = _lib.fastpath()
+    if fp is not None:
+        if not ((residual is None or isinstance(residual, torch.Tensor))
+                and (weight is None or isinstance(weight, torch.Tensor))):
+            return None
+        out = fp.forward(x, residual, weight, float(eps), float(min_mean_sq))
+        if not out:
+            return None
+        return out[0], (x if residual is None else out[1]), out[2]
     code = _lib.TORCH_DTYPE_CODES.get(x.dtype)
     if code is None or x.dim() == 0 or not x.is_contiguous():
         return None
