@@ -116,3 +116,45 @@ def test_launch_stream_is_torchs_current_stream():
     g.replay()
     torch.cuda.synchronize()
     assert torch.equal(yg, ref)
+
+
+def test_graph_replays_of_module_forms_and_interleaved_rope_match_eager():
+    """The module form (floor), the residual add with the floor, the backward through the fast
+    path's outputs, and the interleaved RoPE, captured together and replayed with new inputs."""
+    torch.manual_seed(2)
+    dev = torch.device("cuda", 0)
+    x = torch.randn(64, 4096, device=dev, dtype=torch.bfloat16)
+    r = torch.randn(64, 4096, device=dev, dtype=torch.bfloat16)
+    g = torch.randn(64, 4096, device=dev, dtype=torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(4096, device=dev)).to(torch.bfloat16)
+    q = torch.randn(2, 48, 1024, device=dev, dtype=torch.bfloat16)
+
+    def calls():
+        y1, inv1 = vk.rmsnorm_forward(x, w, 1e-6)
+        y2, h2, inv2 = vk.fused_rmsnorm_residual_forward(x, r, w, 1e-6, min_mean_sq=1e-12)
+        dx, dw = vk.fused_rmsnorm_residual_backward(g, h2, w, inv2, saved_is_h=True)
+        qi = vk.fused_rope_interleaved(q, 10000.0)
+        qb = vk.fused_rope_interleaved(qi, 10000.0, inverse=True)
+        return [y1, inv1, y2, h2, inv2, dx, dw, qi, qb]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            calls()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = calls()
+    for rep in range(3):
+        for t in (x, r, g, q):
+            t.copy_(torch.randn(t.shape, device=dev, dtype=t.dtype))
+        x[rep] = 0                       # a floored row in every replay
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = calls()
+        torch.cuda.synchronize()
+        for i, (got, want) in enumerate(zip(outs, ref)):
+            assert torch.equal(got, want), f"replay {rep}: output {i} differs from the eager call"
