@@ -428,14 +428,56 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2) -> dict:
     _lib.check(rc, "interleaved rope timed")
     ius = e0.elapsed_time(e1) * 1e3 / reps
     ibytes = 2 * tokens * hid * 2
-    del ibufs
+
+    # The model's attention-branch input (models/llama.py:48-49): RMSNorm then the interleaved
+    # RoPE, fused in one pass (velograd_rmsnorm_rope_fwd) and as two passes (module-form norm,
+    # then velograd_rope) over the same buffers.
+    w = (1 + 0.1 * torch.randn(hid, device=dev)).to(torch.bfloat16)
+    inv = torch.empty(tokens, device=dev)
+    mid = torch.empty(tokens, hid, device=dev, dtype=torch.bfloat16)
+    fused_fn, norm_fn = lib.velograd_rmsnorm_rope_fwd, lib.velograd_rmsnorm_fwd
+
+    def fstep(i):
+        x, out = ibufs[i % sets]
+        return fused_fn(x.data_ptr(), None, w.data_ptr(), out.data_ptr(), None, inv.data_ptr(),
+                        tokens, hid, hid, hid, hid, hid, tokens, _lib.DTYPE_BF16,
+                        _lib.DTYPE_BF16, 1e-6, 1e-12, 10000.0, sp)
+
+    def tstep(i):
+        x, out = ibufs[i % sets]
+        rc = norm_fn(x.data_ptr(), None, w.data_ptr(), mid.data_ptr(), None, inv.data_ptr(),
+                     tokens, hid, hid, hid, hid, hid, _lib.DTYPE_BF16, _lib.DTYPE_BF16, 1e-6,
+                     1e-12, sp)
+        return rc | fn(mid.data_ptr(), out.data_ptr(), 1, tokens, 1, hid, hid, 10000.0, 0,
+                       _lib.ROPE_INTERLEAVED, _lib.DTYPE_BF16, sp)
+
+    times = {}
+    for name, st in (("fused", fstep), ("two_pass", tstep)):
+        for i in range(sets * 2):
+            _lib.check(st(i), f"norm+rope {name} warm-up")
+        torch.cuda.synchronize()
+        e0.record(stream)
+        rc = 0
+        for i in range(reps):
+            rc |= st(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        _lib.check(rc, f"norm+rope {name} timed")
+        times[name] = e0.elapsed_time(e1) * 1e3 / reps
+    nbytes_fused = 2 * tokens * hid * 2 + hid * 2 + 4 * tokens
+    del ibufs, mid
     return {"rope_qk_us_mean": round(us, 2), "rope_qk_bytes": nbytes,
             "rope_qk_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
             "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5",
             "rope_interleaved_us_mean": round(ius, 2), "rope_interleaved_bytes": ibytes,
             "rope_interleaved_gbs": round(ibytes / (ius * 1e-6) / 1e9, 1),
             "rope_interleaved_workload": f"x [{tokens},{hid}] bf16, pairs (2i, 2i+1) over the "
-                                         f"hidden vector, base 1e4 (functional.apply_rotary_emb)"}
+                                         f"hidden vector, base 1e4 (functional.apply_rotary_emb)",
+            "norm_rope_fused_us_mean": round(times["fused"], 2),
+            "norm_rope_fused_gbs": round(nbytes_fused / (times["fused"] * 1e-6) / 1e9, 1),
+            "norm_rope_two_pass_us_mean": round(times["two_pass"], 2),
+            "norm_rope_workload": f"RMSNorm (1e-12 floor) then interleaved RoPE of x [{tokens},"
+                                  f"{hid}] bf16 (models/llama.py:48-49), fused vs two passes"}
 
 
 def measure(lib, config: str, steps: int, warmup: int, nsets: int, event_every: int,

@@ -84,6 +84,30 @@ VELOGRAD_API int32_t velograd_rmsnorm_fwd(
     int32_t dtype, int32_t w_dtype, float eps, float min_mean_sq, void* hip_stream);
 
 /*
+ * The reference model's attention-branch input in one pass: its module RMSNorm followed by its
+ * interleaved RoPE of the whole hidden vector (`normed_attn = attention_norm(x);
+ * F.apply_rotary_emb(normed_attn)`, python/velograd/models/llama.py:48-49, with nn.py:338-355
+ * and functional.py:287-315), optionally after a residual add:
+ *   h = x + residual;  mean_sq = max(min_mean_sq, mean(h^2));  n = h / sqrt(mean_sq + eps) * w
+ *   y_2i, y_2i+1 = n_2i cos - n_2i+1 sin, n_2i sin + n_2i+1 cos at angle pos * base^(-2i/dim)
+ * where pos = row % seq (rows hold [outer, seq] positions in order).  y is rotated in fp32
+ * before its single rounding.  inv_rms is the statistic of the norm, so the backward is
+ * velograd_rope(pairing = VELOGRAD_ROPE_INTERLEAVED, inverse = 1) of grad_y followed by
+ * velograd_rmsnorm_residual_bwd with saved = h.  No counterpart in the reference, which makes
+ * two passes (and two Python loops); it replaces that pair.
+ *
+ *   dim  : even.   seq : >= 1 and dividing rows.   base : finite, > 0.
+ * Other arguments as velograd_rmsnorm_fwd.
+ */
+VELOGRAD_API int32_t velograd_rmsnorm_rope_fwd(
+    const void* x, const void* residual, const void* weight,
+    void* y, void* h, float* inv_rms,
+    int64_t rows, int64_t dim,
+    int64_t ld_x, int64_t ld_res, int64_t ld_y, int64_t ld_h,
+    int64_t seq, int32_t dtype, int32_t w_dtype, float eps, float min_mean_sq, float base,
+    void* hip_stream);
+
+/*
  * Forward with an fp8 output epilogue: h and inv_rms as velograd_rmsnorm_residual_fwd, while y
  * leaves as fp8 E4M3 codes with one dequantisation scale per row, ready for an fp8 GEMM:
  *   amax = max |y| over the row (fp32 y, before any rounding; NaN if the row holds a NaN)

@@ -116,6 +116,29 @@ def test_rmsnorm_fwd_zero_rows_is_a_no_op(lib):
     assert _lib.last_error() == ""
 
 
+def _rmsnorm_rope_fwd(lib, **kw):
+    args = dict(x=16, residual=None, weight=None, y=32, h=None, inv_rms=None, rows=4, dim=64,
+                ld_x=64, ld_res=64, ld_y=64, ld_h=64, seq=2, dtype=2, w_dtype=2, eps=1e-6,
+                min_mean_sq=1e-12, base=10000.0, stream=None)
+    args.update(kw)
+    return lib.velograd_rmsnorm_rope_fwd(*args.values())
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dim=63, ld_x=63, ld_y=63), _lib.ERR_INVALID_ARGUMENT, "even dim"),
+    (dict(seq=0), _lib.ERR_INVALID_ARGUMENT, "seq >= 1"),
+    (dict(seq=3), _lib.ERR_INVALID_ARGUMENT, "dividing rows"),
+    (dict(base=0.0), _lib.ERR_INVALID_ARGUMENT, "base"),
+    (dict(base=float("nan")), _lib.ERR_INVALID_ARGUMENT, "base"),
+    (dict(min_mean_sq=-1.0), _lib.ERR_INVALID_ARGUMENT, "min_mean_sq"),
+    (dict(y=16), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(dtype=7), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+])
+def test_rmsnorm_rope_fwd_argument_errors(lib, kw, code, msg):
+    assert _rmsnorm_rope_fwd(lib, **kw) == code
+    assert msg in _lib.last_error() and "velograd_rmsnorm_rope_fwd" in _lib.last_error()
+
+
 def _fwd_fp8(lib, **kw):
     args = dict(x=16, residual=None, weight=None, y=32, y_scale=112, h=None, inv_rms=None,
                 rows=4, dim=64, ld_x=64, ld_res=64, ld_y=64, ld_h=64, dtype=2, w_dtype=2,

@@ -1,0 +1,119 @@
+"""The reference model's attention-branch input in one pass, `F.apply_rotary_emb(attention_norm(x))`
+(models/llama.py:48-49), through velograd_rmsnorm_rope_fwd, against the composition of the two
+pinned oracles: rmsnorm_module_forward (nn.py:338-355, float64, 1e-12 floor) then apply_rotary_emb
+(functional.py:287-315, float64).  Tolerance per rotated element: the angle-scaled RoPE bound of
+tests/_parity.py on the normalised pair, a float32 term for the norm, and half an output ulp for
+bf16/fp16; inv_rms |a-b|/(|b|+1e-6) <= 1e-5; h bit-exact.  The autograd module is checked against
+torch float64 autograd of rms_norm and the complex-number rotation."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fused_rmsnorm as ora
+from tests import _parity as P
+from velograd_amd import kernels as vk
+from velograd_amd import nn as vnn
+
+pytestmark = pytest.mark.gpu
+
+ROUNDING = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8 * 1.01, torch.float16: 2.0 ** -11 * 1.01}
+
+
+def _bound(n: np.ndarray, base: float) -> np.ndarray:
+    """Angle-scaled RoPE tolerance for pairs (n_2i, n_2i+1), plus a float32 term for the norm."""
+    seq, dim = n.shape[-2], n.shape[-1]
+    ang = np.arange(seq)[:, None] * base ** (-2.0 * np.arange(dim // 2) / dim)
+    mag = np.abs(n[..., 0::2]) + np.abs(n[..., 1::2])
+    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 * np.maximum(ang, 1.0) + 2.0 ** -21 + 2.0 ** -20) * mag
+    out = np.empty_like(n)
+    out[..., 0::2] = b
+    out[..., 1::2] = b
+    return out
+
+
+CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 8192), False),
+         (torch.float32, (3, 33, 1000), True), (torch.float16, (2, 50, 256), False),
+         (torch.bfloat16, (3, 5, 6), True), (torch.float32, (4, 2, 3, 40), False)]
+
+
+@pytest.mark.parametrize("dtype,shape,with_res", CASES,
+                         ids=[f"{str(c[0]).split('.')[-1]}-{'x'.join(map(str, c[1]))}-{c[2]}"
+                              for c in CASES])
+@pytest.mark.parametrize("base", [10000.0, 500000.0])
+def test_fused_norm_rope_matches_the_oracle_composition(dtype, shape, with_res, base):
+    print(f"rmsnorm_rope {dtype} {shape} res={with_res} base={base}", flush=True)
+    rng = np.random.default_rng(shape[-1] + len(shape))
+    xs = P.gaussian(rng, shape)
+    xs.reshape(-1, shape[-1])[0] = 0.0              # a floored row (mean square 0)
+    x = P.to_device(xs, dtype)
+    r = P.to_device(P.gaussian(rng, shape), dtype) if with_res else None
+    w = P.to_device(P.weight_vec(rng, shape[-1]), dtype)
+    y, h, inv = vk.rmsnorm_rope_forward(x, w, 1e-6, base, residual=r)
+    assert y.dtype == dtype and y.shape == x.shape and inv.shape == x.shape[:-1] + (1,)
+    h32 = P.upcast(x) + (P.upcast(r) if with_res else 0.0)
+    if with_res:
+        if dtype == torch.float32:
+            assert np.array_equal(P.upcast(h), h32)
+        else:
+            P.assert_within_ulp(h, h32, 0, "h")
+    else:
+        assert h is x
+    n, rinv = ora.rmsnorm_module_forward(h32.astype(np.float64), P.upcast(w).astype(np.float64),
+                                         1e-6)
+    want = ora.apply_rotary_emb(n, base)
+    assert P.rel_err(P.upcast(inv), rinv) <= P.FP32_REL_TOL
+    tol = _bound(n, base) + ROUNDING[dtype] * np.abs(want)
+    err = np.abs(P.upcast(y).astype(np.float64) - want)
+    assert np.all(err <= tol), float((err - tol).max())
+
+
+def test_fused_equals_the_two_pass_path_up_to_the_intermediate_rounding():
+    """fp32: the fused pass and rmsnorm_forward + fused_rope_interleaved agree closely (the
+    two-pass path rounds the normalised rows once more and uses the double-precision walk)."""
+    torch.manual_seed(0)
+    x = torch.randn(2, 256, 1024, device="cuda")
+    w = 1 + 0.1 * torch.randn(1024, device="cuda")
+    y, _, inv = vk.rmsnorm_rope_forward(x, w, 1e-6, 10000.0)
+    n, inv2 = vk.rmsnorm_forward(x, w, 1e-6)
+    y2 = vk.fused_rope_interleaved(n, 10000.0)
+    assert torch.equal(inv, inv2)
+    assert float((y - y2).abs().max()) < 2e-4
+
+
+def test_module_autograd_matches_torch_float64():
+    rng = np.random.default_rng(5)
+    b, s, d = 2, 40, 512
+    x32 = P.gaussian(rng, (b, s, d))
+    mod = vnn.RMSNormRoPE(d, eps=1e-6, base=10000.0).cuda()
+    with torch.no_grad():
+        mod.weight.copy_(torch.from_numpy(P.weight_vec(rng, d)))
+    x = torch.from_numpy(x32).cuda().requires_grad_(True)
+    y = mod(x)
+    g = torch.from_numpy(P.gaussian(rng, (b, s, d))).cuda()
+    y.backward(g)
+
+    t = torch.from_numpy(x32.astype(np.float64)).requires_grad_(True)
+    tw = mod.weight.detach().double().cpu().requires_grad_(True)
+    n = torch.nn.functional.rms_norm(t, (d,), tw, 1e-6)
+    z = torch.view_as_complex(n.reshape(b, s, d // 2, 2))
+    inv_freq = 10000.0 ** (-torch.arange(0, d, 2, dtype=torch.float64) / d)
+    ang = torch.arange(s, dtype=torch.float64)[:, None] * inv_freq[None, :]
+    ref = torch.view_as_real(z * torch.polar(torch.ones_like(ang), ang)).reshape(b, s, d)
+    ref.backward(g.double().cpu())
+    assert float((y.detach().double().cpu() - ref.detach()).abs().max()) < 1e-4
+    assert float((x.grad.double().cpu() - t.grad).abs().max()) < 1e-3 * float(t.grad.abs().max())
+    rw = tw.grad
+    assert float((mod.weight.grad.double().cpu() - rw).abs().max()) < 1e-3 * float(rw.abs().max())
+
+
+def test_errors():
+    x = torch.zeros(2, 4, 7, device="cuda")
+    with pytest.raises(ValueError):
+        vk.rmsnorm_rope_forward(x)                                  # odd dim
+    with pytest.raises(ValueError):
+        vk.rmsnorm_rope_forward(torch.zeros(8, device="cuda"))     # no seq axis
+    with pytest.raises(ValueError):
+        vk.rmsnorm_rope_forward(torch.zeros(2, 4, 8, device="cuda"), base=0.0)
+    with pytest.raises(TypeError):
+        vk.rmsnorm_rope_forward(np.zeros((2, 4, 8), np.float32))

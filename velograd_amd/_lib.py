@@ -63,6 +63,16 @@ SIGNATURES = {
          ctypes.c_float, ctypes.c_float,    # eps, min_mean_sq
          _c_ptr],                           # hip_stream
     ),
+    "velograd_rmsnorm_rope_fwd": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_ptr,            # x, residual, weight
+         _c_ptr, _c_ptr, _c_ptr,            # y, h, inv_rms
+         _c_i64, _c_i64,                    # rows, dim
+         _c_i64, _c_i64, _c_i64, _c_i64,    # ld_x, ld_res, ld_y, ld_h
+         _c_i64, _c_i32, _c_i32,            # seq, dtype, w_dtype
+         ctypes.c_float, ctypes.c_float,    # eps, min_mean_sq
+         ctypes.c_float, _c_ptr],           # base, hip_stream
+    ),
     "velograd_rmsnorm_residual_fwd_fp8": (
         _c_i32,
         [_c_ptr, _c_ptr, _c_ptr,            # x, residual, weight

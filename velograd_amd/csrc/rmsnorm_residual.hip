@@ -180,6 +180,9 @@ struct FwdArgs {
   int32_t tpr;
   float eps;
   float ms_floor;   // > 0: floor on mean(h^2) before eps (the reference module's clamp)
+  int64_t rope_seq;       // kOutRopeI: positions per outer index (row position = row % rope_seq)
+  int32_t rope_half;      // kOutRopeI: dim / 2
+  float rope_c_hi, rope_c_lo;  // kOutRopeI: log2(base) / half as an unevaluated float sum
 };
 
 struct BwdArgs {
@@ -203,6 +206,31 @@ constexpr int kOutDtype = 0;   // y in the activation dtype
 constexpr int kOutFp8Row = 1;  // y as e4m3 codes with one fp32 scale per row
 constexpr int kOutMxE4M3 = 2;  // MXFP8: e4m3 codes, one E8M0 scale per 32 elements
 constexpr int kOutMxE2M1 = 3;  // MXFP4: e2m1 nibbles (two per byte), one E8M0 scale per 32
+constexpr int kOutRopeI = 4;   // y rotated by the reference model's interleaved RoPE
+
+// The reference model's RoPE applied to y in registers (python/velograd/functional.py:287-315;
+// models/llama.py:48-49 rotates the normalised attention input): the pair (y_2i, y_2i+1) of a
+// row at position pos turns by pos * freq_i, freq_i = base^(-2i/dim) = 2^-(i * c) with
+// c = log2(base) / half.  c arrives as c_hi + c_lo (from double on the host) and i * c is formed
+// with its exact rounding error (FMA), so freq_i is within about one ulp of exp2f; the angle is
+// then taken in revolutions and reduced to [-1/2, 1/2] exactly before sincospi, so no
+// large-argument reduction runs.  About 3-4 float32 ulps of the angle in all.
+constexpr float kInv2Pi = 0.159154943091895335768883763372514362f;
+constexpr float kLn2 = 0.693147180559945309417232121458176568f;
+__device__ __forceinline__ void rope_pair(float& y0, float& y1, float pos, int i, float c_hi,
+                                          float c_lo) {
+  const float fi = (float)i;
+  const float e = fi * c_hi;
+  const float e_lo = __builtin_fmaf(fi, c_hi, -e) + fi * c_lo;   // the rest of i * c
+  const float freq = exp2f(-e) * (1.0f - e_lo * kLn2);
+  const float rev = (pos * freq) * kInv2Pi;
+  const float rr = rev - rintf(rev);
+  float s, c;
+  sincospif(2.0f * rr, &s, &c);
+  const float x0 = y0, x1 = y1;
+  y0 = x0 * c - x1 * s;                                                   // functional.py:313
+  y1 = x0 * s + x1 * c;                                                   // functional.py:314
+}
 
 // Largest value over aligned groups of L lanes (L = 4 or 8), on every lane of the group.
 template <int L>
@@ -302,6 +330,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
     for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
   };
 
+  static_assert(OUT != kOutRopeI, "the RoPE output runs in fwd_rope_kernel");
   if constexpr (OUT == kOutDtype) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -406,6 +435,143 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 }
 
 // ------------------------------------------------------------------------------------------
+// Forward with the model's RoPE on y (kOutRopeI), register-resident rows: a workgroup of one row
+// group walks kNormRopeRows consecutive rows, the next row's chunks in flight while the current
+// one reduces.  Each thread keeps the rotation (cos, sin) of its pairs in double and advances
+// it by one position per row (the rotation through freq_j, from a double sincos of freq_j), so a
+// sincospi per pair is evaluated only at the first row of the walk or where the position wraps
+// to 0 (a new outer index); evaluated per (row, pair) it made the fused pass VALU-bound, no
+// faster than two passes.  The start angle is reduced in revolutions before sincospi (about
+// 3-4 float32 ulps), the recurrence adds ~1e-16 per step.
+// ------------------------------------------------------------------------------------------
+constexpr int kNormRopeRows = 16;
+
+template <int DT, int WDT, int NV>
+__global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_rope_kernel(const FwdArgs a) {
+  using C = Codec<DT>;
+  constexpr int V = C::kVec;
+  constexpr int PP = V / 2;  // pairs per chunk
+  __shared__ float red[2][kMaxWavesPerRow];
+  const int tpr = blockDim.x;  // one row group per workgroup
+  const int lt = threadIdx.x;
+  const int nchunk = a.dim / V;
+  const bool has_res = a.res != nullptr;
+  const bool has_w = a.w != nullptr;
+  const bool write_h = has_res && a.h != nullptr;
+  const int64_t row0 = (int64_t)blockIdx.x * kNormRopeRows;
+  const int nrows = (int)((a.rows - row0) < kNormRopeRows ? (a.rows - row0) : kNormRopeRows);
+
+  WeightChunk<DT, WDT> wc[NV];
+  double cr[NV][PP], sr[NV][PP], cst[NV][PP], sst[NV][PP];
+  float fr[NV][PP];
+  auto load_row = [&](int64_t row, u32x4* xv, u32x4* rv) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      xv[k] = u32x4{0u, 0u, 0u, 0u};
+      rv[k] = u32x4{0u, 0u, 0u, 0u};
+      if (c < nchunk) {
+        xv[k] = load16_stream<DT>(a.x, row * a.ld_x + (int64_t)c * V);
+        if (has_res) rv[k] = load16_stream<DT>(a.res, row * a.ld_res + (int64_t)c * V);
+      }
+    }
+  };
+  u32x4 xv[NV], rv[NV];
+  load_row(row0, xv, rv);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = lt + k * tpr;
+    wc[k].load((has_w && c < nchunk) ? a.w : nullptr, (int64_t)c * V);
+#pragma unroll
+    for (int q = 0; q < PP; ++q) {
+      // freq_j = 2^-(j * c) with c = log2(base) / half split as c_hi + c_lo (see rope_pair)
+      const float fj = (float)(c * PP + q);
+      const float e = fj * a.rope_c_hi;
+      const float e_lo = __builtin_fmaf(fj, a.rope_c_hi, -e) + fj * a.rope_c_lo;
+      fr[k][q] = exp2f(-e) * (1.0f - e_lo * kLn2);
+      double sv, cv;
+      sincos((double)fr[k][q], &sv, &cv);
+      cst[k][q] = cv;
+      sst[k][q] = sv;
+    }
+  }
+
+  for (int it = 0; it < nrows; ++it) {
+    const int64_t row = row0 + it;
+    const int64_t pos = row % a.rope_seq;
+    if (it == 0 || pos == 0) {
+      // start rotation at this position: the angle in revolutions, reduced exactly, to sincospi
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+#pragma unroll
+        for (int q = 0; q < PP; ++q) {
+          const float rev = ((float)pos * fr[k][q]) * kInv2Pi;
+          float sv, cv;
+          sincospif(2.0f * (rev - rintf(rev)), &sv, &cv);
+          cr[k][q] = cv;
+          sr[k][q] = sv;
+        }
+      }
+    }
+    u32x4 xn[NV], rn[NV];
+    if (it + 1 < nrows) load_row(row + 1, xn, rn);
+
+    auto make_h = [&](int k, float* hf) {
+      C::unpack(xv[k], hf);
+      if (has_res) {
+        float rf[V];
+        C::unpack(rv[k], rf);
+#pragma unroll
+        for (int i = 0; i < V; ++i) hf[i] = hf[i] + rf[i];
+      }
+    };
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      float hf[V];
+      make_h(k, hf);
+#pragma unroll
+      for (int i = 0; i < V; ++i) ss += hf[i] * hf[i];
+      const int c = lt + k * tpr;
+      if (write_h && c < nchunk)
+        store16_stream<DT>(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf));
+    }
+    ss = row_sum(ss, tpr, 0, red[it & 1]);
+    const float mean_sq = floor_mean_sq(ss / (float)a.dim, a.ms_floor);
+    const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
+    if (lt == 0 && a.inv_rms != nullptr) a.inv_rms[row] = r;
+
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+      float hf[V], wf[V], yf[V];
+      make_h(k, hf);
+      wc[k].unpack(has_w, wf);
+#pragma unroll
+      for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
+#pragma unroll
+      for (int q = 0; q < PP; ++q) {
+        const float cv = (float)cr[k][q], sv = (float)sr[k][q];
+        const float y0 = yf[2 * q], y1 = yf[2 * q + 1];
+        yf[2 * q] = y0 * cv - y1 * sv;                                  // functional.py:313
+        yf[2 * q + 1] = y0 * sv + y1 * cv;                              // functional.py:314
+        const double cn = cr[k][q] * cst[k][q] - sr[k][q] * sst[k][q];
+        sr[k][q] = sr[k][q] * cst[k][q] + cr[k][q] * sst[k][q];
+        cr[k][q] = cn;
+      }
+      if (c < nchunk) store16_stream<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
+    }
+    if (it + 1 < nrows) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        xv[k] = xn[k];
+        rv[k] = rn[k];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
 // Forward, any dim / alignment: one row per workgroup, two passes over the row (the second
 // re-reads x and residual, normally from L2, and recomputes the identical fp32 h).
 // ------------------------------------------------------------------------------------------
@@ -439,6 +605,14 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
   };
   if constexpr (OUT == kOutDtype) {
     for (int j = threadIdx.x; j < a.dim; j += blockDim.x) C::store1(a.y, row * a.ld_y + j, y_at(j));
+  } else if constexpr (OUT == kOutRopeI) {
+    const float pos = (float)(row % a.rope_seq);
+    for (int i = threadIdx.x; i < a.rope_half; i += blockDim.x) {
+      float y0 = y_at(2 * i), y1 = y_at(2 * i + 1);
+      rope_pair(y0, y1, pos, i, a.rope_c_hi, a.rope_c_lo);
+      C::store1(a.y, row * a.ld_y + 2 * i, y0);
+      C::store1(a.y, row * a.ld_y + 2 * i + 1, y1);
+    }
   } else if constexpr (OUT == kOutMxE4M3 || OUT == kOutMxE2M1) {
     // MX epilogue (see fwd_vec_kernel): a third pass, one 32-element block per thread.
     constexpr int kEmax = OUT == kOutMxE4M3 ? vg_mx::kEmaxE4M3 : vg_mx::kEmaxE2M1;
@@ -786,13 +960,27 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
                        0, st, a);
     return;
   }
-  const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups));
-  const dim3 block(p.block);
-  switch (p.nv) {
-    case 1: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 1, OUT>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 2, OUT>), grid, block, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 3, OUT>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 4, OUT>), grid, block, 0, st, a); break;
+  if constexpr (OUT == kOutRopeI) {
+    // One chunk per thread (rows up to 1024 chunks: 8192 bf16/fp16, 4096 fp32 elements); more
+    // chunks would hold 16 more doubles per chunk and spill, so longer rows take the generic
+    // kernel.
+    if (p.nv != 1) {
+      hipLaunchKernelGGL((fwd_generic_kernel<DT, WDT, OUT>), dim3((uint32_t)a.rows),
+                         dim3(kGenericBlock), 0, st, a);
+      return;
+    }
+    hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, 1>),
+                       dim3((uint32_t)((a.rows + kNormRopeRows - 1) / kNormRopeRows)),
+                       dim3(p.tpr), 0, st, a);
+  } else {
+    const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups));
+    const dim3 block(p.block);
+    switch (p.nv) {
+      case 1: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 1, OUT>), grid, block, 0, st, a); break;
+      case 2: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 2, OUT>), grid, block, 0, st, a); break;
+      case 3: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 3, OUT>), grid, block, 0, st, a); break;
+      default: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 4, OUT>), grid, block, 0, st, a); break;
+    }
   }
 }
 
@@ -863,7 +1051,8 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
                 const void* weight, void* y, float* y_scale, uint8_t* mx_scale, int64_t ld_mx,
                 void* h, float* inv_rms, int64_t rows, int64_t dim, int64_t ld_x,
                 int64_t ld_res, int64_t ld_y, int64_t ld_h, int32_t dtype, int32_t w_dtype,
-                float eps, float ms_floor, void* hip_stream) {
+                float eps, float ms_floor, void* hip_stream, int64_t rope_seq = 0,
+                float rope_theta = 0.0f) {
   const bool mx = out == kOutMxE4M3 || out == kOutMxE2M1;
   if (!types_ok(dtype, w_dtype))
     return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
@@ -876,6 +1065,12 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
   if (!(ms_floor >= 0.0f) || !__builtin_isfinite(ms_floor))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
                 "%s: min_mean_sq=%g must be finite and >= 0", what, (double)ms_floor);
+  if (out == kOutRopeI && (dim % 2 != 0 || rope_seq < 1 || (rows > 0 && rows % rope_seq != 0) ||
+                           !(rope_theta > 0.0f) || !__builtin_isfinite(rope_theta)))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "%s: RoPE needs an even dim (%lld), seq >= 1 dividing rows (seq=%lld rows=%lld) "
+                "and a finite base > 0 (%g)",
+                what, (long long)dim, (long long)rope_seq, (long long)rows, (double)rope_theta);
   if (mx && dim % vg_mx::kBlock != 0)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
                 "%s: dim=%lld must be a multiple of the 32-element MX block", what,
@@ -944,11 +1139,18 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
   a.tpr = p.tpr;
   a.eps = eps;
   a.ms_floor = ms_floor;
+  a.rope_seq = rope_seq > 0 ? rope_seq : 1;
+  a.rope_half = (int32_t)(dim / 2);
+  const double c = (rope_theta > 0.0f && dim >= 2) ? log2((double)rope_theta) / (double)(dim / 2)
+                                                   : 0.0;
+  a.rope_c_hi = (float)c;
+  a.rope_c_lo = (float)(c - (double)a.rope_c_hi);
   hipStream_t st = static_cast<hipStream_t>(hip_stream);
   switch (out) {
     case kOutFp8Row: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutFp8Row>(a, p, st))); break;
     case kOutMxE4M3: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutMxE4M3>(a, p, st))); break;
     case kOutMxE2M1: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutMxE2M1>(a, p, st))); break;
+    case kOutRopeI: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutRopeI>(a, p, st))); break;
     default: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutDtype>(a, p, st))); break;
   }
   return check_launch(what);
@@ -990,6 +1192,16 @@ VELOGRAD_API int32_t velograd_rmsnorm_fwd(const void* x, const void* residual,
   return run_fwd("velograd_rmsnorm_fwd", kOutDtype, x, residual, weight, y, nullptr, nullptr, 0,
                  h, inv_rms, rows, dim, ld_x, ld_res, ld_y, ld_h, dtype, w_dtype, eps,
                  min_mean_sq, hip_stream);
+}
+
+VELOGRAD_API int32_t velograd_rmsnorm_rope_fwd(
+    const void* x, const void* residual, const void* weight, void* y, void* h, float* inv_rms,
+    int64_t rows, int64_t dim, int64_t ld_x, int64_t ld_res, int64_t ld_y, int64_t ld_h,
+    int64_t seq, int32_t dtype, int32_t w_dtype, float eps, float min_mean_sq, float base,
+    void* hip_stream) {
+  return run_fwd("velograd_rmsnorm_rope_fwd", kOutRopeI, x, residual, weight, y, nullptr,
+                 nullptr, 0, h, inv_rms, rows, dim, ld_x, ld_res, ld_y, ld_h, dtype, w_dtype, eps,
+                 min_mean_sq, hip_stream, seq, base);
 }
 
 VELOGRAD_API int32_t velograd_rmsnorm_residual_fwd_fp8(

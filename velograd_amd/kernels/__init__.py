@@ -52,6 +52,7 @@ __all__ = [
     "fused_rmsnorm_residual_forward_fp8",
     "fused_rmsnorm_residual_forward_mx",
     "rmsnorm_forward",
+    "rmsnorm_rope_forward",
     "fused_rope",
     "fused_rope_forward",
     "fused_rope_backward",
@@ -651,6 +652,54 @@ def rmsnorm_forward(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps:
         raise ValueError("rmsnorm_forward needs a non-empty last dimension")
     y, _, inv_rms = _forward_device(x, None, weight, eps, min_mean_sq=min_mean_sq)
     return y, inv_rms
+
+
+def rmsnorm_rope_forward(x: torch.Tensor, weight: Optional[torch.Tensor] = None,
+                         eps: float = 1e-6, base: float = 10000.0,
+                         residual: Optional[torch.Tensor] = None,
+                         min_mean_sq: float = 1e-12):
+    """The reference model's attention-branch input in one pass: `attention_norm(x)` (its
+    module RMSNorm, nn.py:338-355, with the 1e-12 floor) then `F.apply_rotary_emb` of the result
+    (functional.py:287-315, interleaved pairs, positions along axis -2), as models/llama.py:48-49
+    chains them; with `residual`, h = x + residual is normalised (and returned).
+
+    Returns (y, h, inv_rms): y the rotated normalised rows in x's dtype, h as
+    fused_rmsnorm_residual_forward (x itself without residual), inv_rms float32 [..., 1].  The
+    backward is the inverse rotation of grad_y (fused_rope_interleaved(..., inverse=True)) then
+    fused_rmsnorm_residual_backward with saved_is_h=True (nn.rms_norm_rope does both).  Device
+    tensors only; x is [..., seq, dim] with dim even.
+    """
+    if not _is_device_tensor(x):
+        raise TypeError("rmsnorm_rope_forward takes torch tensors on a ROCm device")
+    if x.dim() < 2:
+        raise ValueError("rmsnorm_rope_forward: x must be [..., seq, dim]")
+    min_mean_sq = _check_min_mean_sq(min_mean_sq)
+    seq, d = x.shape[-2], x.shape[-1]
+    if d % 2 != 0:
+        raise ValueError(f"rmsnorm_rope_forward: dim={d} must be even (RoPE pairs)")
+    code = _dtype_code(x, "x")
+    device = x.device
+    if residual is not None:
+        if (not isinstance(residual, torch.Tensor) or residual.device != device
+                or residual.dtype != x.dtype or residual.shape != x.shape):
+            raise ValueError("residual must be a tensor shaped and typed like x on its device")
+    w, wcode = _prep_weight(weight, d, x.dtype, device)
+    y = torch.empty(x.shape, dtype=x.dtype, device=device)
+    h = torch.empty(x.shape, dtype=x.dtype, device=device) if residual is not None else x
+    inv_rms = torch.empty(tuple(x.shape[:-1]) + (1,), dtype=torch.float32, device=device)
+    if x.numel() == 0:
+        return y, h, inv_rms
+    x2 = x.contiguous().view(-1, d)
+    r2 = residual.contiguous().view(-1, d) if residual is not None else None
+    rows = x2.shape[0]
+    with torch.cuda.device(device):
+        rc = _lib.load().velograd_rmsnorm_rope_fwd(
+            x2.data_ptr(), _ptr(r2), _ptr(w), y.data_ptr(),
+            h.data_ptr() if residual is not None else None, inv_rms.data_ptr(),
+            rows, d, d, d, d, d, seq, code, wcode, float(eps), min_mean_sq, float(base),
+            _stream(device))
+    _lib.check(rc, "velograd_rmsnorm_rope_fwd")
+    return y, h, inv_rms
 
 
 def fused_rmsnorm_residual(x: Any, residual: Optional[Any] = None, weight: Optional[Any] = None,

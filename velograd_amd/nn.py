@@ -17,6 +17,8 @@ gradient function (python/velograd/kernels/__init__.py:30-31).  Here:
   the module's floor on the mean square.
 * `FusedRoPEFunction` / `apply_rope(q, k, head_dim, theta)` — the fused RoPE kernel with its
   inverse-rotation backward.
+* `RMSNormRoPEFunction` / `rms_norm_rope` / `RMSNormRoPE` — the model's `attention_norm`
+  then `apply_rotary_emb` (`models/llama.py:48-49`) as one forward pass.
 * `RotaryEmbFunction` / `apply_rotary_emb(x, base)` — the reference model's RoPE
   (`functional.py:287-345`, interleaved pairs over the whole last axis, positions on axis -2)
   on the same kernel, with its inverse-rotation backward.
@@ -34,7 +36,8 @@ from . import kernels as _k
 
 __all__ = ["FusedRMSNormResidualFunction", "fused_add_rmsnorm", "RMSNormFunction", "rms_norm",
            "RMSNorm", "FusedAddRMSNorm", "FusedRoPEFunction", "apply_rope",
-           "RotaryEmbFunction", "apply_rotary_emb"]
+           "RotaryEmbFunction", "apply_rotary_emb", "RMSNormRoPEFunction", "rms_norm_rope",
+           "RMSNormRoPE"]
 
 # nn.py:349: mean_sq = max(1e-12, sum(x ** 2 for x in row) / dim)
 REFERENCE_MIN_MEAN_SQ = 1e-12
@@ -175,6 +178,58 @@ def apply_rope(q: torch.Tensor, k: Optional[torch.Tensor] = None,
     q_rot = FusedRoPEFunction.apply(q, head_dim, theta)
     k_rot = FusedRoPEFunction.apply(k, head_dim, theta) if k is not None else None
     return q_rot, k_rot
+
+
+class RMSNormRoPEFunction(torch.autograd.Function):
+    """`F.apply_rotary_emb(attention_norm(x))` of the reference's model (models/llama.py:48-49)
+    in one forward pass; the backward rotates grad_y back (one launch) and runs the fused
+    RMSNorm backward with the saved x (nn.py:357-383, functional.py:316-345 chained)."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, weight: Optional[torch.Tensor], eps: float, base: float,
+                min_mean_sq: float):
+        y, h, inv_rms = _k.rmsnorm_rope_forward(x, weight, eps, base, None, min_mean_sq)
+        ctx.save_for_backward(h, weight, inv_rms)
+        ctx.base = base
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y: torch.Tensor):
+        h, weight, inv_rms = ctx.saved_tensors
+        g = _k.fused_rope_interleaved(grad_y.contiguous(), ctx.base, inverse=True)
+        dx, dweight = _k.fused_rmsnorm_residual_backward(g, h, weight, inv_rms, saved_is_h=True)
+        need_x, need_w = ctx.needs_input_grad[:2]
+        if dweight is not None and weight is not None and dweight.dtype != weight.dtype:
+            dweight = dweight.to(weight.dtype)
+        return (dx if need_x else None,
+                dweight.view_as(weight) if (need_w and dweight is not None) else None,
+                None, None, None)
+
+
+def rms_norm_rope(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                  base: float = 10000.0,
+                  min_mean_sq: float = REFERENCE_MIN_MEAN_SQ) -> torch.Tensor:
+    """Differentiable `apply_rotary_emb(RMSNorm(x))` with the reference's semantics, fused."""
+    return RMSNormRoPEFunction.apply(x, weight, eps, base, min_mean_sq)
+
+
+class RMSNormRoPE(torch.nn.Module):
+    """The reference block's `attention_norm` followed by `F.apply_rotary_emb`
+    (models/llama.py:44,48-49) as one module: weight [dim] initialised to ones (nn.py:334)."""
+
+    def __init__(self, dim: int, eps: float = 1e-6, base: float = 10000.0, device=None,
+                 dtype=None):
+        super().__init__()
+        self.dim = dim
+        self.eps = eps
+        self.base = base
+        self.weight = torch.nn.Parameter(torch.ones(dim, device=device, dtype=dtype))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return rms_norm_rope(x, self.weight, self.eps, self.base, REFERENCE_MIN_MEAN_SQ)
+
+    def extra_repr(self) -> str:
+        return f"{self.dim}, eps={self.eps}, base={self.base}"
 
 
 class RotaryEmbFunction(torch.autograd.Function):
