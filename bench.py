@@ -74,6 +74,10 @@ def parse_args(argv=None):
                    help="skip the config E decode-latency table (reported under extra)")
     p.add_argument("--no-rope", action="store_true",
                    help="skip timing the fused RoPE kernel (reported under extra)")
+    p.add_argument("--no-norm-rope", action="store_true",
+                   help="skip the fused versus two-pass RMSNorm + RoPE timing (its two-pass leg "
+                        "runs the forward kernel at another shape, which would mix into a "
+                        "per-kernel profile of the headline forward)")
     p.add_argument("--no-torch-baseline", action="store_true",
                    help="skip the PyTorch eager comparison and the reference benchmark's shapes")
     p.add_argument("--no-copy-ceiling", action="store_true",
@@ -362,7 +366,7 @@ def decode_latency(lib, stream, calls: int = 1000) -> list:
     return out
 
 
-def rope_timing(lib, tokens: int, stream, sets: int = 2) -> dict:
+def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True) -> dict:
     """Fused RoPE (velograd_rope) on a Llama-3-8B-like attention input of the same token
     count: q [tokens, 32, 128] and k [tokens, 8, 128] bf16, theta 500000, one launch each per
     step, rotating over `sets` buffer sets.  Bytes: q and k read once and written once."""
@@ -429,6 +433,17 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2) -> dict:
     ius = e0.elapsed_time(e1) * 1e3 / reps
     ibytes = 2 * tokens * hid * 2
 
+    out = {"rope_qk_us_mean": round(us, 2), "rope_qk_bytes": nbytes,
+           "rope_qk_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5",
+           "rope_interleaved_us_mean": round(ius, 2), "rope_interleaved_bytes": ibytes,
+           "rope_interleaved_gbs": round(ibytes / (ius * 1e-6) / 1e9, 1),
+           "rope_interleaved_workload": f"x [{tokens},{hid}] bf16, pairs (2i, 2i+1) over the "
+                                        f"hidden vector, base 1e4 (functional.apply_rotary_emb)"}
+    if not norm_rope:
+        del ibufs
+        return out
+
     # The model's attention-branch input (models/llama.py:48-49): RMSNorm then the interleaved
     # RoPE, fused in one pass (velograd_rmsnorm_rope_fwd) and as two passes (module-form norm,
     # then velograd_rope) over the same buffers.
@@ -466,18 +481,13 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2) -> dict:
         times[name] = e0.elapsed_time(e1) * 1e3 / reps
     nbytes_fused = 2 * tokens * hid * 2 + hid * 2 + 4 * tokens
     del ibufs, mid
-    return {"rope_qk_us_mean": round(us, 2), "rope_qk_bytes": nbytes,
-            "rope_qk_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5",
-            "rope_interleaved_us_mean": round(ius, 2), "rope_interleaved_bytes": ibytes,
-            "rope_interleaved_gbs": round(ibytes / (ius * 1e-6) / 1e9, 1),
-            "rope_interleaved_workload": f"x [{tokens},{hid}] bf16, pairs (2i, 2i+1) over the "
-                                         f"hidden vector, base 1e4 (functional.apply_rotary_emb)",
-            "norm_rope_fused_us_mean": round(times["fused"], 2),
-            "norm_rope_fused_gbs": round(nbytes_fused / (times["fused"] * 1e-6) / 1e9, 1),
-            "norm_rope_two_pass_us_mean": round(times["two_pass"], 2),
-            "norm_rope_workload": f"RMSNorm (1e-12 floor) then interleaved RoPE of x [{tokens},"
-                                  f"{hid}] bf16 (models/llama.py:48-49), fused vs two passes"}
+    out.update({
+        "norm_rope_fused_us_mean": round(times["fused"], 2),
+        "norm_rope_fused_gbs": round(nbytes_fused / (times["fused"] * 1e-6) / 1e9, 1),
+        "norm_rope_two_pass_us_mean": round(times["two_pass"], 2),
+        "norm_rope_workload": f"RMSNorm (1e-12 floor) then interleaved RoPE of x [{tokens},"
+                              f"{hid}] bf16 (models/llama.py:48-49), fused vs two passes"})
+    return out
 
 
 def measure(lib, config: str, steps: int, warmup: int, nsets: int, event_every: int,
@@ -765,7 +775,7 @@ def main(argv=None) -> int:
         if d % 32 == 0:
             extra.update(mx_forward_timing(lib, sets, rows, d, s, code, eps, stream))
     if not args.no_rope:
-        extra.update(rope_timing(lib, rows, stream))
+        extra.update(rope_timing(lib, rows, stream, norm_rope=not args.no_norm_rope))
     if not args.no_torch_baseline:
         extra.update(torch_eager_timing(sets, rows, d, s, eps, with_bwd, stream))
         extra["speedup_vs_torch_eager"] = round(
