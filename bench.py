@@ -466,8 +466,14 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True)
         return rc | fn(mid.data_ptr(), out.data_ptr(), 1, tokens, 1, hid, hid, 10000.0, 0,
                        _lib.ROPE_INTERLEAVED, _lib.DTYPE_BF16, sp)
 
+    def nstep(i):
+        x, out = ibufs[i % sets]
+        return norm_fn(x.data_ptr(), None, w.data_ptr(), out.data_ptr(), None, inv.data_ptr(),
+                       tokens, hid, hid, hid, hid, hid, _lib.DTYPE_BF16, _lib.DTYPE_BF16, 1e-6,
+                       1e-12, sp)
+
     times = {}
-    for name, st in (("fused", fstep), ("two_pass", tstep)):
+    for name, st in (("fused", fstep), ("two_pass", tstep), ("norm_only", nstep)):
         for i in range(sets * 2):
             _lib.check(st(i), f"norm+rope {name} warm-up")
         torch.cuda.synchronize()
@@ -485,6 +491,9 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True)
         "norm_rope_fused_us_mean": round(times["fused"], 2),
         "norm_rope_fused_gbs": round(nbytes_fused / (times["fused"] * 1e-6) / 1e9, 1),
         "norm_rope_two_pass_us_mean": round(times["two_pass"], 2),
+        # the module-form RMSNorm alone (nn.py:338-355: x read, y written, no residual)
+        "norm_module_us_mean": round(times["norm_only"], 2),
+        "norm_module_gbs": round(nbytes_fused / (times["norm_only"] * 1e-6) / 1e9, 1),
         "norm_rope_workload": f"RMSNorm (1e-12 floor) then interleaved RoPE of x [{tokens},"
                               f"{hid}] bf16 (models/llama.py:48-49), fused vs two passes"})
     return out

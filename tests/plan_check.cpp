@@ -68,9 +68,11 @@ int main() {
         for (int prefer = -1; prefer <= kMaxNV + 1; ++prefer) {
           check_row_plan(plan_rows(dim, eb, aligned != 0, prefer, kFwdOrder), dim, eb,
                          aligned != 0);
+          check_row_plan(plan_rows(dim, eb, aligned != 0, prefer, kFwdOrderOneStream), dim, eb,
+                         aligned != 0);
           check_row_plan(plan_rows(dim, eb, aligned != 0, prefer, kBwdOrder), dim, eb,
                          aligned != 0);
-          plans += 2;
+          plans += 3;
         }
       }
     }

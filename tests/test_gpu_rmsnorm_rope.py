@@ -70,14 +70,17 @@ def test_fused_norm_rope_matches_the_oracle_composition(dtype, shape, with_res, 
 
 def test_fused_equals_the_two_pass_path_up_to_the_intermediate_rounding():
     """fp32: the fused pass and rmsnorm_forward + fused_rope_interleaved agree closely (the
-    two-pass path rounds the normalised rows once more and uses the double-precision walk)."""
+    two-pass path rounds the normalised rows once more and uses the double-precision walk).
+    The row statistic is the same fp32 sum of squares taken in another order (the module-form
+    norm without a residual reads two 16-byte chunks per thread, the fused pass one), so the
+    two inv_rms agree to a couple of ulps rather than bit for bit."""
     torch.manual_seed(0)
     x = torch.randn(2, 256, 1024, device="cuda")
     w = 1 + 0.1 * torch.randn(1024, device="cuda")
     y, _, inv = vk.rmsnorm_rope_forward(x, w, 1e-6, 10000.0)
     n, inv2 = vk.rmsnorm_forward(x, w, 1e-6)
     y2 = vk.fused_rope_interleaved(n, 10000.0)
-    assert torch.equal(inv, inv2)
+    assert P.rel_err(P.upcast(inv), P.upcast(inv2)) <= 2.0 ** -21
     assert float((y - y2).abs().max()) < 2e-4
 
 

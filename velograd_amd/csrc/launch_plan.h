@@ -41,10 +41,14 @@ struct RowPlan {
 };
 
 // Automatic orders in which chunks-per-thread values are tried (measured on MI355X, bf16 rows of
-// 4096 and 8192): the forward is fastest with one chunk per thread (more waves per row, all of
-// a row's loads in one instruction per lane); the persistent backward with two (it keeps the
-// next row's chunks in flight too, so it trades waves for bytes per lane).
+// 4096 and 8192): the forward with a residual (two streams read, two written) is fastest with
+// one chunk per thread (more waves per row, all of a row's loads in one instruction per lane);
+// without one (x read, y written) with two, since one 16-byte load per lane leaves too few
+// bytes in flight (16384 x 4096: 44.5 us against 51.0 us, the plain copy's speed); the
+// persistent backward with two (it keeps the next row's chunks in flight too, so it trades
+// waves for bytes per lane).
 constexpr int kFwdOrder[kMaxNV] = {1, 2, 3, 4};
+constexpr int kFwdOrderOneStream[kMaxNV] = {2, 4, 3, 1};
 constexpr int kBwdOrder[kMaxNV] = {2, 3, 4, 1};
 
 // Register-resident layout for rows of `dim` elements of `elem_bytes` bytes, or the generic

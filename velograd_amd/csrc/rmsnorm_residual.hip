@@ -938,8 +938,10 @@ const Tuning& tuning() {
   return t;
 }
 
-RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned) {
-  return vg_plan::plan_rows(dim, elem_bytes, aligned, tuning().fwd_nv, vg_plan::kFwdOrder);
+// `one_stream`: no residual, so the row kernel reads x and writes y only.
+RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned, bool one_stream) {
+  return vg_plan::plan_rows(dim, elem_bytes, aligned, tuning().fwd_nv,
+                            one_stream ? vg_plan::kFwdOrderOneStream : vg_plan::kFwdOrder);
 }
 
 BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus) {
@@ -1115,7 +1117,9 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
   const bool aligned = aligned16(x) && ld_ok(ld_x, eb) && y_aligned &&
                        (!residual || (aligned16(residual) && ld_ok(ld_res, eb))) &&
                        (!h || (aligned16(h) && ld_ok(ld_h, eb))) && (!weight || aligned16(weight));
-  const RowPlan p = plan_fwd(dim, eb, aligned);
+  // The fused norm + RoPE kernel holds one chunk per thread, so it keeps the residual order
+  // (one chunk first) either way.
+  const RowPlan p = plan_fwd(dim, eb, aligned, residual == nullptr && out != kOutRopeI);
   if (!vg_plan::row_plan_valid(p, dim, eb))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: internal launch plan rejected (dim=%lld)",
                 what, (long long)dim);
