@@ -175,7 +175,8 @@ def load_traffic(config: str):
 def stream_ceilings(sets, stream_bytes: int, stream) -> dict:
     """Same-run practical ceiling: plain streaming kernels (velograd_amd/csrc/stream_probe.hip)
     with the forward's (2 reads + 2 writes) and the backward's (2 reads + 1 write) byte pattern
-    over tensors of the workload's size, rotating over the same buffer sets (cold MALL)."""
+    over tensors of the workload's size, rotating over the same buffer sets (cold MALL); plus the
+    same streams read only and written only, which show what mixing the two directions costs."""
     import ctypes
 
     import torch
@@ -193,7 +194,9 @@ def stream_ceilings(sets, stream_bytes: int, stream) -> dict:
     out = {}
     for name, pattern, nstreams, keys in (("copy", 0, 2, ("x", None, "y", None)),
                                           ("fwd_pattern", 1, 4, ("x", "res", "y", "h")),
-                                          ("bwd_pattern", 2, 3, ("x", "res", "y", None))):
+                                          ("bwd_pattern", 2, 3, ("x", "res", "y", None)),
+                                          ("read_only", 3, 2, ("x", "res", "y", None)),
+                                          ("write_only", 4, 2, ("x", None, "y", "h"))):
         def run(i):
             b = sets[i % len(sets)]
             ptrs = [b[k].data_ptr() if k else None for k in keys]

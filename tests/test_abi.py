@@ -287,3 +287,21 @@ def test_last_error_is_per_thread(lib):
     assert seen["b"][0] == _lib.ERR_INVALID_ARGUMENT and "invalid shape" in seen["b"][1]
     # this thread's own last error is untouched by the workers
     assert _fwd(lib, rows=0, x=None, y=None) == 0 and _lib.last_error() == ""
+
+
+def test_stream_probe_rejects_bad_arguments():
+    """The bench's same-run ceiling probe checks its arguments before launching anything."""
+    from velograd_amd.build import PROBE_LIB_PATH
+    if not os.path.exists(PROBE_LIB_PATH):
+        pytest.skip("stream probe not built")
+    fn = ctypes.CDLL(PROBE_LIB_PATH).velograd_stream_probe
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p]
+    p = 4096  # never dereferenced: every call below fails its argument check first
+    assert fn(0, p, p, p, p, 0, None) == -1            # no vectors
+    assert fn(0, None, p, p, p, 16, None) == -1        # no source
+    assert fn(1, p, None, p, p, 16, None) == -1        # fwd pattern: second source missing
+    assert fn(1, p, p, p, None, 16, None) == -1        # fwd pattern: second output missing
+    assert fn(3, p, None, p, None, 16, None) == -1     # read-only: second source missing
+    assert fn(4, p, None, p, None, 16, None) == -1     # write-only: second output missing
+    assert fn(9, p, p, p, p, 16, None) == -1           # unknown pattern

@@ -3,6 +3,10 @@
 //   pattern 0  copy     1 read  + 1 write
 //   pattern 1  fwd-like 2 reads + 2 writes   (x, residual -> h, y)
 //   pattern 2  bwd-like 2 reads + 1 write    (grad_y, h -> dx)
+//   pattern 3  read-only  2 reads            (stores only on a 128-bit value random data never
+//                                             holds, so the loads cannot be removed)
+//   pattern 4  write-only 2 writes
+// Patterns 3 and 4 bound what mixing reads and writes costs: the same streams, one direction.
 // Each thread moves two 16-byte vectors per stream with non-temporal accesses, one pass over
 // the buffers (no grid-stride loop): the fastest shape found by a sweep over vectors per
 // thread, workgroup size, grid size and cache policy on MI355X.
@@ -25,8 +29,9 @@ __global__ __launch_bounds__(kBlock) void stream_kernel(const u32x4* a, const u3
 #pragma unroll
   for (int k = 0; k < kPerThread; ++k) {
     const int64_t i = base + (int64_t)k * kBlock;
+    va[k] = u32x4{(uint32_t)i, 1u, 2u, 3u};
     if (i < n16) {
-      va[k] = __builtin_nontemporal_load(a + i);
+      if (NR >= 1) va[k] = __builtin_nontemporal_load(a + i);
       if (NR == 2) vb[k] = __builtin_nontemporal_load(b + i);
     }
   }
@@ -36,8 +41,13 @@ __global__ __launch_bounds__(kBlock) void stream_kernel(const u32x4* a, const u3
     if (i < n16) {
       u32x4 v = va[k];
       if (NR == 2) v += vb[k];
-      __builtin_nontemporal_store(v, c + i);
-      if (NW == 2) __builtin_nontemporal_store(v ^ u32x4{1u, 1u, 1u, 1u}, d + i);
+      if (NW == 0) {
+        if (v.x == 0x9E3779B9u && v.y == 0x7F4A7C15u && v.z == 0xF39CC060u && v.w == 0x5CEDC834u)
+          c[i] = v;
+      } else {
+        __builtin_nontemporal_store(v, c + i);
+        if (NW == 2) __builtin_nontemporal_store(v ^ u32x4{1u, 1u, 1u, 1u}, d + i);
+      }
     }
   }
 }
@@ -51,8 +61,8 @@ extern "C" VELOGRAD_API int32_t velograd_stream_probe(int32_t pattern, const voi
                                                       const void* b, void* c, void* d,
                                                       int64_t n16, void* hip_stream) {
   if (n16 <= 0 || a == nullptr || c == nullptr) return -1;
-  if ((pattern == 1 || pattern == 2) && b == nullptr) return -1;
-  if (pattern == 1 && d == nullptr) return -1;
+  if ((pattern == 1 || pattern == 2 || pattern == 3) && b == nullptr) return -1;
+  if ((pattern == 1 || pattern == 4) && d == nullptr) return -1;
   const int64_t grid = (n16 + (int64_t)kBlock * kPerThread - 1) / ((int64_t)kBlock * kPerThread);
   if (grid > INT32_MAX) return -1;
   hipStream_t st = static_cast<hipStream_t>(hip_stream);
@@ -64,6 +74,8 @@ extern "C" VELOGRAD_API int32_t velograd_stream_probe(int32_t pattern, const voi
     case 0: hipLaunchKernelGGL((stream_kernel<1, 1>), dim3(grid), dim3(kBlock), 0, st, A, B, C, D, n16); break;
     case 1: hipLaunchKernelGGL((stream_kernel<2, 2>), dim3(grid), dim3(kBlock), 0, st, A, B, C, D, n16); break;
     case 2: hipLaunchKernelGGL((stream_kernel<2, 1>), dim3(grid), dim3(kBlock), 0, st, A, B, C, D, n16); break;
+    case 3: hipLaunchKernelGGL((stream_kernel<2, 0>), dim3(grid), dim3(kBlock), 0, st, A, B, C, D, n16); break;
+    case 4: hipLaunchKernelGGL((stream_kernel<0, 2>), dim3(grid), dim3(kBlock), 0, st, A, B, C, D, n16); break;
     default: return -1;
   }
   return (int32_t)hipGetLastError();
