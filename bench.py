@@ -75,9 +75,8 @@ def parse_args(argv=None):
     p.add_argument("--no-rope", action="store_true",
                    help="skip timing the fused RoPE kernel (reported under extra)")
     p.add_argument("--no-norm-rope", action="store_true",
-                   help="skip the fused versus two-pass RMSNorm + RoPE timing (its two-pass leg "
-                        "runs the forward kernel at another shape, which would mix into a "
-                        "per-kernel profile of the headline forward)")
+                   help="skip the fused versus two-pass RMSNorm + RoPE timing and the "
+                        "module-form norm on its buffers")
     p.add_argument("--no-torch-baseline", action="store_true",
                    help="skip the PyTorch eager comparison and the reference benchmark's shapes")
     p.add_argument("--no-copy-ceiling", action="store_true",
