@@ -709,12 +709,13 @@ def reference_benchmark_shapes(stream, calls: int = 500) -> dict:
 
 
 def other_configs(lib, main_config: str, stream) -> dict:
-    """The other bandwidth configurations at modest step counts (B forward, D forward +
-    backward, C when it is not the headline), reported under extra."""
+    """The other configurations at modest step counts (A forward, the reference's own fp32 case:
+    6.3 MB per step, so launch-bound and MALL-resident; B forward; D forward + backward; C when it
+    is not the headline), reported under extra."""
     import torch
 
     out = {}
-    for cfg, steps, nsets in (("B", 100, 4), ("C", 100, 4), ("D", 40, 2)):
+    for cfg, steps, nsets in (("A", 2000, 4), ("B", 100, 4), ("C", 100, 4), ("D", 40, 2)):
         if cfg == main_config:
             continue
         m = measure(lib, cfg, steps, 5, nsets, 5, stream)
