@@ -488,8 +488,49 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True)
         _lib.check(rc, f"norm+rope {name} timed")
         times[name] = e0.elapsed_time(e1) * 1e3 / reps
     nbytes_fused = 2 * tokens * hid * 2 + hid * 2 + 4 * tokens
-    del ibufs, mid
+
+    # Its backward: grad_y rotated back and the norm's backward in one pass
+    # (velograd_rmsnorm_rope_bwd), against the two passes (velograd_rope inverse into `mid`,
+    # then velograd_rmsnorm_residual_bwd).  grad_y is the forward's output buffer, h is x.
+    from velograd_amd import kernels as vk
+    dxb = torch.empty(tokens, hid, device=dev, dtype=torch.bfloat16)
+    dwb = torch.empty(hid, device=dev, dtype=torch.float32)
+    ws_bytes = vk.bwd_workspace_bytes(tokens, hid, dev)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    rope_bwd_fn, bwd_fn = lib.velograd_rmsnorm_rope_bwd, lib.velograd_rmsnorm_residual_bwd
+
+    def bstep(i):
+        x, gy = ibufs[i % sets]
+        return rope_bwd_fn(gy.data_ptr(), x.data_ptr(), w.data_ptr(), inv.data_ptr(),
+                           dxb.data_ptr(), dwb.data_ptr(), ws.data_ptr(), ws_bytes, tokens, hid,
+                           hid, hid, hid, tokens, _lib.DTYPE_BF16, _lib.DTYPE_BF16, 10000.0, sp)
+
+    def b2step(i):
+        x, gy = ibufs[i % sets]
+        rc = fn(gy.data_ptr(), mid.data_ptr(), 1, tokens, 1, hid, hid, 10000.0, 1,
+                _lib.ROPE_INTERLEAVED, _lib.DTYPE_BF16, sp)
+        return rc | bwd_fn(mid.data_ptr(), x.data_ptr(), 1, w.data_ptr(), inv.data_ptr(), None,
+                           dxb.data_ptr(), None, dwb.data_ptr(), ws.data_ptr(), ws_bytes, tokens,
+                           hid, hid, hid, hid, hid, hid, _lib.DTYPE_BF16, _lib.DTYPE_BF16, sp)
+
+    for name, st in (("bwd_fused", bstep), ("bwd_two_pass", b2step)):
+        for i in range(sets * 2):
+            _lib.check(st(i), f"norm+rope {name} warm-up")
+        torch.cuda.synchronize()
+        e0.record(stream)
+        rc = 0
+        for i in range(reps):
+            rc |= st(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        _lib.check(rc, f"norm+rope {name} timed")
+        times[name] = e0.elapsed_time(e1) * 1e3 / reps
+    nbytes_bwd = 3 * tokens * hid * 2 + hid * 2 + 4 * tokens + 4 * hid
+    del ibufs, mid, dxb, ws
     out.update({
+        "norm_rope_bwd_fused_us_mean": round(times["bwd_fused"], 2),
+        "norm_rope_bwd_fused_gbs": round(nbytes_bwd / (times["bwd_fused"] * 1e-6) / 1e9, 1),
+        "norm_rope_bwd_two_pass_us_mean": round(times["bwd_two_pass"], 2),
         "norm_rope_fused_us_mean": round(times["fused"], 2),
         "norm_rope_fused_gbs": round(nbytes_fused / (times["fused"] * 1e-6) / 1e9, 1),
         "norm_rope_two_pass_us_mean": round(times["two_pass"], 2),

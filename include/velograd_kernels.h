@@ -93,8 +93,9 @@ VELOGRAD_API int32_t velograd_rmsnorm_fwd(
  * where pos = row % seq (rows hold [outer, seq] positions in order).  y is rotated in fp32
  * before its single rounding.  inv_rms is the statistic of the norm, so the backward is
  * velograd_rope(pairing = VELOGRAD_ROPE_INTERLEAVED, inverse = 1) of grad_y followed by
- * velograd_rmsnorm_residual_bwd with saved = h.  No counterpart in the reference, which makes
- * two passes (and two Python loops); it replaces that pair.
+ * velograd_rmsnorm_residual_bwd with saved = h, or both in one pass:
+ * velograd_rmsnorm_rope_bwd.  No counterpart in the reference, which makes two passes (and two
+ * Python loops); it replaces that pair.
  *
  *   dim  : even.   seq : >= 1 and dividing rows.   base : finite, > 0.
  * Other arguments as velograd_rmsnorm_fwd.
@@ -199,8 +200,32 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
     int32_t dtype, int32_t w_dtype, void* hip_stream);
 
 /*
- * Workspace needed by velograd_rmsnorm_residual_bwd for dweight on `device` (a HIP device
- * ordinal).  No counterpart in the reference, whose NumPy backward allocates its own
+ * Backward of velograd_rmsnorm_rope_fwd in one pass: grad_y (the gradient of the rotated y) is
+ * rotated back pair by pair in registers, (g_2i, g_2i+1) -> (g_2i cos + g_2i+1 sin,
+ * g_2i+1 cos - g_2i sin) at the forward's angles (the rotation's backward, functional.py:316-345),
+ * then the norm's backward runs on it as velograd_rmsnorm_residual_bwd does with saved = h
+ * (nn.py:357-383 for the module form; fused.py:48-66):
+ *   dx = inv_rms * (gw - xhat * mean(gw * xhat)),  gw = g * w,  xhat = h * inv_rms,
+ *   dweight = sum over rows of g * xhat.
+ * One HBM pass over grad_y, h and dx instead of two over grad_y.  With a residual in the
+ * forward, dx is also the gradient of the residual.  No counterpart in the reference (two
+ * passes there).
+ *
+ *   grad_y, h, dx : [rows, dim] in `dtype` (unit stride along dim; row strides ld_*).
+ *   weight, inv_rms, dweight, workspace, ws_bytes : as velograd_rmsnorm_residual_bwd (the size
+ *                 query covers this entry point's plans too).
+ *   seq, base     : as velograd_rmsnorm_rope_fwd (even dim, seq >= 1 dividing rows, finite
+ *                 base > 0).
+ */
+VELOGRAD_API int32_t velograd_rmsnorm_rope_bwd(
+    const void* grad_y, const void* h, const void* weight, const float* inv_rms,
+    void* dx, float* dweight, void* workspace, size_t ws_bytes,
+    int64_t rows, int64_t dim, int64_t ld_g, int64_t ld_h, int64_t ld_dx,
+    int64_t seq, int32_t dtype, int32_t w_dtype, float base, void* hip_stream);
+
+/*
+ * Workspace needed by velograd_rmsnorm_residual_bwd and velograd_rmsnorm_rope_bwd for dweight
+ * on `device` (a HIP device ordinal).  No counterpart in the reference, whose NumPy backward allocates its own
  * temporaries (fused.py:58-65); returns 0 if the device cannot be queried.
  */
 VELOGRAD_API size_t velograd_rmsnorm_residual_bwd_workspace_bytes(int64_t rows, int64_t dim,

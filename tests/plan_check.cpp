@@ -102,6 +102,18 @@ int main() {
                   CHECK(b.lds_bytes <= 64 * 1024, "lds %zu", b.lds_bytes);
                   CHECK(b.lds_bytes == 0 || (b.rp.vec && b.rp.groups > 1),
                         "lds without a group combine");
+                  // the fused-RoPE plan: same facts, its own block bound, and its step table
+                  // (dim floats of LDS) within 64 KiB
+                  const BwdPlan br =
+                      plan_bwd_rope(rows, dim, eb, aligned != 0, cus, prefer, max_block, waves);
+                  check_row_plan(br.rp, dim, eb, aligned != 0);
+                  CHECK(!br.rp.vec || br.rp.block <= max_block_for_nv_rope(br.rp.nv),
+                        "rope block %d over its bound for nv %d", br.rp.block, br.rp.nv);
+                  CHECK(!br.rp.vec || dim * 4 <= 64 * 1024, "rope step table %lld floats",
+                        (long long)dim);
+                  CHECK((size_t)br.wgs * (size_t)dim * sizeof(float) <= ws,
+                        "rope partials %lld x %lld exceed workspace %zu", (long long)br.wgs,
+                        (long long)dim, ws);
                   ++plans;
                 }
               }

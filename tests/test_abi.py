@@ -185,6 +185,37 @@ def test_bwd_argument_errors(lib, kw, code, msg):
     assert msg in _lib.last_error()
 
 
+def _rmsnorm_rope_bwd(lib, **kw):
+    args = dict(grad_y=16, h=32, weight=None, inv_rms=48, dx=64, dweight=None, ws=None,
+                ws_bytes=0, rows=4, dim=64, ld_g=64, ld_h=64, ld_dx=64, seq=2, dtype=2,
+                w_dtype=2, base=10000.0, stream=None)
+    args.update(kw)
+    return lib.velograd_rmsnorm_rope_bwd(*args.values())
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dim=63, ld_g=63, ld_h=63, ld_dx=63), _lib.ERR_INVALID_ARGUMENT, "even dim"),
+    (dict(seq=0), _lib.ERR_INVALID_ARGUMENT, "seq >= 1"),
+    (dict(seq=3), _lib.ERR_INVALID_ARGUMENT, "dividing rows"),
+    (dict(base=0.0), _lib.ERR_INVALID_ARGUMENT, "base"),
+    (dict(base=float("inf")), _lib.ERR_INVALID_ARGUMENT, "base"),
+    (dict(dtype=7), _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    (dict(inv_rms=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(h=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(ld_dx=8), _lib.ERR_INVALID_ARGUMENT, "row strides"),
+    (dict(dx=16), _lib.ERR_INVALID_ARGUMENT, "alias"),
+    (dict(dx=32), _lib.ERR_INVALID_ARGUMENT, "alias"),
+])
+def test_rmsnorm_rope_bwd_argument_errors(lib, kw, code, msg):
+    assert _rmsnorm_rope_bwd(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_rmsnorm_rope_bwd_zero_rows_is_a_no_op(lib):
+    assert _rmsnorm_rope_bwd(lib, rows=0, grad_y=None, h=None, inv_rms=None, dx=None) == 0
+    assert _lib.last_error() == ""
+
+
 def test_check_maps_status_to_python_exceptions():
     with pytest.raises(TypeError):
         _lib.check(_lib.ERR_UNSUPPORTED_DTYPE, "x")

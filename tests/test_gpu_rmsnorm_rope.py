@@ -3,7 +3,9 @@
 pinned oracles: rmsnorm_module_forward (nn.py:338-355, float64, 1e-12 floor) then apply_rotary_emb
 (functional.py:287-315, float64).  Tolerance per rotated element: the angle-scaled RoPE bound of
 tests/_parity.py on the normalised pair, a float32 term for the norm, and half an output ulp for
-bf16/fp16; inv_rms |a-b|/(|b|+1e-6) <= 1e-5; h bit-exact.  The autograd module is checked against
+bf16/fp16; inv_rms |a-b|/(|b|+1e-6) <= 1e-5; h bit-exact.  The one-pass backward
+(velograd_rmsnorm_rope_bwd) is checked against the composition of the inverse rotation and the
+module backward, with the bound stated above its test.  The autograd module is checked against
 torch float64 autograd of rms_norm and the complex-number rotation."""
 
 import numpy as np
@@ -120,3 +122,105 @@ def test_errors():
         vk.rmsnorm_rope_forward(torch.zeros(2, 4, 8, device="cuda"), base=0.0)
     with pytest.raises(TypeError):
         vk.rmsnorm_rope_forward(np.zeros((2, 4, 8), np.float32))
+
+
+# ---------------------------------------------------------------------------------------------
+# The backward in one pass (velograd_rmsnorm_rope_bwd): grad_y rotated back in registers, then
+# the norm's backward.  Truth is the composition of the two pinned float64 oracles: the inverse
+# interleaved rotation (functional.py:316-345) then the module backward (nn.py:357-383) with the
+# device's h and inv_rms.  Bound: the forward's angle-scaled rotation bound on each gradient pair
+# (float32 angles), plus 2^-16 of the pair for the float32 rotation recurrence of the walk,
+# propagated through dx = r (w g - xhat mean(w g xhat)) and dweight = sum g xhat; on top of it
+# the usual dx rule (1 ulp or the operand-scaled floor) and the dweight rule (1e-3).
+# ---------------------------------------------------------------------------------------------
+def _rope_grad_bound(g: np.ndarray, base: float) -> np.ndarray:
+    seq, dim = g.shape[-2], g.shape[-1]
+    ang = np.arange(seq)[:, None] * base ** (-2.0 * np.arange(dim // 2) / dim)
+    mag = np.abs(g[..., 0::2]) + np.abs(g[..., 1::2])
+    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 * np.maximum(ang, 1.0) + 2.0 ** -16) * mag
+    out = np.empty_like(g)
+    out[..., 0::2] = b
+    out[..., 1::2] = b
+    return out
+
+
+def _check_rope_backward(dx, dw, g, h, w, inv, base, what, g_round=0.0):
+    """`g_round`: relative rounding of the rotated-back gradient before the norm's backward
+    (the two-pass path stores it in the activation dtype; the fused pass keeps it in fp32)."""
+    d = g.shape[-1]
+    g64, h64 = P.upcast(g).astype(np.float64), P.upcast(h).astype(np.float64)
+    r = P.upcast(inv).astype(np.float64)
+    w64 = np.ones(d) if w is None else P.upcast(w).astype(np.float64).reshape(-1)
+    gn = ora.apply_rotary_emb(g64, base, inverse=True)
+    tdx, tdw = ora.rmsnorm_module_backward(gn, h64, None if w is None else w64, r)
+    xhat = h64 * r
+    dg = _rope_grad_bound(g64, base) + g_round * np.abs(gn)
+    ddx = r * (np.abs(w64) * dg + np.abs(xhat) * np.mean(np.abs(w64 * xhat) * dg, axis=-1,
+                                                           keepdims=True))
+    gw = gn * w64
+    scale = P.dx_scale(gw.reshape(-1, d), xhat.reshape(-1, d), r.reshape(-1, 1)).reshape(gn.shape)
+    half_ulp = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}[dx.dtype]
+    err = np.abs(P.upcast(dx).astype(np.float64) - tdx)
+    tol = ddx + P.DX_FLOOR * scale + half_ulp * np.abs(tdx) + 1e-6 * scale
+    assert np.all(err <= tol), f"{what}: dx over its bound by {float((err - tol).max()):.3e}"
+    if w is not None:
+        ddw = np.sum((np.abs(xhat) * dg).reshape(-1, d), axis=0)
+        got = dw.detach().cpu().numpy().astype(np.float64)
+        sc = np.maximum(np.abs(tdw), np.sqrt(np.mean(tdw * tdw)))
+        assert np.all(np.abs(got - tdw) <= ddw + P.DWEIGHT_REL_TOL * sc), f"{what}: dweight"
+    else:
+        assert dw is None
+
+
+BWD_CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 8192), True),
+             (torch.float32, (3, 33, 1000), True), (torch.float16, (2, 50, 256), False),
+             (torch.bfloat16, (3, 5, 6), True), (torch.float32, (4, 2, 3, 40), True),
+             (torch.bfloat16, (1, 16384, 4096), True), (torch.bfloat16, (8, 2048, 4096), True)]
+
+
+@pytest.mark.parametrize("dtype,shape,with_w", BWD_CASES,
+                         ids=[f"{str(c[0]).split('.')[-1]}-{'x'.join(map(str, c[1]))}-w{c[2]}"
+                              for c in BWD_CASES])
+@pytest.mark.parametrize("base", [10000.0, 500000.0])
+def test_fused_backward_matches_the_oracle_composition(dtype, shape, with_w, base):
+    print(f"rmsnorm_rope backward {dtype} {shape} w={with_w} base={base}", flush=True)
+    rng = np.random.default_rng(shape[-1] * 3 + len(shape))
+    x = P.to_device(P.gaussian(rng, shape), dtype)
+    w = P.to_device(P.weight_vec(rng, shape[-1]), dtype) if with_w else None
+    g = P.to_device(P.gaussian(rng, shape), dtype)
+    _, h, inv = vk.rmsnorm_rope_forward(x, w, 1e-6, base)
+    dx, dw = vk.rmsnorm_rope_backward(g, h, w, inv, base)
+    torch.cuda.synchronize()
+    _check_rope_backward(dx, dw, g, h, w, inv, base, f"{dtype} {shape}")
+    # the two-pass path it replaces lands in the same bound (and the two agree closely)
+    g_back = vk.fused_rope_interleaved(g, base, inverse=True)
+    dx2, dw2 = vk.fused_rmsnorm_residual_backward(g_back, h, w, inv, saved_is_h=True)
+    g_round = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}[dtype]
+    _check_rope_backward(dx2, dw2, g, h, w, inv, base, f"two-pass {dtype} {shape}", g_round)
+
+
+def test_fused_backward_is_deterministic():
+    rng = np.random.default_rng(9)
+    x = P.to_device(P.gaussian(rng, (4, 1024, 4096)), torch.bfloat16)
+    w = P.to_device(P.weight_vec(rng, 4096), torch.bfloat16)
+    g = P.to_device(P.gaussian(rng, (4, 1024, 4096)), torch.bfloat16)
+    _, h, inv = vk.rmsnorm_rope_forward(x, w, 1e-6, 10000.0)
+    outs = [vk.rmsnorm_rope_backward(g, h, w, inv, 10000.0) for _ in range(3)]
+    for dx, dw in outs[1:]:
+        assert torch.equal(dx, outs[0][0]) and torch.equal(dw, outs[0][1])
+
+
+def test_backward_errors():
+    g = torch.zeros(2, 4, 8, device="cuda")
+    inv = torch.ones(2, 4, 1, device="cuda")
+    with pytest.raises(ValueError):
+        vk.rmsnorm_rope_backward(torch.zeros(2, 4, 7, device="cuda"),
+                                 torch.zeros(2, 4, 7, device="cuda"), None, inv)   # odd dim
+    with pytest.raises(ValueError):
+        vk.rmsnorm_rope_backward(g, g[:, :2], None, inv)                           # h shape
+    with pytest.raises(ValueError):
+        vk.rmsnorm_rope_backward(g, g, None, inv[:, :2])                           # inv_rms rows
+    with pytest.raises(ValueError):
+        vk.rmsnorm_rope_backward(g, g, None, inv, base=-1.0)                       # base
+    with pytest.raises(TypeError):
+        vk.rmsnorm_rope_backward(np.zeros((2, 4, 8), np.float32), g, None, inv)

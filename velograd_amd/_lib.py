@@ -106,6 +106,16 @@ SIGNATURES = {
          _c_i32, _c_i32,                    # dtype, w_dtype
          _c_ptr],                           # hip_stream
     ),
+    "velograd_rmsnorm_rope_bwd": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr,    # grad_y, h, weight, inv_rms
+         _c_ptr, _c_ptr,                    # dx, dweight
+         _c_ptr, _c_size,                   # workspace, ws_bytes
+         _c_i64, _c_i64,                    # rows, dim
+         _c_i64, _c_i64, _c_i64,            # ld_g, ld_h, ld_dx
+         _c_i64, _c_i32, _c_i32,            # seq, dtype, w_dtype
+         ctypes.c_float, _c_ptr],           # base, hip_stream
+    ),
     "velograd_rmsnorm_residual_bwd_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i32]),
     "velograd_rope": (
         _c_i32,

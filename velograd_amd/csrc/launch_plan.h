@@ -32,6 +32,13 @@ constexpr int kGenericBlock = 256;
 // NV <= 2 -> 1024 threads (128 VGPRs), NV 3..4 -> 512 (256).
 VG_HOST_DEVICE constexpr int max_block_for_nv(int nv) { return nv <= 2 ? 1024 : 512; }
 
+// The same bound for the backward with the fused inverse RoPE of grad_y: its rotation state
+// (cos and sin per pair) takes more VGPRs, so NV <= 2 -> 768 threads (170 VGPRs),
+// NV 3 -> 512 (256); with NV 4 the kernel would spill, so those rows take the generic kernel.
+VG_HOST_DEVICE constexpr int max_block_for_nv_rope(int nv) {
+  return nv <= 2 ? 768 : (nv == 3 ? 512 : 0);
+}
+
 struct RowPlan {
   bool vec;    // register-resident path
   int nv;      // 16-byte chunks per thread
@@ -141,9 +148,24 @@ inline BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned,
   return b;
 }
 
-// Workspace of the backward's dweight partial rows.  The plan depends on the element size and
-// on pointer alignment, which a size query does not know, so this is the largest need over
-// every plan the backward can pick for (rows, dim).
+// Backward plan with the fused inverse RoPE: the same layout under max_block_for_nv_rope, or the
+// generic plan where a row group does not fit that bound.
+inline BwdPlan plan_bwd_rope(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
+                             int prefer_nv, int max_block, int waves_per_cu) {
+  const RowPlan rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrder);
+  int mb = max_block;
+  if (rp.vec) {
+    const int bound = max_block_for_nv_rope(rp.nv);
+    if (bound < rp.tpr) return plan_bwd(rows, dim, elem_bytes, false, cus, prefer_nv, max_block,
+                                        waves_per_cu);  // generic
+    if (bound < mb) mb = bound;
+  }
+  return plan_bwd(rows, dim, elem_bytes, aligned, cus, prefer_nv, mb, waves_per_cu);
+}
+
+// Workspace of the backward's dweight partial rows.  The plan depends on the element size, on
+// pointer alignment and on whether the RoPE gradient is fused, which a size query does not know,
+// so this is the largest need over every plan the backward can pick for (rows, dim).
 inline size_t bwd_workspace_bytes(int64_t rows, int64_t dim, int cus, int prefer_nv,
                                   int max_block, int waves_per_cu) {
   if (rows <= 0 || dim <= 0 || cus <= 0) return 0;
@@ -154,6 +176,9 @@ inline size_t bwd_workspace_bytes(int64_t rows, int64_t dim, int cus, int prefer
       const int64_t n =
           plan_bwd(rows, dim, sizes[si], al != 0, cus, prefer_nv, max_block, waves_per_cu).wgs;
       if (n > most) most = n;
+      const int64_t nr = plan_bwd_rope(rows, dim, sizes[si], al != 0, cus, prefer_nv, max_block,
+                                       waves_per_cu).wgs;
+      if (nr > most) most = nr;
     }
   }
   return (size_t)most * (size_t)dim * sizeof(float);

@@ -199,6 +199,8 @@ struct BwdArgs {
   int32_t dim;
   int32_t tpr;
   int32_t iters;  // rows visited per slot = ceil(rows / slots)
+  int64_t rope_seq;            // kRopeG: positions per outer index (row position = row % rope_seq)
+  float rope_c_hi, rope_c_lo;  // kRopeG: log2(base) / half as an unevaluated float sum
 };
 
 // Output modes of the forward kernels.
@@ -217,16 +219,26 @@ constexpr int kOutRopeI = 4;   // y rotated by the reference model's interleaved
 // large-argument reduction runs.  About 3-4 float32 ulps of the angle in all.
 constexpr float kInv2Pi = 0.159154943091895335768883763372514362f;
 constexpr float kLn2 = 0.693147180559945309417232121458176568f;
-__device__ __forceinline__ void rope_pair(float& y0, float& y1, float pos, int i, float c_hi,
-                                          float c_lo) {
+__device__ __forceinline__ float rope_freq(int i, float c_hi, float c_lo) {
   const float fi = (float)i;
   const float e = fi * c_hi;
   const float e_lo = __builtin_fmaf(fi, c_hi, -e) + fi * c_lo;   // the rest of i * c
-  const float freq = exp2f(-e) * (1.0f - e_lo * kLn2);
+  return exp2f(-e) * (1.0f - e_lo * kLn2);
+}
+
+// cos and sin of pair i's angle at position pos.
+__device__ __forceinline__ void rope_cos_sin(float pos, int i, float c_hi, float c_lo, float& c,
+                                             float& s) {
+  const float freq = rope_freq(i, c_hi, c_lo);
   const float rev = (pos * freq) * kInv2Pi;
   const float rr = rev - rintf(rev);
-  float s, c;
   sincospif(2.0f * rr, &s, &c);
+}
+
+__device__ __forceinline__ void rope_pair(float& y0, float& y1, float pos, int i, float c_hi,
+                                          float c_lo) {
+  float s, c;
+  rope_cos_sin(pos, i, c_hi, c_lo, c, s);
   const float x0 = y0, x1 = y1;
   y0 = x0 * c - x1 * s;                                                   // functional.py:313
   y1 = x0 * s + x1 * c;                                                   // functional.py:314
@@ -658,15 +670,26 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
 // ------------------------------------------------------------------------------------------
 constexpr int kSavedIsH = 1;
 constexpr int kGradH = 2;
+// kRopeG: grad_y is the gradient of the interleaved-RoPE-rotated output (the model's
+// F.apply_rotary_emb(attention_norm(x)), models/llama.py:48-49), rotated back in registers
+// before use: the backward of the rotation (functional.py:316-345) fused into the norm's.
+constexpr int kRopeG = 4;
 
 template <int DT, int WDT, int NV, int FLAGS>
-__global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const BwdArgs a) {
+__global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(NV)
+                                               : max_block_for_nv(NV)) void bwd_vec_kernel(const BwdArgs a) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
   constexpr bool SAVED_IS_H = (FLAGS & kSavedIsH) != 0;
   constexpr bool HAS_GH = (FLAGS & kGradH) != 0;
+  constexpr bool ROPE = (FLAGS & kRopeG) != 0;
   constexpr int NH = HAS_GH ? NV : 1;  // grad_h chunks (a dummy slot when absent)
+  constexpr int P = V / 2;             // RoPE pairs per chunk
+  constexpr int NR = ROPE ? NV : 1;    // rotation state slots (a dummy slot without RoPE)
   __shared__ float red[2][kMaxWavesPerRow];
+  // dim floats of dynamic LDS: with kRopeG the walk's step rotations (cos, sin per pair), then
+  // (after a barrier) the combine of the row groups' dweight columns.
+  extern __shared__ __align__(16) float dyn_lds[];
 
   const int tpr = a.tpr;
   const int grp = threadIdx.x / tpr;
@@ -677,6 +700,50 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
   const int nchunk = a.dim / V;
   const bool has_w = a.w != nullptr;
   const bool has_dres = a.dres != nullptr;
+
+  // RoPE: each thread holds (cos, sin) of its pairs at the current row's position and advances
+  // them by the rotation through nslots positions (the walk's row step) from the LDS table; where
+  // the position wraps to a new outer index they are evaluated directly.  Float32 state: each
+  // step adds about an ulp, far below the output rounding of bf16/fp16 and inside the fp32 dx
+  // tolerance for the walks' lengths.
+  float rc[NR][P], rs[NR][P];
+  if constexpr (ROPE) {
+    for (int q = threadIdx.x; q < a.dim / 2; q += blockDim.x) {
+      double sv, cv;
+      sincos((double)nslots * (double)rope_freq(q, a.rope_c_hi, a.rope_c_lo), &sv, &cv);
+      dyn_lds[2 * q] = (float)cv;
+      dyn_lds[2 * q + 1] = (float)sv;
+    }
+    __syncthreads();
+  }
+  auto rope_start = [&](int64_t pos) {
+    if constexpr (ROPE) {
+#pragma unroll
+      for (int k = 0; k < NR; ++k) {
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          rope_cos_sin((float)pos, (lt + k * tpr) * P + p, a.rope_c_hi, a.rope_c_lo, rc[k][p],
+                       rs[k][p]);
+      }
+    }
+  };
+  auto rope_step = [&]() {
+    if constexpr (ROPE) {
+#pragma unroll
+      for (int k = 0; k < NR; ++k) {
+        const int c = lt + k * tpr;
+        if (c < nchunk) {
+#pragma unroll
+          for (int p = 0; p < P; ++p) {
+            const float sc = dyn_lds[2 * (c * P + p)], ss = dyn_lds[2 * (c * P + p) + 1];
+            const float cn = rc[k][p] * sc - rs[k][p] * ss;
+            rs[k][p] = rs[k][p] * sc + rc[k][p] * ss;
+            rc[k][p] = cn;
+          }
+        }
+      }
+    }
+  };
 
   // Packed weight chunks and the fp32 dweight column accumulators live for the whole walk; the
   // row's g and saved chunks stay packed and are decoded once per pass.
@@ -711,6 +778,15 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
   auto decode = [&](const u32x4* gv, const u32x4* sv, float rr, int k, float* gf, float* xh,
                     float* wf) {
     C::unpack(gv[k], gf);
+    if constexpr (ROPE) {
+      // inverse rotation of each pair (y0, y1) -> (y0 c + y1 s, y1 c - y0 s)
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const float g0 = gf[2 * p], g1 = gf[2 * p + 1];
+        gf[2 * p] = g0 * rc[k][p] + g1 * rs[k][p];
+        gf[2 * p + 1] = g1 * rc[k][p] - g0 * rs[k][p];
+      }
+    }
     C::unpack(sv[k], xh);
     if constexpr (SAVED_IS_H) {
 #pragma unroll
@@ -723,6 +799,8 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
   u32x4 gv[NV], sv[NV], hv[NH];
   float rr;
   load_row(row, gv, sv, hv, rr);
+  int64_t pos = ROPE ? row % a.rope_seq : 0;
+  rope_start(pos);
 
   for (int it = 0; it < a.iters; ++it) {
     const bool ok = row < a.rows;
@@ -785,6 +863,15 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
       for (int i = 0; i < V; ++i) acc[k][i] += gf[i] * xh[i];
     }
 
+    if constexpr (ROPE) {
+      pos += nslots;
+      if (pos < a.rope_seq) {
+        rope_step();
+      } else {
+        pos = nrow % a.rope_seq;
+        rope_start(pos);
+      }
+    }
     row = nrow;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -812,7 +899,8 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void bwd_vec_kernel(const Bwd
     }
     return;
   }
-  extern __shared__ __align__(16) float comb[];
+  float* comb = dyn_lds;
+  if constexpr (ROPE) __syncthreads();  // every thread is done with the step table
   for (int gi = 0; gi < groups; ++gi) {
     if (grp == gi) {
 #pragma unroll
@@ -841,6 +929,7 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
   using CW = Codec<WDT>;
   constexpr bool SAVED_IS_H = (FLAGS & kSavedIsH) != 0;
   constexpr bool HAS_GH = (FLAGS & kGradH) != 0;
+  constexpr bool ROPE = (FLAGS & kRopeG) != 0;
   __shared__ float red[2][kGenericBlock / kWave];
   const int64_t slot = blockIdx.x;
   const int64_t nslots = gridDim.x;
@@ -852,9 +941,21 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
     const int64_t row = slot + (int64_t)it * nslots;
     if (row >= a.rows) break;  // uniform across the workgroup
     const float rr = a.inv_rms[row];
+    // element j of grad_y rotated back: its pair (y0, y1) -> (y0 c + y1 s, y1 c - y0 s)
+    auto grad_at = [&](int j) {
+      const float gj = C::load1(a.g, row * a.ld_g + j);
+      if constexpr (ROPE) {
+        const float gp = C::load1(a.g, row * a.ld_g + (j ^ 1));
+        float c, sn;
+        rope_cos_sin((float)(row % a.rope_seq), j >> 1, a.rope_c_hi, a.rope_c_lo, c, sn);
+        return (j & 1) ? gj * c - gp * sn : gj * c + gp * sn;
+      } else {
+        return gj;
+      }
+    };
     float s = 0.0f;
     for (int j = threadIdx.x; j < a.dim; j += blockDim.x) {
-      const float gf = C::load1(a.g, row * a.ld_g + j);
+      const float gf = grad_at(j);
       float xh = C::load1(a.saved, row * a.ld_s + j);
       if constexpr (SAVED_IS_H) xh = xh * rr;
       const float gw = has_w ? gf * CW::load1(a.w, j) : gf;
@@ -863,7 +964,7 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
     s = row_sum(s, blockDim.x, 0, red[it & 1]);
     const float m = s / (float)a.dim;
     for (int j = threadIdx.x; j < a.dim; j += blockDim.x) {
-      const float gf = C::load1(a.g, row * a.ld_g + j);
+      const float gf = grad_at(j);
       float xh = C::load1(a.saved, row * a.ld_s + j);
       if constexpr (SAVED_IS_H) xh = xh * rr;
       const float gw = has_w ? gf * CW::load1(a.w, j) : gf;
@@ -944,8 +1045,11 @@ RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned, bool one_stream) {
                             one_stream ? vg_plan::kFwdOrderOneStream : vg_plan::kFwdOrder);
 }
 
-BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus) {
+BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus, bool rope) {
   const Tuning& t = tuning();
+  if (rope)
+    return vg_plan::plan_bwd_rope(rows, dim, elem_bytes, aligned, cus, t.bwd_nv, t.bwd_block,
+                                  t.bwd_waves_per_cu);
   return vg_plan::plan_bwd(rows, dim, elem_bytes, aligned, cus, t.bwd_nv, t.bwd_block,
                            t.bwd_waves_per_cu);
 }
@@ -996,16 +1100,29 @@ void launch_bwd_flags(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
     hipLaunchKernelGGL((bwd_generic_kernel<DT, WDT, F>), grid, block, 0, st, a);
     return;
   }
-  switch (p.nv) {
-    case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, F>), grid, block, lds, st, a); break;
-    case 2: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 2, F>), grid, block, lds, st, a); break;
-    case 3: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 3, F>), grid, block, lds, st, a); break;
-    default: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 4, F>), grid, block, lds, st, a); break;
+  if constexpr ((F & kRopeG) != 0) {
+    // NV 4 is never planned with the RoPE gradient (max_block_for_nv_rope); it is not compiled
+    switch (p.nv) {
+      case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, F>), grid, block, lds, st, a); break;
+      case 2: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 2, F>), grid, block, lds, st, a); break;
+      default: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 3, F>), grid, block, lds, st, a); break;
+    }
+  } else {
+    switch (p.nv) {
+      case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, F>), grid, block, lds, st, a); break;
+      case 2: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 2, F>), grid, block, lds, st, a); break;
+      case 3: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 3, F>), grid, block, lds, st, a); break;
+      default: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 4, F>), grid, block, lds, st, a); break;
+    }
   }
 }
 
 template <int DT, int WDT>
-void launch_bwd(const BwdArgs& a, bool saved_is_h, const BwdPlan& b, hipStream_t st) {
+void launch_bwd(const BwdArgs& a, bool saved_is_h, bool rope, const BwdPlan& b, hipStream_t st) {
+  if (rope) {  // the module form: the saved tensor is h, no residual-stream gradient
+    launch_bwd_flags<DT, WDT, kSavedIsH | kRopeG>(a, b, st);
+    return;
+  }
   const int flags = (saved_is_h ? kSavedIsH : 0) | (a.gh != nullptr ? kGradH : 0);
   switch (flags) {
     case 0: launch_bwd_flags<DT, WDT, 0>(a, b, st); break;
@@ -1160,6 +1277,120 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
   return check_launch(what);
 }
 
+// The backward behind both C entry points.  rope_seq > 0: grad_y is the gradient of the
+// interleaved-RoPE output (velograd_rmsnorm_rope_bwd); the saved tensor is then h.
+int32_t run_bwd(const void* grad_y, const void* saved, int32_t saved_is_h, const void* weight,
+                const float* inv_rms, const void* grad_h, void* dx, void* dres, float* dweight,
+                void* workspace, size_t ws_bytes, int64_t rows, int64_t dim, int64_t ld_g,
+                int64_t ld_saved, int64_t ld_grad_h, int64_t ld_dx, int64_t ld_dres,
+                int32_t dtype, int32_t w_dtype, void* hip_stream, int64_t rope_seq = 0,
+                float rope_base = 0.0f) {
+  if (!types_ok(dtype, w_dtype))
+    return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
+                "bwd: unsupported dtype/w_dtype pair (%d, %d): weight must be the activation "
+                "dtype or fp32",
+                (int)dtype, (int)w_dtype);
+  if (rows < 0 || dim <= 0 || dim > INT32_MAX)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: invalid shape rows=%lld dim=%lld",
+                (long long)rows, (long long)dim);
+  if (weight == nullptr) dweight = nullptr;  // no weight, no weight gradient (fused.py:62-65)
+  hipStream_t st = static_cast<hipStream_t>(hip_stream);
+  if (rows == 0) {
+    // Sum over zero rows: dweight = 0, written by stage 2 with no partial rows.
+    if (dweight != nullptr) {
+      hipLaunchKernelGGL(dweight_reduce_kernel, dim3((uint32_t)((dim + kWave - 1) / kWave)),
+                         dim3(kReduceBlock), 0, st, (const float*)nullptr, 0, (int32_t)dim,
+                         dweight);
+      return check_launch("velograd_rmsnorm_residual_bwd(dweight)");
+    }
+    clear_error();
+    return 0;
+  }
+  if (grad_y == nullptr || saved == nullptr || inv_rms == nullptr || dx == nullptr)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "bwd: grad_y, saved, inv_rms and dx must not be NULL");
+  if (ld_g < dim || ld_saved < dim || ld_dx < dim || (dres && ld_dres < dim) ||
+      (grad_h && ld_grad_h < dim))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "bwd: row strides must be >= dim (ld_g=%lld ld_saved=%lld ld_grad_h=%lld "
+                "ld_dx=%lld ld_dres=%lld)",
+                (long long)ld_g, (long long)ld_saved, (long long)ld_grad_h, (long long)ld_dx,
+                (long long)ld_dres);
+  // dx may be grad_h itself (accumulating in place: each element is read before it is written
+  // by the same thread); no other output may alias an input.
+  if (dx == grad_y || dx == saved || dx == dres ||
+      (dres && (dres == grad_y || dres == saved || dres == grad_h)))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: outputs must not alias inputs");
+  if (grad_h == dx && ld_grad_h != ld_dx)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "bwd: dx may alias grad_h only with the same row stride");
+
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess)
+    return fail(VELOGRAD_ERR_DEVICE_QUERY, "bwd: hipGetDevice failed");
+  const int cus = cu_count(device);
+  if (cus <= 0) return fail(VELOGRAD_ERR_DEVICE_QUERY, "bwd: cannot query the CU count");
+
+  const int eb = elem_bytes_of(dtype);
+  const bool aligned = aligned16(grad_y) && aligned16(saved) && aligned16(dx) &&
+                       ld_ok(ld_g, eb) && ld_ok(ld_saved, eb) && ld_ok(ld_dx, eb) &&
+                       (!dres || (aligned16(dres) && ld_ok(ld_dres, eb))) &&
+                       (!grad_h || (aligned16(grad_h) && ld_ok(ld_grad_h, eb))) &&
+                       (!weight || aligned16(weight));
+  const bool rope = rope_seq > 0;
+  BwdPlan plan = plan_bwd(rows, dim, eb, aligned, cus, rope);
+  // The RoPE walk keeps its step rotations (two floats per pair: dim floats) in the same dynamic
+  // LDS as the group combine, one after the other.
+  if (rope && plan.rp.vec) plan.lds_bytes = (size_t)dim * sizeof(float);
+  if (!vg_plan::row_plan_valid(plan.rp, dim, eb) || plan.wgs < 1 || plan.wgs > INT32_MAX ||
+      plan.lds_bytes > 64 * 1024 ||
+      (rope && plan.rp.vec && plan.rp.block > vg_plan::max_block_for_nv_rope(plan.rp.nv)))
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: internal launch plan rejected (dim=%lld)",
+                (long long)dim);
+  const int64_t slots = plan.wgs * plan.rp.groups;  // row slots walking the rows
+
+  float* partial = nullptr;
+  if (dweight != nullptr) {
+    const size_t need = (size_t)plan.wgs * (size_t)dim * sizeof(float);
+    if (workspace == nullptr || ws_bytes < need)
+      return fail(VELOGRAD_ERR_WORKSPACE_TOO_SMALL,
+                  "bwd: workspace of %zu bytes given, %zu needed", ws_bytes, need);
+    if (!aligned16(workspace))
+      return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: workspace must be 16-byte aligned");
+    partial = static_cast<float*>(workspace);
+  }
+
+  BwdArgs a;
+  a.g = grad_y;
+  a.saved = saved;
+  a.w = weight;
+  a.inv_rms = inv_rms;
+  a.gh = grad_h;
+  a.dx = dx;
+  a.dres = dres;
+  a.partial = partial;
+  a.rows = rows;
+  a.ld_g = ld_g;
+  a.ld_gh = ld_grad_h;
+  a.ld_s = ld_saved;
+  a.ld_dx = ld_dx;
+  a.ld_dres = ld_dres;
+  a.dim = (int32_t)dim;
+  a.tpr = plan.rp.tpr;
+  a.iters = (int32_t)((rows + slots - 1) / slots);
+  a.rope_seq = rope ? rope_seq : 1;
+  const double c = rope ? log2((double)rope_base) / (double)(dim / 2) : 0.0;
+  a.rope_c_hi = (float)c;
+  a.rope_c_lo = (float)(c - (double)a.rope_c_hi);
+  VG_DISPATCH_TYPES(dtype, w_dtype, (launch_bwd<kD, kW>(a, saved_is_h != 0, rope, plan, st)));
+  int32_t rc = check_launch(rope ? "velograd_rmsnorm_rope_bwd" : "velograd_rmsnorm_residual_bwd");
+  if (rc != 0 || dweight == nullptr) return rc;
+  hipLaunchKernelGGL(dweight_reduce_kernel, dim3((uint32_t)((dim + kWave - 1) / kWave)),
+                     dim3(kReduceBlock), 0, st, (const float*)partial, (int32_t)plan.wgs,
+                     (int32_t)dim, dweight);
+  return check_launch("velograd_rmsnorm_residual_bwd(dweight)");
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------------------------
@@ -1237,101 +1468,25 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
     void* workspace, size_t ws_bytes, int64_t rows, int64_t dim, int64_t ld_g, int64_t ld_saved,
     int64_t ld_grad_h, int64_t ld_dx, int64_t ld_dres, int32_t dtype, int32_t w_dtype,
     void* hip_stream) {
-  if (!types_ok(dtype, w_dtype))
-    return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
-                "bwd: unsupported dtype/w_dtype pair (%d, %d): weight must be the activation "
-                "dtype or fp32",
-                (int)dtype, (int)w_dtype);
-  if (rows < 0 || dim <= 0 || dim > INT32_MAX)
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: invalid shape rows=%lld dim=%lld",
-                (long long)rows, (long long)dim);
-  if (weight == nullptr) dweight = nullptr;  // no weight, no weight gradient (fused.py:62-65)
-  hipStream_t st = static_cast<hipStream_t>(hip_stream);
-  if (rows == 0) {
-    // Sum over zero rows: dweight = 0, written by stage 2 with no partial rows.
-    if (dweight != nullptr) {
-      hipLaunchKernelGGL(dweight_reduce_kernel, dim3((uint32_t)((dim + kWave - 1) / kWave)),
-                         dim3(kReduceBlock), 0, st, (const float*)nullptr, 0, (int32_t)dim,
-                         dweight);
-      return check_launch("velograd_rmsnorm_residual_bwd(dweight)");
-    }
-    clear_error();
-    return 0;
-  }
-  if (grad_y == nullptr || saved == nullptr || inv_rms == nullptr || dx == nullptr)
+  return run_bwd(grad_y, saved, saved_is_h, weight, inv_rms, grad_h, dx, dres, dweight, workspace,
+                 ws_bytes, rows, dim, ld_g, ld_saved, ld_grad_h, ld_dx, ld_dres, dtype, w_dtype,
+                 hip_stream);
+}
+
+VELOGRAD_API int32_t velograd_rmsnorm_rope_bwd(
+    const void* grad_y, const void* h, const void* weight, const float* inv_rms, void* dx,
+    float* dweight, void* workspace, size_t ws_bytes, int64_t rows, int64_t dim, int64_t ld_g,
+    int64_t ld_h, int64_t ld_dx, int64_t seq, int32_t dtype, int32_t w_dtype, float base,
+    void* hip_stream) {
+  if (dim % 2 != 0 || seq < 1 || (rows > 0 && rows % seq != 0) || !(base > 0.0f) ||
+      !__builtin_isfinite(base))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
-                "bwd: grad_y, saved, inv_rms and dx must not be NULL");
-  if (ld_g < dim || ld_saved < dim || ld_dx < dim || (dres && ld_dres < dim) ||
-      (grad_h && ld_grad_h < dim))
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
-                "bwd: row strides must be >= dim (ld_g=%lld ld_saved=%lld ld_grad_h=%lld "
-                "ld_dx=%lld ld_dres=%lld)",
-                (long long)ld_g, (long long)ld_saved, (long long)ld_grad_h, (long long)ld_dx,
-                (long long)ld_dres);
-  // dx may be grad_h itself (accumulating in place: each element is read before it is written
-  // by the same thread); no other output may alias an input.
-  if (dx == grad_y || dx == saved || dx == dres ||
-      (dres && (dres == grad_y || dres == saved || dres == grad_h)))
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: outputs must not alias inputs");
-  if (grad_h == dx && ld_grad_h != ld_dx)
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
-                "bwd: dx may alias grad_h only with the same row stride");
-
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess)
-    return fail(VELOGRAD_ERR_DEVICE_QUERY, "bwd: hipGetDevice failed");
-  const int cus = cu_count(device);
-  if (cus <= 0) return fail(VELOGRAD_ERR_DEVICE_QUERY, "bwd: cannot query the CU count");
-
-  const int eb = elem_bytes_of(dtype);
-  const bool aligned = aligned16(grad_y) && aligned16(saved) && aligned16(dx) &&
-                       ld_ok(ld_g, eb) && ld_ok(ld_saved, eb) && ld_ok(ld_dx, eb) &&
-                       (!dres || (aligned16(dres) && ld_ok(ld_dres, eb))) &&
-                       (!grad_h || (aligned16(grad_h) && ld_ok(ld_grad_h, eb))) &&
-                       (!weight || aligned16(weight));
-  const BwdPlan plan = plan_bwd(rows, dim, eb, aligned, cus);
-  if (!vg_plan::row_plan_valid(plan.rp, dim, eb) || plan.wgs < 1 || plan.wgs > INT32_MAX ||
-      plan.lds_bytes > 64 * 1024)
-    return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: internal launch plan rejected (dim=%lld)",
-                (long long)dim);
-  const int64_t slots = plan.wgs * plan.rp.groups;  // row slots walking the rows
-
-  float* partial = nullptr;
-  if (dweight != nullptr) {
-    const size_t need = (size_t)plan.wgs * (size_t)dim * sizeof(float);
-    if (workspace == nullptr || ws_bytes < need)
-      return fail(VELOGRAD_ERR_WORKSPACE_TOO_SMALL,
-                  "bwd: workspace of %zu bytes given, %zu needed", ws_bytes, need);
-    if (!aligned16(workspace))
-      return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: workspace must be 16-byte aligned");
-    partial = static_cast<float*>(workspace);
-  }
-
-  BwdArgs a;
-  a.g = grad_y;
-  a.saved = saved;
-  a.w = weight;
-  a.inv_rms = inv_rms;
-  a.gh = grad_h;
-  a.dx = dx;
-  a.dres = dres;
-  a.partial = partial;
-  a.rows = rows;
-  a.ld_g = ld_g;
-  a.ld_gh = ld_grad_h;
-  a.ld_s = ld_saved;
-  a.ld_dx = ld_dx;
-  a.ld_dres = ld_dres;
-  a.dim = (int32_t)dim;
-  a.tpr = plan.rp.tpr;
-  a.iters = (int32_t)((rows + slots - 1) / slots);
-  VG_DISPATCH_TYPES(dtype, w_dtype, (launch_bwd<kD, kW>(a, saved_is_h != 0, plan, st)));
-  int32_t rc = check_launch("velograd_rmsnorm_residual_bwd");
-  if (rc != 0 || dweight == nullptr) return rc;
-  hipLaunchKernelGGL(dweight_reduce_kernel, dim3((uint32_t)((dim + kWave - 1) / kWave)),
-                     dim3(kReduceBlock), 0, st, (const float*)partial, (int32_t)plan.wgs,
-                     (int32_t)dim, dweight);
-  return check_launch("velograd_rmsnorm_residual_bwd(dweight)");
+                "velograd_rmsnorm_rope_bwd: RoPE needs an even dim (%lld), seq >= 1 dividing rows "
+                "(seq=%lld rows=%lld) and a finite base > 0 (%g)",
+                (long long)dim, (long long)seq, (long long)rows, (double)base);
+  return run_bwd(grad_y, h, 1, weight, inv_rms, nullptr, dx, nullptr, dweight, workspace,
+                 ws_bytes, rows, dim, ld_g, ld_h, dim, ld_dx, dim, dtype, w_dtype, hip_stream,
+                 seq, base);
 }
 
 }  // extern "C"

@@ -53,6 +53,7 @@ __all__ = [
     "fused_rmsnorm_residual_forward_mx",
     "rmsnorm_forward",
     "rmsnorm_rope_forward",
+    "rmsnorm_rope_backward",
     "fused_rope",
     "fused_rope_forward",
     "fused_rope_backward",
@@ -666,8 +667,9 @@ def rmsnorm_rope_forward(x: torch.Tensor, weight: Optional[torch.Tensor] = None,
     Returns (y, h, inv_rms): y the rotated normalised rows in x's dtype, h as
     fused_rmsnorm_residual_forward (x itself without residual), inv_rms float32 [..., 1].  The
     backward is the inverse rotation of grad_y (fused_rope_interleaved(..., inverse=True)) then
-    fused_rmsnorm_residual_backward with saved_is_h=True (nn.rms_norm_rope does both).  Device
-    tensors only; x is [..., seq, dim] with dim even.
+    fused_rmsnorm_residual_backward with saved_is_h=True, which rmsnorm_rope_backward does in
+    one pass (nn.rms_norm_rope uses it).  Device tensors only; x is [..., seq, dim] with dim
+    even.
     """
     if not _is_device_tensor(x):
         raise TypeError("rmsnorm_rope_forward takes torch tensors on a ROCm device")
@@ -700,6 +702,60 @@ def rmsnorm_rope_forward(x: torch.Tensor, weight: Optional[torch.Tensor] = None,
             _stream(device))
     _lib.check(rc, "velograd_rmsnorm_rope_fwd")
     return y, h, inv_rms
+
+
+def rmsnorm_rope_backward(grad_y: torch.Tensor, h: torch.Tensor,
+                          weight: Optional[torch.Tensor], inv_rms: torch.Tensor,
+                          base: float = 10000.0):
+    """Backward of rmsnorm_rope_forward in one pass (velograd_rmsnorm_rope_bwd): grad_y is
+    rotated back pair by pair (functional.py:316-345) and the norm's backward runs on it with
+    h saved (nn.py:357-383, fused.py:48-66); the same result as
+    fused_rmsnorm_residual_backward(fused_rope_interleaved(grad_y, base, inverse=True), h,
+    weight, inv_rms, saved_is_h=True) without the intermediate tensor.
+
+    Returns (grad_x, grad_weight): grad_x in grad_y's dtype (also the residual's gradient when
+    the forward had one), grad_weight float32 [D] or None without weight.  h is the forward's
+    h (x itself without residual); device tensors [..., seq, dim] only.
+    """
+    if not _is_device_tensor(grad_y):
+        raise TypeError("rmsnorm_rope_backward takes torch tensors on a ROCm device")
+    if grad_y.dim() < 2:
+        raise ValueError("rmsnorm_rope_backward: grad_y must be [..., seq, dim]")
+    seq, d = grad_y.shape[-2], grad_y.shape[-1]
+    if d % 2 != 0:
+        raise ValueError(f"rmsnorm_rope_backward: dim={d} must be even (RoPE pairs)")
+    code = _dtype_code(grad_y, "grad_y")
+    device = grad_y.device
+    if (not isinstance(h, torch.Tensor) or h.device != device or h.dtype != grad_y.dtype
+            or h.shape != grad_y.shape):
+        raise ValueError("h must be a tensor shaped and typed like grad_y on its device")
+    rows = math.prod(grad_y.shape[:-1])
+    if not isinstance(inv_rms, torch.Tensor) or inv_rms.device != device:
+        raise ValueError("inv_rms must be a tensor on the same device as grad_y")
+    if inv_rms.numel() != rows:
+        raise ValueError(f"inv_rms has {inv_rms.numel()} elements, expected one per row ({rows})")
+    r = inv_rms.reshape(rows).to(torch.float32).contiguous()
+    w, wcode = _prep_weight(weight, d, grad_y.dtype, device)
+    dx = torch.empty(grad_y.shape, dtype=grad_y.dtype, device=device)
+    dweight = torch.empty((d,), dtype=torch.float32, device=device) if w is not None else None
+    if rows == 0 or d == 0:
+        if dweight is not None:
+            dweight.zero_()
+        return dx, dweight
+    g2 = grad_y.contiguous().view(-1, d)
+    h2 = h.contiguous().view(-1, d)
+    ws = None
+    ws_bytes = 0
+    if dweight is not None:
+        ws_bytes = bwd_workspace_bytes(rows, d, device)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        rc = _lib.load().velograd_rmsnorm_rope_bwd(
+            g2.data_ptr(), h2.data_ptr(), _ptr(w), r.data_ptr(), dx.data_ptr(), _ptr(dweight),
+            _ptr(ws), ws_bytes, rows, d, d, d, d, seq, code, wcode, float(base),
+            _stream(device))
+    _lib.check(rc, "velograd_rmsnorm_rope_bwd")
+    return dx, dweight
 
 
 def fused_rmsnorm_residual(x: Any, residual: Optional[Any] = None, weight: Optional[Any] = None,

@@ -182,8 +182,8 @@ def apply_rope(q: torch.Tensor, k: Optional[torch.Tensor] = None,
 
 class RMSNormRoPEFunction(torch.autograd.Function):
     """`F.apply_rotary_emb(attention_norm(x))` of the reference's model (models/llama.py:48-49)
-    in one forward pass; the backward rotates grad_y back (one launch) and runs the fused
-    RMSNorm backward with the saved x (nn.py:357-383, functional.py:316-345 chained)."""
+    in one forward pass; the backward rotates grad_y back and runs the RMSNorm backward with the
+    saved x in one pass as well (nn.py:357-383, functional.py:316-345 chained)."""
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, weight: Optional[torch.Tensor], eps: float, base: float,
@@ -196,8 +196,7 @@ class RMSNormRoPEFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_y: torch.Tensor):
         h, weight, inv_rms = ctx.saved_tensors
-        g = _k.fused_rope_interleaved(grad_y.contiguous(), ctx.base, inverse=True)
-        dx, dweight = _k.fused_rmsnorm_residual_backward(g, h, weight, inv_rms, saved_is_h=True)
+        dx, dweight = _k.rmsnorm_rope_backward(grad_y, h, weight, inv_rms, ctx.base)
         need_x, need_w = ctx.needs_input_grad[:2]
         if dweight is not None and weight is not None and dweight.dtype != weight.dtype:
             dweight = dweight.to(weight.dtype)
