@@ -120,7 +120,8 @@ def test_launch_stream_is_torchs_current_stream():
 
 def test_graph_replays_of_module_forms_and_interleaved_rope_match_eager():
     """The module form (floor), the residual add with the floor, the backward through the fast
-    path's outputs, and the interleaved RoPE, captured together and replayed with new inputs."""
+    path's outputs, the interleaved RoPE, and the norm + RoPE forward with its one-pass
+    backward, captured together and replayed with new inputs."""
     torch.manual_seed(2)
     dev = torch.device("cuda", 0)
     x = torch.randn(64, 4096, device=dev, dtype=torch.bfloat16)
@@ -135,7 +136,10 @@ def test_graph_replays_of_module_forms_and_interleaved_rope_match_eager():
         dx, dw = vk.fused_rmsnorm_residual_backward(g, h2, w, inv2, saved_is_h=True)
         qi = vk.fused_rope_interleaved(q, 10000.0)
         qb = vk.fused_rope_interleaved(qi, 10000.0, inverse=True)
-        return [y1, inv1, y2, h2, inv2, dx, dw, qi, qb]
+        # the attention-branch input: norm + RoPE forward and its one-pass backward
+        yr, hr, invr = vk.rmsnorm_rope_forward(x.view(2, 32, 4096), w, 1e-6, 10000.0)
+        dxr, dwr = vk.rmsnorm_rope_backward(g.view(2, 32, 4096), hr, w, invr, 10000.0)
+        return [y1, inv1, y2, h2, inv2, dx, dw, qi, qb, yr, invr, dxr, dwr]
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
