@@ -33,10 +33,11 @@ constexpr int kGenericBlock = 256;
 VG_HOST_DEVICE constexpr int max_block_for_nv(int nv) { return nv <= 2 ? 1024 : 512; }
 
 // The same bound for the backward with the fused inverse RoPE of grad_y: its rotation state
-// (cos and sin per pair) takes more VGPRs, so NV <= 2 -> 768 threads (170 VGPRs),
-// NV 3 -> 512 (256); with NV 4 the kernel would spill, so those rows take the generic kernel.
+// (cos and sin per pair) takes more VGPRs, so NV 1 -> 1024 threads (92 VGPRs used),
+// NV 2 -> 768 (170), NV 3 -> 512 (256); with NV 4 the kernel would spill, so those rows take
+// the generic kernel.
 VG_HOST_DEVICE constexpr int max_block_for_nv_rope(int nv) {
-  return nv <= 2 ? 768 : (nv == 3 ? 512 : 0);
+  return nv <= 1 ? 1024 : (nv == 2 ? 768 : (nv == 3 ? 512 : 0));
 }
 
 struct RowPlan {
@@ -57,6 +58,10 @@ struct RowPlan {
 constexpr int kFwdOrder[kMaxNV] = {1, 2, 3, 4};
 constexpr int kFwdOrderOneStream[kMaxNV] = {2, 4, 3, 1};
 constexpr int kBwdOrder[kMaxNV] = {2, 3, 4, 1};
+// The backward with the fused RoPE gradient prefers one chunk per thread: its rotation state
+// then fits 1024-thread workgroups (16384 x 4096 bf16: 84.0 us against 89.7 us at two chunks
+// in 768-thread workgroups).
+constexpr int kBwdOrderRope[kMaxNV] = {1, 2, 3, 4};
 
 // Register-resident layout for rows of `dim` elements of `elem_bytes` bytes, or the generic
 // plan when the row does not split into 16-byte chunks or does not fit in registers.
@@ -126,9 +131,10 @@ struct BwdPlan {
 };
 
 inline BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
-                        int prefer_nv, int max_block, int waves_per_cu) {
+                        int prefer_nv, int max_block, int waves_per_cu,
+                        const int (&order)[kMaxNV] = kBwdOrder) {
   BwdPlan b;
-  b.rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrder);
+  b.rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, order);
   RowPlan& p = b.rp;
   if (p.vec) {
     int mb = max_block_for_nv(p.nv);
@@ -152,7 +158,7 @@ inline BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned,
 // generic plan where a row group does not fit that bound.
 inline BwdPlan plan_bwd_rope(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
                              int prefer_nv, int max_block, int waves_per_cu) {
-  const RowPlan rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrder);
+  const RowPlan rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrderRope);
   int mb = max_block;
   if (rp.vec) {
     const int bound = max_block_for_nv_rope(rp.nv);
@@ -160,7 +166,8 @@ inline BwdPlan plan_bwd_rope(int64_t rows, int64_t dim, int elem_bytes, bool ali
                                         waves_per_cu);  // generic
     if (bound < mb) mb = bound;
   }
-  return plan_bwd(rows, dim, elem_bytes, aligned, cus, prefer_nv, mb, waves_per_cu);
+  return plan_bwd(rows, dim, elem_bytes, aligned, cus, prefer_nv, mb, waves_per_cu,
+                  kBwdOrderRope);
 }
 
 // Workspace of the backward's dweight partial rows.  The plan depends on the element size, on
