@@ -26,6 +26,11 @@ PROBE_LIB_PATH = os.path.join(LIB_DIR, "libvelograd_stream_probe.so")
 
 OFFLOAD_ARCH = "gfx950"
 
+# Plain C++ check of the C ABI without torch (tests/c_abi_check.cpp, run by a GPU test): host
+# code only, linked against the kernels library and the HIP runtime.
+C_ABI_CHECK_SRC = os.path.join(REPO_DIR, "tests", "c_abi_check.cpp")
+C_ABI_CHECK_BIN = os.path.join(REPO_DIR, "tests", "_build", "c_abi_check")
+
 # Host-only pybind11 binding of the forward's fast path to torch tensors (a CPython extension
 # module next to the package's Python files).  Optional at run time: without it the ctypes path
 # runs the same kernels.
@@ -103,13 +108,33 @@ def build_fastpath(verbose: bool = False) -> str:
     return out
 
 
+def build_c_abi_check(verbose: bool = False) -> str:
+    """Compile tests/c_abi_check.cpp against the built library (host C++ through hipcc)."""
+    out = C_ABI_CHECK_BIN
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    rel = os.path.relpath(LIB_DIR, os.path.dirname(out))
+    cmd = [find_hipcc(), "-O2", "-std=c++17", "-Wall", "-I", INCLUDE_DIR, C_ABI_CHECK_SRC,
+           "-o", tmp, "-L", LIB_DIR, "-lvelograd_kernels", f"-Wl,-rpath,$ORIGIN/{rel}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(
+            "C ABI check build failed (exit %d):\n%s\n%s" % (proc.returncode, proc.stdout,
+                                                              proc.stderr))
+    os.replace(tmp, out)
+    return out
+
+
 def build_library(verbose: bool = False) -> str:
     """Compile the kernels (and the bench's stream probe) for gfx950, then the torch-tensor
-    fast path; return the kernels' .so."""
+    fast path and the plain C++ ABI check; return the kernels' .so."""
     os.makedirs(LIB_DIR, exist_ok=True)
     _hipcc(SRCS, LIB_PATH, verbose)
     _hipcc([PROBE_SRC], PROBE_LIB_PATH, verbose)
     build_fastpath(verbose)
+    build_c_abi_check(verbose)
     return LIB_PATH
 
 
