@@ -303,16 +303,20 @@ def fused_rope(x, k=None, head_dim: Optional[int] = None, base: float = 10000.0)
     return q_rot
 
 
-def apply_rotary_emb(x, base: float = 10000.0, inverse: bool = False) -> np.ndarray:
+def apply_rotary_emb(x, base: float = 10000.0, inverse: bool = False,
+                     positions=None) -> np.ndarray:
     """python/velograd/functional.py:287-315 (forward) and :316-345 (inverse = the backward's
     rotation) in float64, the precision of the reference's Python floats: interleaved pairs
-    (x_2i, x_2i+1) of the last axis, position = index along axis -2."""
+    (x_2i, x_2i+1) of the last axis, position = index along axis -2.  `positions` (one per index
+    of axis -2) replaces that index, for rows taken out of a longer sequence."""
     x = np.asarray(x, dtype=np.float64)
     seq_len, dim = x.shape[-2], x.shape[-1]                              # :289-290
     assert dim % 2 == 0, "Dimension must be even for RoPE pairs"         # :291
     i = np.arange(dim // 2, dtype=np.float64)
     theta = 1.0 / (base ** ((2.0 * i) / float(dim)))                     # :302
-    angle = np.arange(seq_len, dtype=np.float64)[:, None] * theta        # :303
+    pos = (np.arange(seq_len, dtype=np.float64) if positions is None
+           else np.asarray(positions, dtype=np.float64).reshape(seq_len))
+    angle = pos[:, None] * theta                                         # :303
     cos_val, sin_val = np.cos(angle), np.sin(angle)                      # :304-305
     if inverse:
         sin_val = -sin_val

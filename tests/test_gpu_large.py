@@ -63,6 +63,53 @@ def test_forward_backward_beyond_2_pow_31_elements(big):
     torch.cuda.synchronize()
 
 
+def test_norm_rope_backward_beyond_2_pow_31_elements(big):
+    """The one-pass norm + RoPE backward over one sequence of 262147 positions: dx on the rows
+    next to the 2^31-element boundary against the oracle composition at their positions (the
+    rotation's inverse, then the module backward, both float64), the full dweight against a
+    float64 sum of (rotated-back g) * xhat computed by torch on the device in row blocks, with
+    the angles pos * base^(-2i/dim) in float64 (functional.py:302-303, 316-345)."""
+    x, _, w = big
+    _say(f"large norm+rope backward {ROWS}x{D} bf16")
+    x3 = x.view(1, ROWS, D)
+    _, h, inv = vk.rmsnorm_rope_forward(x3, w, 1e-6, 10000.0)
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    g = torch.randn(1, ROWS, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    dx, dw = vk.rmsnorm_rope_backward(g, h, w, inv, 10000.0)
+    rows = np.array(CHECK_ROWS)
+    g64 = g[0, CHECK_ROWS].double().cpu().numpy()
+    h64 = h[0, CHECK_ROWS].double().cpu().numpy()
+    r64 = inv[0, CHECK_ROWS].double().cpu().numpy()
+    w64 = P.upcast(w).astype(np.float64)
+    gn = ora.apply_rotary_emb(g64, 10000.0, inverse=True, positions=rows)
+    rdx, _ = ora.rmsnorm_module_backward(gn, h64, w64, r64)
+    # angles in double: 16 float32 ulps of the pair at any position, plus 2^-12 for the float32
+    # rotation recurrence over this walk's 512 steps per row slot
+    dg = np.repeat((P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -12)
+                   * (np.abs(g64[:, 0::2]) + np.abs(g64[:, 1::2])), 2, axis=1)
+    xhat = h64 * r64
+    tol = r64 * (np.abs(w64) * dg + np.abs(xhat) * np.mean(np.abs(w64 * xhat) * dg, axis=-1,
+                                                           keepdims=True))
+    tol += P.DX_FLOOR * P.dx_scale(gn * w64, xhat, r64) + 2.0 ** -8 * np.abs(rdx)
+    err = np.abs(dx[0, CHECK_ROWS].double().cpu().numpy() - rdx)
+    assert np.all(err <= tol), float((err - tol).max())
+    del dx
+    ref = torch.zeros(D, dtype=torch.float64, device="cuda")
+    inv_freq = 10000.0 ** (-torch.arange(0, D, 2, dtype=torch.float64, device="cuda") / D)
+    for r0 in range(0, ROWS, 16384):
+        r1 = min(ROWS, r0 + 16384)
+        ang = torch.arange(r0, r1, dtype=torch.float64, device="cuda")[:, None] * inv_freq
+        c, sn = torch.cos(ang), torch.sin(ang)
+        gb = g[0, r0:r1].double()
+        gn = torch.empty_like(gb)
+        gn[:, 0::2] = gb[:, 0::2] * c + gb[:, 1::2] * sn
+        gn[:, 1::2] = gb[:, 1::2] * c - gb[:, 0::2] * sn
+        ref += (gn * (h[0, r0:r1].double() * inv[0, r0:r1].double())).sum(0)
+    P.assert_dweight(dw.double().cpu().numpy(), ref.cpu().numpy())
+    del g
+    torch.cuda.synchronize()
+
+
 def test_quantised_forwards_beyond_2_pow_31_bytes(big):
     x, res, w = big
     w32 = P.upcast(w)

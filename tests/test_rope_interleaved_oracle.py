@@ -117,3 +117,15 @@ def _inverse_not_negated(x, base, inverse):
 ])
 def test_planted_mistakes_are_caught(mistake, caught_by):
     assert caught_by in _failures(mistake)
+
+
+def test_positions_argument_matches_rows_of_the_whole_sequence():
+    """Rows taken out of a sequence, rotated with their own positions, equal the same rows of the
+    whole sequence rotated (forward and inverse)."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 300, 64))
+    rows = np.array([0, 1, 7, 150, 298, 299])
+    for inverse in (False, True):
+        whole = ora.apply_rotary_emb(x, 500000.0, inverse=inverse)
+        part = ora.apply_rotary_emb(x[:, rows], 500000.0, inverse=inverse, positions=rows)
+        assert np.array_equal(part, whole[:, rows])

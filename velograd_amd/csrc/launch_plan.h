@@ -33,11 +33,11 @@ constexpr int kGenericBlock = 256;
 VG_HOST_DEVICE constexpr int max_block_for_nv(int nv) { return nv <= 2 ? 1024 : 512; }
 
 // The same bound for the backward with the fused inverse RoPE of grad_y: its rotation state
-// (cos and sin per pair) takes more VGPRs, so NV 1 -> 1024 threads (92 VGPRs used),
-// NV 2 -> 768 (170), NV 3 -> 512 (256); with NV 4 the kernel would spill, so those rows take
-// the generic kernel.
+// (cos and sin per pair) takes more VGPRs, so NV 1 -> 1024 threads (95 VGPRs used),
+// NV 2 and 3 -> 512 (256); with NV 4 the kernel would spill, so those rows take the generic
+// kernel.
 VG_HOST_DEVICE constexpr int max_block_for_nv_rope(int nv) {
-  return nv <= 1 ? 1024 : (nv == 2 ? 768 : (nv == 3 ? 512 : 0));
+  return nv <= 1 ? 1024 : (nv <= 3 ? 512 : 0);
 }
 
 struct RowPlan {

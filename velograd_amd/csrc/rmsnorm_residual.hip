@@ -213,29 +213,24 @@ constexpr int kOutRopeI = 4;   // y rotated by the reference model's interleaved
 // The reference model's RoPE applied to y in registers (python/velograd/functional.py:287-315;
 // models/llama.py:48-49 rotates the normalised attention input): the pair (y_2i, y_2i+1) of a
 // row at position pos turns by pos * freq_i, freq_i = base^(-2i/dim) = 2^-(i * c) with
-// c = log2(base) / half.  c arrives as c_hi + c_lo (from double on the host) and i * c is formed
-// with its exact rounding error (FMA), so freq_i is within about one ulp of exp2f; the angle is
-// then taken in revolutions and reduced to [-1/2, 1/2] exactly before sincospi, so no
-// large-argument reduction runs.  About 3-4 float32 ulps of the angle in all.
-constexpr float kInv2Pi = 0.159154943091895335768883763372514362f;
-constexpr float kLn2 = 0.693147180559945309417232121458176568f;
-__device__ __forceinline__ float rope_freq(int i, float c_hi, float c_lo) {
-  const float fi = (float)i;
-  const float e = fi * c_hi;
-  const float e_lo = __builtin_fmaf(fi, c_hi, -e) + fi * c_lo;   // the rest of i * c
-  return exp2f(-e) * (1.0f - e_lo * kLn2);
+// c = log2(base) / half.  c arrives as c_hi + c_lo (from double on the host); freq_i and the
+// angle pos * freq_i are formed in double, as the reference's Python floats are, and the angle is
+// reduced exactly to [-1/2, 1/2] revolutions before a float32 sincospi, so cos and sin are within
+// a few float32 ulps at any position (a float32 angle would carry pos * freq_i * 2^-24 radians of
+// error: 0.016 rad at position 2.6e5).
+constexpr double kInv2PiD = 0.159154943091895335768883763372514362;
+__device__ __forceinline__ double rope_freq(int i, float c_hi, float c_lo) {
+  return exp2(-(double)i * ((double)c_hi + (double)c_lo));
 }
 
 // cos and sin of pair i's angle at position pos.
-__device__ __forceinline__ void rope_cos_sin(float pos, int i, float c_hi, float c_lo, float& c,
+__device__ __forceinline__ void rope_cos_sin(int64_t pos, int i, float c_hi, float c_lo, float& c,
                                              float& s) {
-  const float freq = rope_freq(i, c_hi, c_lo);
-  const float rev = (pos * freq) * kInv2Pi;
-  const float rr = rev - rintf(rev);
-  sincospif(2.0f * rr, &s, &c);
+  const double rev = (double)pos * rope_freq(i, c_hi, c_lo) * kInv2PiD;
+  sincospif(2.0f * (float)(rev - rint(rev)), &s, &c);
 }
 
-__device__ __forceinline__ void rope_pair(float& y0, float& y1, float pos, int i, float c_hi,
+__device__ __forceinline__ void rope_pair(float& y0, float& y1, int64_t pos, int i, float c_hi,
                                           float c_lo) {
   float s, c;
   rope_cos_sin(pos, i, c_hi, c_lo, c, s);
@@ -450,11 +445,11 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 // Forward with the model's RoPE on y (kOutRopeI), register-resident rows: a workgroup of one row
 // group walks kNormRopeRows consecutive rows, the next row's chunks in flight while the current
 // one reduces.  Each thread keeps the rotation (cos, sin) of its pairs in double and advances
-// it by one position per row (the rotation through freq_j, from a double sincos of freq_j), so a
-// sincospi per pair is evaluated only at the first row of the walk or where the position wraps
-// to 0 (a new outer index); evaluated per (row, pair) it made the fused pass VALU-bound, no
-// faster than two passes.  The start angle is reduced in revolutions before sincospi (about
-// 3-4 float32 ulps), the recurrence adds ~1e-16 per step.
+// it by one position per row (the rotation through freq_j, from a double sincos of freq_j), so
+// trigonometry runs only before the walk; evaluated per (row, pair) it made the fused pass
+// VALU-bound, no faster than two passes.  The walk's first angle is the double pos * freq_j
+// reduced exactly before a float sincospi (a few float32 ulps); where the position wraps to 0 (a
+// new outer index) the rotation restarts at the identity; the recurrence adds ~1e-16 per step.
 // ------------------------------------------------------------------------------------------
 constexpr int kNormRopeRows = 16;
 
@@ -475,7 +470,6 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_rope_kernel(const Fw
 
   WeightChunk<DT, WDT> wc[NV];
   double cr[NV][PP], sr[NV][PP], cst[NV][PP], sst[NV][PP];
-  float fr[NV][PP];
   auto load_row = [&](int64_t row, u32x4* xv, u32x4* rv) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -496,32 +490,31 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_rope_kernel(const Fw
     wc[k].load((has_w && c < nchunk) ? a.w : nullptr, (int64_t)c * V);
 #pragma unroll
     for (int q = 0; q < PP; ++q) {
-      // freq_j = 2^-(j * c) with c = log2(base) / half split as c_hi + c_lo (see rope_pair)
-      const float fj = (float)(c * PP + q);
-      const float e = fj * a.rope_c_hi;
-      const float e_lo = __builtin_fmaf(fj, a.rope_c_hi, -e) + fj * a.rope_c_lo;
-      fr[k][q] = exp2f(-e) * (1.0f - e_lo * kLn2);
-      double sv, cv;
-      sincos((double)fr[k][q], &sv, &cv);
+      const double fd = rope_freq(c * PP + q, a.rope_c_hi, a.rope_c_lo);
+      double sv, cv;  // the rotation through one position
+      sincos(fd, &sv, &cv);
       cst[k][q] = cv;
       sst[k][q] = sv;
+      // the rotation at the walk's first position: double angle, reduced exactly, float sincospi
+      const double rev = (double)(row0 % a.rope_seq) * fd * kInv2PiD;
+      float sf, cf;
+      sincospif(2.0f * (float)(rev - rint(rev)), &sf, &cf);
+      cr[k][q] = cf;
+      sr[k][q] = sf;
     }
   }
 
   for (int it = 0; it < nrows; ++it) {
     const int64_t row = row0 + it;
     const int64_t pos = row % a.rope_seq;
-    if (it == 0 || pos == 0) {
-      // start rotation at this position: the angle in revolutions, reduced exactly, to sincospi
+    if (it > 0 && pos == 0) {
+      // a new outer index: position 0, the identity rotation
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
 #pragma unroll
         for (int q = 0; q < PP; ++q) {
-          const float rev = ((float)pos * fr[k][q]) * kInv2Pi;
-          float sv, cv;
-          sincospif(2.0f * (rev - rintf(rev)), &sv, &cv);
-          cr[k][q] = cv;
-          sr[k][q] = sv;
+          cr[k][q] = 1.0;
+          sr[k][q] = 0.0;
         }
       }
     }
@@ -618,7 +611,7 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
   if constexpr (OUT == kOutDtype) {
     for (int j = threadIdx.x; j < a.dim; j += blockDim.x) C::store1(a.y, row * a.ld_y + j, y_at(j));
   } else if constexpr (OUT == kOutRopeI) {
-    const float pos = (float)(row % a.rope_seq);
+    const int64_t pos = row % a.rope_seq;
     for (int i = threadIdx.x; i < a.rope_half; i += blockDim.x) {
       float y0 = y_at(2 * i), y1 = y_at(2 * i + 1);
       rope_pair(y0, y1, pos, i, a.rope_c_hi, a.rope_c_lo);
@@ -710,7 +703,7 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
   if constexpr (ROPE) {
     for (int q = threadIdx.x; q < a.dim / 2; q += blockDim.x) {
       double sv, cv;
-      sincos((double)nslots * (double)rope_freq(q, a.rope_c_hi, a.rope_c_lo), &sv, &cv);
+      sincos((double)nslots * rope_freq(q, a.rope_c_hi, a.rope_c_lo), &sv, &cv);
       dyn_lds[2 * q] = (float)cv;
       dyn_lds[2 * q + 1] = (float)sv;
     }
@@ -722,7 +715,7 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
       for (int k = 0; k < NR; ++k) {
 #pragma unroll
         for (int p = 0; p < P; ++p)
-          rope_cos_sin((float)pos, (lt + k * tpr) * P + p, a.rope_c_hi, a.rope_c_lo, rc[k][p],
+          rope_cos_sin(pos, (lt + k * tpr) * P + p, a.rope_c_hi, a.rope_c_lo, rc[k][p],
                        rs[k][p]);
       }
     }
@@ -947,7 +940,7 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
       if constexpr (ROPE) {
         const float gp = C::load1(a.g, row * a.ld_g + (j ^ 1));
         float c, sn;
-        rope_cos_sin((float)(row % a.rope_seq), j >> 1, a.rope_c_hi, a.rope_c_lo, c, sn);
+        rope_cos_sin(row % a.rope_seq, j >> 1, a.rope_c_hi, a.rope_c_lo, c, sn);
         return (j & 1) ? gj * c - gp * sn : gj * c + gp * sn;
       } else {
         return gj;
