@@ -514,9 +514,10 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_rope_kernel(const Fw
     }
   }
 
-  for (int it = 0; it < nrows; ++it) {
+  // the position advances with the row and wraps at rope_seq (no division inside the walk)
+  int64_t pos = row0 % a.rope_seq;
+  for (int it = 0; it < nrows; ++it, pos = (pos + 1 == a.rope_seq) ? 0 : pos + 1) {
     const int64_t row = row0 + it;
-    const int64_t pos = row % a.rope_seq;
     if (it > 0 && pos == 0) {
       // a new outer index: position 0, the identity rotation
 #pragma unroll
