@@ -215,6 +215,35 @@ def test_fused_backward_is_deterministic():
         assert torch.equal(dx, outs[0][0]) and torch.equal(dw, outs[0][1])
 
 
+def test_fused_forward_is_bitwise_repeatable_on_any_stream():
+    """The forward at the headline shape, with and without a residual, gives bit-identical y,
+    h and inv_rms on every call: on the current stream and on a side stream, interleaved with
+    calls on other buffers."""
+    rng = np.random.default_rng(21)
+    x = P.to_device(P.gaussian(rng, (8, 2048, 4096)), torch.bfloat16)
+    r = P.to_device(P.gaussian(rng, (8, 2048, 4096)), torch.bfloat16)
+    x2 = P.to_device(P.gaussian(rng, (8, 2048, 4096)), torch.bfloat16)
+    w = P.to_device(P.weight_vec(rng, 4096), torch.bfloat16)
+    ref = vk.rmsnorm_rope_forward(x, w, 1e-5, 10000.0)
+    ref_r = vk.rmsnorm_rope_forward(x, w, 1e-5, 10000.0, residual=r)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    outs = []
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            outs.append((vk.rmsnorm_rope_forward(x, w, 1e-5, 10000.0), ref))
+            vk.rmsnorm_rope_forward(x2, w, 1e-5, 10000.0, residual=r)
+            outs.append((vk.rmsnorm_rope_forward(x, w, 1e-5, 10000.0, residual=r), ref_r))
+    torch.cuda.current_stream().wait_stream(side)
+    outs.append((vk.rmsnorm_rope_forward(x, w, 1e-5, 10000.0), ref))
+    torch.cuda.synchronize()
+    for got, want in outs:
+        assert torch.equal(got[0], want[0]), "y"
+        assert torch.equal(got[2], want[2]), "inv_rms"
+        if want[1] is not None:
+            assert torch.equal(got[1], want[1]), "h"
+
+
 def test_backward_errors():
     g = torch.zeros(2, 4, 8, device="cuda")
     inv = torch.ones(2, 4, 1, device="cuda")
