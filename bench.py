@@ -13,10 +13,12 @@ touched by the step before it.
 Output: one JSON line (the driver's contract) with
   value      = algorithmic bytes of a step / wall time of a step (GB/s, whole job, 1 GPU)
   roofline   = the forward kernel (the larger of the two): algorithmic bytes per launch over its
-               mean launch duration from HIP events on the launch stream, against 8 TB/s HBM;
-               `traffic` comes from the committed rocprofv3 PMC summary when present
-  cpu_baseline = the NumPy restatement of the reference CPU path (oracle/) on a bounded sample of
-               rows of the same workload, on this host, single-threaded NumPy.
+               mean launch duration from HIP events on the launch stream (a pass of its own after
+               the timed steps, `--kernel-events` launches), against 8 TB/s HBM; `traffic` comes
+               from the committed rocprofv3 PMC summary when present (extra.roofline_bwd: the
+               backward's two stages the same way)
+  cpu_baseline = the NumPy restatement of the reference CPU path (oracle/) on the whole workload,
+               on the GPU leg's own inputs, on this host, single-threaded NumPy.
 """
 
 from __future__ import annotations
@@ -25,6 +27,7 @@ import argparse
 import json
 import os
 import platform
+import statistics
 import subprocess
 import sys
 import time
@@ -62,8 +65,9 @@ def parse_args(argv=None):
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", choices=sorted(CONFIGS), default="C")
     p.add_argument("--sets", type=int, default=4, help="rotating buffer sets (MALL hygiene)")
-    p.add_argument("--event-every", type=int, default=10,
-                   help="record per-kernel HIP events on every N-th timed step")
+    p.add_argument("--kernel-events", type=int, default=100,
+                   help="launches of each kernel timed with HIP events after the timed steps "
+                        "(at least 50)")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU-baseline budget; 0 skips it")
     p.add_argument("--no-fp8", action="store_true",
@@ -95,24 +99,11 @@ def lscpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(rows: int, d: int, eps: float, budget_s: float, with_bwd: bool):
-    """The oracle (NumPy restatement of fused.py:28-66) on a bounded sample of rows."""
-    import numpy as np
-
-    from oracle import fused_rmsnorm as ora
-
-    sample_rows = min(rows, 1024)
-    rng = np.random.default_rng(0)
-    # bf16-representable inputs upcast to fp32, prepared outside the timed region
-    def bf16ish(a):
-        u = a.astype(np.float32).view(np.uint32)
-        u = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
-        return u.view(np.float32)
-    x = bf16ish(rng.standard_normal((sample_rows, d), dtype=np.float32))
-    res = bf16ish(rng.standard_normal((sample_rows, d), dtype=np.float32))
-    w = bf16ish((1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
-    g = bf16ish(rng.standard_normal((sample_rows, d), dtype=np.float32))
-
+def _time_oracle_step(ora, x, res, w, g, eps: float, with_bwd: bool, budget_s: float,
+                      min_runs: int = 5):
+    """Median wall time of the reference CPU path (fused.py:28-66 through the oracle's NumPy
+    restatement) on the given fp32 arrays: forward, then xhat = h * inv_rms and the backward.
+    One untimed warm-up, then at least `min_runs` timed runs and until `budget_s` has passed."""
     def one():
         y, h, inv = ora.fused_rmsnorm_residual_forward(x, res, w, eps)
         if with_bwd:
@@ -125,11 +116,32 @@ def cpu_baseline(rows: int, d: int, eps: float, budget_s: float, with_bwd: bool)
         t0 = time.perf_counter()
         one()
         times.append(time.perf_counter() - t0)
-        if len(times) >= 5 and time.perf_counter() - t_start >= budget_s:
+        if len(times) >= min_runs and time.perf_counter() - t_start >= budget_s:
             break
-    med = sorted(times)[len(times) // 2]
-    rows_per_s = sample_rows / med
+    return statistics.median(times), len(times)
 
+
+def cpu_baseline(rows: int, d: int, s: int, eps: float, budget_s: float, with_bwd: bool,
+                 inputs):
+    """The oracle (NumPy restatement of fused.py:28-66) timed on this host at the workload's
+    full size, on `inputs` = (x, residual, weight, grad_y): fp32 upcasts of the GPU leg's own
+    first buffer set (the same numbers the GPU computes on), copied to the host outside the
+    timed region.  GB/s uses the GPU workload's algorithmic bytes (element size `s`).  A
+    1024-row slice of the same arrays is timed too."""
+    import numpy as np
+
+    from oracle import fused_rmsnorm as ora
+
+    x, res, w, g = inputs
+    per_row = (fwd_bytes(rows, d, s) + (bwd_bytes(rows, d, s) if with_bwd else 0)) / rows
+    med, nruns = _time_oracle_step(ora, x, res, w, g, eps, with_bwd, budget_s)
+    rows_per_s = rows / med
+
+    sample_rows = min(rows, 1024)
+    smed, snruns = _time_oracle_step(ora, x[:sample_rows], res[:sample_rows], w,
+                                     g[:sample_rows], eps, with_bwd, min(budget_s, 2.0))
+
+    rng = np.random.default_rng(0)
     # the shapes of the reference's own benchmark (benchmarks/bench_vs_pytorch.py:43-72), fp32
     xb = rng.standard_normal((512, 4096), dtype=np.float32)
     wb = rng.standard_normal(4096, dtype=np.float32)
@@ -143,19 +155,22 @@ def cpu_baseline(rows: int, d: int, eps: float, budget_s: float, with_bwd: bool)
             t0 = time.perf_counter()
             fn()
             tt.append(time.perf_counter() - t0)
-        ref_shapes[name] = round(sorted(tt)[3] * 1e3, 3)
-    per_row = (fwd_bytes(rows, d, 2) + (bwd_bytes(rows, d, 2) if with_bwd else 0)) / rows
+        ref_shapes[name] = round(statistics.median(tt) * 1e3, 3)
     return {
         "value": round(rows_per_s * per_row / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"{sample_rows} of {rows} rows x {d}, fwd{'+bwd' if with_bwd else ''}, fp32 "
-                   f"upcasts of bf16-representable inputs, NumPy (single-threaded ufuncs); median "
-                   f"of {len(times)} runs after 1 warm-up; GB/s = rows/s x the bf16 algorithmic "
-                   f"bytes per row of the GPU workload"),
+        "sample": (f"the whole workload: {rows} rows x {d}, fwd{'+bwd' if with_bwd else ''}, on "
+                   f"fp32 upcasts of the GPU leg's own first buffer set; NumPy (single-threaded "
+                   f"ufuncs); median of {nruns} runs after 1 warm-up; GB/s = the GPU workload's "
+                   f"algorithmic bytes / median time"),
         "ms_median": round(med * 1e3, 3),
         "rows_per_s": round(rows_per_s, 1),
+        "runs": nruns,
+        "sample_1024_rows": {"ms_median": round(smed * 1e3, 3), "runs": snruns,
+                             "rows_per_s": round(sample_rows / smed, 1),
+                             "gbs": round(sample_rows / smed * per_row / 1e9, 4)},
         "host_cpu": lscpu_model(),
         "os_cpu_count": os.cpu_count(),
         "affinity_cpus": len(os.sched_getaffinity(0)),
@@ -163,12 +178,14 @@ def cpu_baseline(rows: int, d: int, eps: float, budget_s: float, with_bwd: bool)
     }
 
 
-def load_traffic(config: str):
+def load_traffic(config: str, which: str = "fwd"):
+    """HBM bytes per launch of the forward (`which` = "fwd") or of the backward's two stages
+    ("bwd") from the committed rocprofv3 PMC summary of `config`, or None."""
     path = os.path.join(REPO, "profiles", f"pmc_traffic_config_{config}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("fwd_traffic_bytes_per_launch")
+        return json.load(f).get(f"{which}_traffic_bytes_per_launch")
 
 
 def stream_ceilings(sets, stream_bytes: int, stream) -> dict:
@@ -542,10 +559,10 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True)
     return out
 
 
-def measure(lib, config: str, steps: int, warmup: int, nsets: int, event_every: int,
+def measure(lib, config: str, steps: int, warmup: int, nsets: int, kernel_events: int,
             stream) -> dict:
     """Time `steps` steps of `config` (forward, plus backward where the config has one) on
-    `nsets` rotating buffer sets; per-kernel HIP events on every `event_every`-th step."""
+    `nsets` rotating buffer sets, then per-kernel HIP events over `kernel_events` more steps."""
     import torch
 
     from velograd_amd import _lib
@@ -622,24 +639,31 @@ def measure(lib, config: str, steps: int, warmup: int, nsets: int, event_every: 
         _lib.check(step(k), "warm-up step")
     torch.cuda.synchronize()
 
-    # Kernel durations come from HIP events recorded on the launch stream inside the timed
-    # region, on every `event_every`-th step: each marker adds a little time to its step, so
-    # sampling keeps the wall-clock figure close to an unmarked run.
-    every = max(1, event_every)
-    sampled = [k for k in range(steps) if k % every == 0]
-    events = {k: [torch.cuda.Event(enable_timing=True) for _ in range(3)] for k in sampled}
-    torch.cuda.synchronize()
+    # Wall clock over `steps` unmarked steps: no event markers inside the timed region.
     t0 = time.perf_counter()
     rc = 0
     for k in range(steps):
-        rc |= step(k, events.get(k))
+        rc |= step(k)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     _lib.check(rc, "timed steps")
-    events = list(events.values())
 
-    fwd_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
-    mean_fwd_ms = sum(fwd_ms) / len(fwd_ms)
+    # Kernel durations: a pass of its own after the timed region, the same step sequence with
+    # HIP events on the launch stream around each forward and each backward (both stages),
+    # `kernel_events` launches of each whatever `steps` is.  The first step after the
+    # synchronisation is dropped (its launch starts from an idle queue).
+    nev = max(50, kernel_events)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(nev + 1)]
+    torch.cuda.synchronize()
+    rc = 0
+    for k in range(nev + 1):
+        rc |= step(steps + k, events[k])
+    torch.cuda.synchronize()
+    _lib.check(rc, "kernel event pass")
+    events = events[1:]
+
+    fwd_ms = [e[0].elapsed_time(e[1]) for e in events]
+    mean_fwd_ms = statistics.fmean(fwd_ms)
     fb = fwd_bytes(rows, d, s)
     bb = bwd_bytes(rows, d, s) if with_bwd else 0
     ms_per_step = (t1 - t0) * 1e3 / steps
@@ -648,17 +672,19 @@ def measure(lib, config: str, steps: int, warmup: int, nsets: int, event_every: 
         "value": value,
         "ms_per_step": ms_per_step,
         "fwd_us_mean": round(mean_fwd_ms * 1e3, 2),
-        "fwd_us_median": round(fwd_ms[len(fwd_ms) // 2] * 1e3, 2),
+        "fwd_us_median": round(statistics.median(fwd_ms) * 1e3, 2),
+        "fwd_us_min": round(min(fwd_ms) * 1e3, 2),
         "fwd_gbs": round(fb / (mean_fwd_ms * 1e-3) / 1e9, 1),
         "fwd_bytes": fb,
         "kernel_event_samples": len(events),
     }
     if with_bwd:
-        bwd_ms = sorted(e[1].elapsed_time(e[2]) for e in events)
-        mean_bwd_ms = sum(bwd_ms) / len(bwd_ms)
+        bwd_ms = [e[1].elapsed_time(e[2]) for e in events]
+        mean_bwd_ms = statistics.fmean(bwd_ms)
         out.update({
             "bwd_us_mean": round(mean_bwd_ms * 1e3, 2),
-            "bwd_us_median": round(bwd_ms[len(bwd_ms) // 2] * 1e3, 2),
+            "bwd_us_median": round(statistics.median(bwd_ms) * 1e3, 2),
+            "bwd_us_min": round(min(bwd_ms) * 1e3, 2),
             "bwd_gbs": round(bb / (mean_bwd_ms * 1e-3) / 1e9, 1),
             "bwd_bytes": bb,
             "bwd_workspace_bytes": ws_bytes,
@@ -759,7 +785,7 @@ def other_configs(lib, main_config: str, stream) -> dict:
     for cfg, steps, nsets in (("A", 2000, 4), ("B", 100, 4), ("C", 100, 4), ("D", 40, 2)):
         if cfg == main_config:
             continue
-        m = measure(lib, cfg, steps, 5, nsets, 5, stream)
+        m = measure(lib, cfg, steps, 5, nsets, 400 if cfg == "A" else 50, stream)
         for k in ("_sets", "_fwd_args", "_bwd_args", "_s", "_code"):
             m.pop(k)
         m["value"] = round(m["value"], 1)
@@ -788,7 +814,8 @@ def main(argv=None) -> int:
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
     rows, d, eps, with_bwd = CONFIGS[args.config]
-    m = measure(lib, args.config, args.steps, args.warmup, args.sets, args.event_every, stream)
+    m = measure(lib, args.config, args.steps, args.warmup, args.sets, args.kernel_events,
+                stream)
     sets, fwd_args, bwd_args = m.pop("_sets"), m.pop("_fwd_args"), m.pop("_bwd_args")
     fwd_fn = lib.velograd_rmsnorm_residual_fwd
     bwd_fn = lib.velograd_rmsnorm_residual_bwd
@@ -798,6 +825,19 @@ def main(argv=None) -> int:
     fb, bb = m["fwd_bytes"], m.get("bwd_bytes", 0)
     mean_fwd_ms = m["fwd_us_mean"] * 1e-3
     extra = m
+    if with_bwd:
+        # the backward (stage 1 + stage 2, one entry-point call) against the same roofline
+        bw_gbs = bb / (m["bwd_us_mean"] * 1e-6) / 1e9
+        extra["roofline_bwd"] = {
+            "bound": "hbm", "kernel": "bwd_vec_kernel + dweight_reduce_kernel",
+            "achieved": round(bw_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(bw_gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(args.config, "bwd"),
+            "us_mean": m["bwd_us_mean"], "us_median": m["bwd_us_median"]}
+    cpu_inputs = None
+    if args.cpu_seconds > 0:
+        b0 = sets[0]
+        cpu_inputs = tuple(b0[k].float().cpu().numpy() for k in ("x", "res", "w"))
+        cpu_inputs += (b0["g"].float().cpu().numpy() if with_bwd else None,)
 
     if not args.no_copy_ceiling:
         ceil = stream_ceilings(sets, rows * d * s, stream)
@@ -842,8 +882,9 @@ def main(argv=None) -> int:
         extra["other_configs"] = other_configs(lib, args.config, stream)
 
     cpu = None
-    if args.cpu_seconds > 0:
-        cpu = cpu_baseline(rows, d, eps, args.cpu_seconds, with_bwd)
+    if cpu_inputs is not None:
+        cpu = cpu_baseline(rows, d, s, eps, args.cpu_seconds, with_bwd, cpu_inputs)
+        del cpu_inputs
 
     line = {
         "metric": METRIC,
