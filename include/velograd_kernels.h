@@ -13,7 +13,9 @@
  *     calling thread is returned by velograd_kernels_last_error().
  *   - The library never allocates or frees device memory and never synchronises the host:
  *     every buffer (outputs and the backward workspace) belongs to the caller, and every
- *     launch is asynchronous on `hip_stream` (a hipStream_t; NULL = the null stream).
+ *     launch is asynchronous on `hip_stream` (a hipStream_t; NULL = the null stream).  The one
+ *     device array the library holds is the fixed 16 MiB scratch of
+ *     velograd_rmsnorm_residual_bwd_noalloc, placed with its code on each GPU it runs on.
  *   - Tensors are row-major [rows, dim] with unit stride along dim; `ld_*` is the row stride in
  *     elements.  Rows are independent; the normalisation runs over dim.
  *   - Results are deterministic: the same inputs on the same device give bitwise identical
@@ -195,6 +197,32 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
     const void* weight, const float* inv_rms, const void* grad_h,
     void* dx, void* dres, float* dweight,
     void* workspace, size_t ws_bytes,
+    int64_t rows, int64_t dim,
+    int64_t ld_g, int64_t ld_saved, int64_t ld_grad_h, int64_t ld_dx, int64_t ld_dres,
+    int32_t dtype, int32_t w_dtype, void* hip_stream);
+
+/*
+ * velograd_rmsnorm_residual_bwd without a workspace argument: the allocation-free variant.
+ * No counterpart in the reference.  It is for callers that cannot allocate device memory or
+ * size a workspace: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  It allocates nothing and calls no allocating routine; the dweight partial rows
+ * go to a scratch array of 16 MiB that the library holds on each GPU it runs on until the
+ * process ends.
+ *
+ *   Arguments and results as velograd_rmsnorm_residual_bwd (same kernels, so bitwise the same
+ *   outputs), minus `workspace` and `ws_bytes`.
+ *   Limit: returns VELOGRAD_ERR_WORKSPACE_TOO_SMALL, launching nothing, when dweight would
+ *   need more than the 16 MiB, i.e. one fp32 row of dim per partial: 256 partials on a 256-CU
+ *   MI355X for 16-byte-aligned bf16/fp16 rows up to dim 16384 (fp32 up to 4096), and up to
+ *   min(rows, 4 per CU) partials on the generic path (unaligned or odd-sized rows).
+ *   Calls that overlap on one GPU (several streams or host threads at once) share the scratch
+ *   and race: serialise them.  The scratch keeps the last call's contents; nothing in it has
+ *   to start at zero.
+ */
+VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd_noalloc(
+    const void* grad_y, const void* saved, int32_t saved_is_h,
+    const void* weight, const float* inv_rms, const void* grad_h,
+    void* dx, void* dres, float* dweight,
     int64_t rows, int64_t dim,
     int64_t ld_g, int64_t ld_saved, int64_t ld_grad_h, int64_t ld_dx, int64_t ld_dres,
     int32_t dtype, int32_t w_dtype, void* hip_stream);

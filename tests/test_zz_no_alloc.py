@@ -1,0 +1,152 @@
+"""velograd_rmsnorm_residual_bwd_noalloc, the allocation-free backward, through the C ABI.
+
+It runs the kernels of velograd_rmsnorm_residual_bwd with the dweight partial rows in the
+library's own device scratch array, so its outputs must equal that entry point's bit for bit.
+Two calls in a row, the second on a smaller input, show that what the first call left in the
+scratch does not leak into the second.  Sizes beyond the scratch are refused before anything is
+launched.  Graph replays of the variant equal its eager result."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from velograd_amd import _lib
+from velograd_amd import kernels as vk
+
+from tests._parity import assert_dweight, gaussian, to_device, upcast, weight_vec
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+SCRATCH_BYTES = 16 << 20
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _inputs(rng, rows, dim, dtype, wdtype, saved_is_h, grad_h):
+    g = to_device(gaussian(rng, (rows, dim)), dtype)
+    h = to_device(gaussian(rng, (rows, dim)), dtype)
+    w = to_device(weight_vec(rng, dim), wdtype)
+    inv = torch.from_numpy(
+        (1.0 / np.sqrt(np.mean(upcast(h).astype(np.float64) ** 2, axis=1) + 1e-5))
+        .astype(np.float32)).to(DEV)
+    saved = h if saved_is_h else (h.float() * inv[:, None]).to(dtype)
+    gh = to_device(gaussian(rng, (rows, dim)), dtype) if grad_h else None
+    return g, saved, w, inv, gh
+
+
+def _run(lib, noalloc, g, saved, saved_is_h, w, inv, gh, with_dres, with_dw):
+    rows, dim = g.shape
+    dx = torch.empty_like(g)
+    dres = torch.empty_like(g) if with_dres else None
+    dw = torch.empty(dim, device=DEV, dtype=torch.float32) if with_dw else None
+    code = _lib.TORCH_DTYPE_CODES[g.dtype]
+    wcode = _lib.TORCH_DTYPE_CODES[w.dtype]
+    stream = torch.cuda.current_stream().cuda_stream
+    head = (_p(g), _p(saved), int(saved_is_h), _p(w), _p(inv), _p(gh), _p(dx), _p(dres), _p(dw))
+    tail = (rows, dim, dim, dim, dim, dim, dim, code, wcode, stream)
+    if noalloc:
+        rc = lib.velograd_rmsnorm_residual_bwd_noalloc(*head, *tail)
+    else:
+        ws_bytes = vk.bwd_workspace_bytes(rows, dim, DEV)
+        ws = torch.empty(max(ws_bytes, 16), device=DEV, dtype=torch.uint8)
+        rc = lib.velograd_rmsnorm_residual_bwd(*head, _p(ws), ws_bytes, *tail)
+    _lib.check(rc, "noalloc" if noalloc else "workspace")
+    torch.cuda.synchronize()
+    return dx, dres, dw
+
+
+# (rows, dim, dtype, weight dtype, saved is h, grad_h, dres): the first call is the largest;
+# every later one is smaller and takes another plan (1024-thread rows, 64-thread row groups,
+# the generic kernel for an odd dim).
+CALLS = [
+    (4096, 4096, torch.bfloat16, torch.bfloat16, True, False, True),
+    (300, 1000, torch.bfloat16, torch.float32, False, True, False),
+    (257, 1001, torch.float32, torch.float32, True, False, False),
+]
+
+
+def test_noalloc_matches_workspace_entry_point_on_calls_in_a_row():
+    lib = _lib.load()
+    rng = np.random.default_rng(0)
+    for i, (rows, dim, dt, wdt, sih, gh, dres) in enumerate(CALLS):
+        print(f"noalloc call {i}: rows={rows} dim={dim} {dt} w={wdt} saved_is_h={sih} "
+              f"grad_h={gh} dres={dres}", flush=True)
+        need = vk.bwd_workspace_bytes(rows, dim, DEV)
+        assert 0 < need <= SCRATCH_BYTES
+        g, saved, w, inv, ghv = _inputs(rng, rows, dim, dt, wdt, sih, gh)
+        want = _run(lib, False, g, saved, sih, w, inv, ghv, dres, True)
+        got = _run(lib, True, g, saved, sih, w, inv, ghv, dres, True)
+        assert torch.equal(got[0], want[0]), f"call {i}: dx differs"
+        if dres:
+            assert torch.equal(got[1], want[1]), f"call {i}: dres differs"
+            assert torch.equal(got[1], got[0])
+        assert torch.equal(got[2], want[2]), f"call {i}: dweight differs"
+        # and dweight is the sum over rows of g * xhat (float64 truth), to the parity bar
+        xhat = upcast(saved).astype(np.float64)
+        if sih:
+            xhat = xhat * upcast(inv).astype(np.float64)[:, None]
+        truth = (upcast(g).astype(np.float64) * xhat).sum(axis=0)
+        assert_dweight(upcast(got[2]), truth, what=f"call {i} dweight")
+
+
+def test_noalloc_without_dweight_matches():
+    lib = _lib.load()
+    rng = np.random.default_rng(1)
+    g, saved, w, inv, _ = _inputs(rng, 512, 2048, torch.bfloat16, torch.bfloat16, True, False)
+    want = _run(lib, False, g, saved, True, w, inv, None, False, False)
+    got = _run(lib, True, g, saved, True, w, inv, None, False, False)
+    assert torch.equal(got[0], want[0])
+
+
+def test_noalloc_refuses_sizes_beyond_the_scratch():
+    lib = _lib.load()
+    # fp32 rows of 16384 take the generic kernel: 1024 partial rows of 64 KiB = 64 MiB
+    rows, dim = 2048, 16384
+    assert vk.bwd_workspace_bytes(rows, dim, DEV) > SCRATCH_BYTES
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.velograd_rmsnorm_residual_bwd_noalloc(
+        16, 48, 1, 64, 80, None, 96, None, 112, rows, dim, dim, dim, dim, dim, dim,
+        _lib.DTYPE_F32, _lib.DTYPE_F32, stream)
+    assert rc == _lib.ERR_WORKSPACE_TOO_SMALL
+    msg = _lib.last_error()
+    assert "fixed maximum" in msg and str(SCRATCH_BYTES) in msg, msg
+
+
+def test_noalloc_graph_replays_equal_eager():
+    """The variant's use case: HIP graph capture with no allocation inside the captured work.
+    Each replay follows eager work on the same stream and is checked against the eager bits."""
+    lib = _lib.load()
+    rng = np.random.default_rng(2)
+    rows, dim = 2048, 4096
+    g, saved, w, inv, _ = _inputs(rng, rows, dim, torch.bfloat16, torch.bfloat16, True, False)
+    want = _run(lib, True, g, saved, True, w, inv, None, False, True)
+    dx = torch.empty_like(g)
+    dw = torch.empty(dim, device=DEV, dtype=torch.float32)
+    code = _lib.DTYPE_BF16
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = lib.velograd_rmsnorm_residual_bwd_noalloc(
+                _p(g), _p(saved), 1, _p(w), _p(inv), None, _p(dx), None, _p(dw), rows, dim,
+                dim, dim, dim, dim, dim, code, code, ctypes.c_void_p(side.cuda_stream))
+    torch.cuda.current_stream().wait_stream(side)
+    _lib.check(rc, "noalloc under capture")
+    for rep in range(4):
+        # eager work in between: a no-alloc backward on other inputs (it rewrites the scratch),
+        # then the outputs are clobbered
+        other = _inputs(rng, 1024, 4096, torch.bfloat16, torch.bfloat16, True, False)
+        _run(lib, True, other[0], other[1], True, other[2], other[3], None, False, True)
+        dx.fill_(float("nan"))
+        dw.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dx, want[0]), f"replay {rep}: dx differs"
+        assert torch.equal(dw, want[2]), f"replay {rep}: dweight differs"

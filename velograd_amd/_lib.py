@@ -106,6 +106,17 @@ SIGNATURES = {
          _c_i32, _c_i32,                    # dtype, w_dtype
          _c_ptr],                           # hip_stream
     ),
+    "velograd_rmsnorm_residual_bwd_noalloc": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_i32,            # grad_y, saved, saved_is_h
+         _c_ptr, _c_ptr, _c_ptr,            # weight, inv_rms, grad_h
+         _c_ptr, _c_ptr, _c_ptr,            # dx, dres, dweight
+         _c_i64, _c_i64,                    # rows, dim
+         _c_i64, _c_i64, _c_i64,            # ld_g, ld_saved, ld_grad_h
+         _c_i64, _c_i64,                    # ld_dx, ld_dres
+         _c_i32, _c_i32,                    # dtype, w_dtype
+         _c_ptr],                           # hip_stream
+    ),
     "velograd_rmsnorm_rope_bwd": (
         _c_i32,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr,    # grad_y, h, weight, inv_rms

@@ -23,6 +23,8 @@
 // Row sums: DPP inside each 16-lane row of the wave, readlane across the four rows, LDS only
 // across the waves that share a row; every order is fixed, so results are bitwise reproducible.
 
+#include <mutex>
+
 #include "common.h"
 #include "fp8_e4m3.h"
 #include "mx_formats.h"
@@ -1167,6 +1169,35 @@ size_t workspace_bytes_for(int64_t rows, int64_t dim, int cus) {
   return vg_plan::bwd_workspace_bytes(rows, dim, cus, t.bwd_nv, t.bwd_block, t.bwd_waves_per_cu);
 }
 
+// ------------------------------------------------------------------------------------------
+// Scratch of the allocation-free backward (velograd_rmsnorm_residual_bwd_noalloc): the dweight
+// partial rows live in this file-scope device array instead of a caller workspace.  Each GPU
+// the library runs on holds its own copy, at its own address, until the process ends.  In host
+// code `scratch` names a host-side stand-in, never the device memory: the device address comes
+// from hipGetSymbolAddress, once per device with that device current, and only that address is
+// passed to kernels.  Nothing in it needs to start at zero (stage 1 writes every partial row it
+// hands to stage 2 before stage 2 reads it), so no call clears it.  Calls that overlap on one
+// GPU (two streams, or two host threads) share the array and race.
+// ------------------------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// Device address of `scratch` on `device` (the current device), or null with the HIP error.
+void* scratch_on(int device, hipError_t* err) {
+  std::call_once(g_scratch_once[device], [device] {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_err[device] = e;
+    g_scratch_ptr[device] = (e == hipSuccess) ? p : nullptr;
+  });
+  *err = g_scratch_err[device];
+  return g_scratch_ptr[device];
+}
+
 // Shared by the forward entry points.  `out` is the epilogue (kOut*): for kOutFp8Row y holds one
 // e4m3 byte per element and y_scale one fp32 per row; for the MX modes y holds e4m3 bytes or
 // e2m1 nibbles and mx_scale one E8M0 byte per 32 elements.  ld_y (and ld_mx) count bytes then.
@@ -1288,7 +1319,7 @@ int32_t run_bwd(const void* grad_y, const void* saved, int32_t saved_is_h, const
                 void* workspace, size_t ws_bytes, int64_t rows, int64_t dim, int64_t ld_g,
                 int64_t ld_saved, int64_t ld_grad_h, int64_t ld_dx, int64_t ld_dres,
                 int32_t dtype, int32_t w_dtype, void* hip_stream, int64_t rope_seq = 0,
-                float rope_base = 0.0f) {
+                float rope_base = 0.0f, bool static_scratch = false) {
   if (!types_ok(dtype, w_dtype))
     return fail(VELOGRAD_ERR_UNSUPPORTED_DTYPE,
                 "bwd: unsupported dtype/w_dtype pair (%d, %d): weight must be the activation "
@@ -1356,6 +1387,23 @@ int32_t run_bwd(const void* grad_y, const void* saved, int32_t saved_is_h, const
   float* partial = nullptr;
   if (dweight != nullptr) {
     const size_t need = (size_t)plan.wgs * (size_t)dim * sizeof(float);
+    if (static_scratch) {
+      // velograd_rmsnorm_residual_bwd_noalloc: the partial rows go to the library's own array
+      if (need > kNoAllocScratchBytes)
+        return fail(VELOGRAD_ERR_WORKSPACE_TOO_SMALL,
+                    "bwd_noalloc: dweight needs %zu bytes of scratch for rows=%lld dim=%lld, above "
+                    "the fixed maximum of %zu bytes; pass a workspace to "
+                    "velograd_rmsnorm_residual_bwd instead",
+                    need, (long long)rows, (long long)dim, kNoAllocScratchBytes);
+      if (device < 0 || device >= kMaxDevices)
+        return fail(VELOGRAD_ERR_DEVICE_QUERY, "bwd_noalloc: device %d out of range", device);
+      hipError_t e = hipSuccess;
+      workspace = scratch_on(device, &e);
+      if (workspace == nullptr)
+        return fail((int32_t)e, "bwd_noalloc: hipGetSymbolAddress of the scratch failed: %s",
+                    hipGetErrorString(e));
+      ws_bytes = kNoAllocScratchBytes;
+    }
     if (workspace == nullptr || ws_bytes < need)
       return fail(VELOGRAD_ERR_WORKSPACE_TOO_SMALL,
                   "bwd: workspace of %zu bytes given, %zu needed", ws_bytes, need);
@@ -1475,6 +1523,16 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
   return run_bwd(grad_y, saved, saved_is_h, weight, inv_rms, grad_h, dx, dres, dweight, workspace,
                  ws_bytes, rows, dim, ld_g, ld_saved, ld_grad_h, ld_dx, ld_dres, dtype, w_dtype,
                  hip_stream);
+}
+
+VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd_noalloc(
+    const void* grad_y, const void* saved, int32_t saved_is_h, const void* weight,
+    const float* inv_rms, const void* grad_h, void* dx, void* dres, float* dweight, int64_t rows,
+    int64_t dim, int64_t ld_g, int64_t ld_saved, int64_t ld_grad_h, int64_t ld_dx,
+    int64_t ld_dres, int32_t dtype, int32_t w_dtype, void* hip_stream) {
+  return run_bwd(grad_y, saved, saved_is_h, weight, inv_rms, grad_h, dx, dres, dweight, nullptr,
+                 0, rows, dim, ld_g, ld_saved, ld_grad_h, ld_dx, ld_dres, dtype, w_dtype,
+                 hip_stream, 0, 0.0f, /*static_scratch=*/true);
 }
 
 VELOGRAD_API int32_t velograd_rmsnorm_rope_bwd(
