@@ -13,8 +13,8 @@ touched by the step before it.
 Output: one JSON line (the driver's contract) with
   value      = algorithmic bytes of a step / wall time of a step (GB/s, whole job, 1 GPU)
   roofline   = the forward kernel (the larger of the two): algorithmic bytes per launch over its
-               mean launch time from HIP events on the launch stream, after the timed steps:
-               batches of 10 back-to-back launches with events around each batch only
+               mean launch time from HIP events on the launch stream, in passes run before the
+               warm-up: batches of 10 back-to-back launches with events around each batch only
                (`--kernel-events` launches); per-launch events in the step sequence give the
                medians and minima.  Against 8 TB/s HBM; `traffic` comes from the committed
                rocprofv3 PMC summary when present (extra.roofline_bwd: the backward's two stages
@@ -68,7 +68,7 @@ def parse_args(argv=None):
     p.add_argument("--config", choices=sorted(CONFIGS), default="C")
     p.add_argument("--sets", type=int, default=4, help="rotating buffer sets (MALL hygiene)")
     p.add_argument("--kernel-events", type=int, default=100,
-                   help="launches of each kernel timed with HIP events after the timed steps "
+                   help="launches of each kernel timed with HIP events before the warm-up "
                         "(at least 50)")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU-baseline budget; 0 skips it")
@@ -78,6 +78,8 @@ def parse_args(argv=None):
                    help="skip the B/C/D summary lines (reported under extra)")
     p.add_argument("--no-decode", action="store_true",
                    help="skip the config E decode-latency table (reported under extra)")
+    p.add_argument("--decode-calls", type=int, default=1000,
+                   help="calls per config E shape for the back-to-back and host timings")
     p.add_argument("--no-rope", action="store_true",
                    help="skip timing the fused RoPE kernel (reported under extra)")
     p.add_argument("--no-norm-rope", action="store_true",
@@ -637,29 +639,18 @@ def measure(lib, config: str, steps: int, warmup: int, nsets: int, kernel_events
                 evs[2].record(stream)
         return rc
 
-    for k in range(warmup):
-        _lib.check(step(k), "warm-up step")
-    torch.cuda.synchronize()
-
-    # Wall clock over `steps` unmarked steps: no event markers inside the timed region.
-    t0 = time.perf_counter()
-    rc = 0
-    for k in range(steps):
-        rc |= step(k)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    _lib.check(rc, "timed steps")
-
-    # Kernel durations: a pass of its own after the timed region, the same step sequence with
-    # HIP events on the launch stream around each forward and each backward (both stages),
-    # `kernel_events` launches of each whatever `steps` is.  The first step after the
-    # synchronisation is dropped (its launch starts from an idle queue).
+    # Kernel durations, in passes of their own before the warm-up and the timed steps: the step
+    # sequence with HIP events on the launch stream around each forward and each backward (both
+    # stages), `kernel_events` launches of each whatever `steps` is; the first step after the
+    # synchronisation is dropped (its launch starts from an idle queue).  Running them first
+    # also means the timed steps start on a GPU that has been busy, as in a training loop: with
+    # a 5-step warm-up straight after setup, 20 timed steps read about 4% below the steady state.
     nev = max(50, kernel_events)
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(nev + 1)]
     torch.cuda.synchronize()
     rc = 0
     for k in range(nev + 1):
-        rc |= step(steps + k, events[k])
+        rc |= step(k, events[k])
     torch.cuda.synchronize()
     _lib.check(rc, "kernel event pass")
     events = events[1:]
@@ -684,6 +675,19 @@ def measure(lib, config: str, steps: int, warmup: int, nsets: int, kernel_events
 
     fwd_batch_ms, nbatched = batch_mean_ms(fwd_fn, fwd_args)
     bwd_batch_ms = batch_mean_ms(bwd_fn, bwd_args)[0] if with_bwd else None
+
+    for k in range(warmup):
+        _lib.check(step(k), "warm-up step")
+    torch.cuda.synchronize()
+
+    # Wall clock over `steps` unmarked steps: no event markers inside the timed region.
+    t0 = time.perf_counter()
+    rc = 0
+    for k in range(steps):
+        rc |= step(k)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.check(rc, "timed steps")
 
     fwd_ms = [e[0].elapsed_time(e[1]) for e in events]
     mean_fwd_ms = fwd_batch_ms
@@ -903,7 +907,7 @@ def main(argv=None) -> int:
             extra["torch_eager_step_us"] / (ms_per_step * 1e3), 3)
         extra["reference_benchmark_shapes"] = reference_benchmark_shapes(stream)
     if not args.no_decode:
-        extra["config_E_decode"] = decode_latency(lib, stream)
+        extra["config_E_decode"] = decode_latency(lib, stream, max(10, args.decode_calls))
     if not args.no_other_configs:
         del sets, fwd_args, bwd_args
         torch.cuda.empty_cache()
