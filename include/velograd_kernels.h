@@ -266,7 +266,9 @@ VELOGRAD_API size_t velograd_rmsnorm_residual_bwd_workspace_bytes(int64_t rows, 
 /*
  * Rotary position embedding on one tensor (call once for q and once for k), laid out as
  * [outer, seq, heads, dim]; the position of x[o, s, h, :] is s.  For j < rot_dim / 2,
- *   freq_j = 1 / theta^(2j / rot_dim), angle = s * freq_j (fp32), and the pair (a, b) of j
+ *   freq_j = 1 / theta^(2j / rot_dim), angle = s * freq_j (fp32 for VELOGRAD_ROPE_HALF as
+ *   fused.py:98-103 forms it; double, reduced exactly before a float32 sincospi, for
+ *   VELOGRAD_ROPE_INTERLEAVED as functional.py:302-305 does), and the pair (a, b) of j
  *   becomes (a cos - b sin, a sin + b cos); elements rot_dim .. dim-1 are copied.
  * pairing VELOGRAD_ROPE_HALF: (a, b) = (x_j, x_{j + rot_dim/2}).  Replaces fused_rope_forward
  *   (python/velograd/kernels/fused.py:72-130; positions fused.py:96-98, angles :98-103, copied

@@ -139,12 +139,13 @@ def test_rope_empty_and_deterministic():
 # Interleaved pairs: the reference model's apply_rotary_emb (functional.py:287-345)
 # ---------------------------------------------------------------------------------------------
 def _interleaved_bound(x: np.ndarray, base: float) -> np.ndarray:
-    """The angle-scaled float32 tolerance of tests/_parity.py for pairs (x_2i, x_2i+1)."""
+    """Tolerance for pairs (x_2i, x_2i+1): ROPE_ANGLE_ULPS float32 ulps of the pair for cos and
+    sin plus 2^-21 for the rotation's products.  It does not grow with the position: both paths
+    form the angles in double (as the reference's Python floats do) and reduce them exactly
+    before a float32 sincospi (the scalar path) or walk them in double (the 16-byte path)."""
     x = np.abs(np.asarray(x, np.float64))
-    seq, dim = x.shape[-2], x.shape[-1]
-    ang = np.arange(seq)[:, None] * base ** (-2.0 * np.arange(dim // 2) / dim)
     mag = x[..., 0::2] + x[..., 1::2]
-    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 * np.maximum(ang, 1.0) + 2.0 ** -21) * mag
+    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -21) * mag
     out = np.empty_like(x)
     out[..., 0::2] = b
     out[..., 1::2] = b
@@ -154,7 +155,10 @@ def _interleaved_bound(x: np.ndarray, base: float) -> np.ndarray:
 INTERLEAVED_CASES = [(torch.float32, (37, 64)), (torch.bfloat16, (2, 128, 4096)),
                      (torch.float16, (3, 50, 256)), (torch.bfloat16, (1, 64, 8192)),
                      (torch.float32, (3, 5, 6)), (torch.bfloat16, (2, 9, 12)),
-                     (torch.float32, (2, 9, 12)), (torch.float32, (4, 2, 3, 40))]
+                     (torch.float32, (2, 9, 12)), (torch.float32, (4, 2, 3, 40)),
+                     # the scalar path at long positions (10 and 12 elements do not split into
+                     # 16-byte chunks of whole pairs)
+                     (torch.float32, (1, 32768, 10)), (torch.bfloat16, (1, 20000, 12))]
 
 
 @pytest.mark.parametrize("dtype,shape", INTERLEAVED_CASES,

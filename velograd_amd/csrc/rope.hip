@@ -2,7 +2,8 @@
 // pairings of a head vector's elements.
 //
 // Math, for every head vector x[o, s, h, :] at position s and pair j < half = rot_dim / 2:
-//     freq_j = 1 / theta^(2j / rot_dim),  angle = s * freq_j          (fp32, fused.py:98-103)
+//     freq_j = 1 / theta^(2j / rot_dim),  angle = s * freq_j
+//     (fp32 for rotate half, fused.py:98-103; double for interleaved, functional.py:302-305)
 //     (a, b) -> (a cos - b sin,  a sin + b cos)
 //   "rotate half" (python/velograd/kernels/fused.py:72-130, src/cuda/fused_kernels.cu:145-181):
 //     (a, b) = (x_j, x_{j+half}); elements at rot_dim and beyond are copied (fused.py:119-120).
@@ -17,7 +18,7 @@
 // head), then streams the tokens' elements with 16-byte loads and stores, every element moving
 // through HBM once.  The kernel is HBM-bound: ~6 flops per element pair.
 //
-// Numerics: freq_j = 1 / powf(theta, e) in float32, as the reference forms it with NumPy's
+// Numerics of rotate half: freq_j = 1 / powf(theta, e) in float32, as the reference forms it with NumPy's
 // float32 power (faithful, within 1 ulp; so is ocml's powf: the two may differ by an ulp or
 // two, which moves the angle by that many ulps of |angle|); the angle is the float32 product
 // s * freq_j as np.outer forms it; sincosf is ocml's (a few ulps); products and sums round as
@@ -51,9 +52,32 @@ struct RopeArgs {
   int32_t interleaved;  // pairs (2j, 2j+1) instead of (j, j + half)
 };
 
-// Fills freq[half], then cos/sin[t * half + j] for the workgroup's tokens.
+constexpr double kInv2Pi = 0.159154943091895335768883763372514362;  // 1 / (2 pi)
+
+// Fills freq[half], then cos/sin[t * half + j] for the workgroup's tokens.  Rotate-half forms
+// them in float32 as its reference does (fused.py:98-103); the interleaved pairing forms freq_j
+// and the angle in double, as its reference's Python floats do (functional.py:302-305), and
+// reduces the angle exactly to [-1/2, 1/2] revolutions before a float32 sincospi, so cos and
+// sin are within a few float32 ulps at any position (the 16-byte path, rope_run_kernel, walks
+// the same double-precision angles).
 __device__ inline void rope_tables(const RopeArgs& a, int64_t tok0, int ntok, float* freq,
                                    float* cs, float* sn) {
+  if (a.interleaved) {
+    const double log2_theta = log2((double)a.theta);
+    const int n = ntok * a.half;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int t = i / a.half;
+      const int j = i - t * a.half;
+      const double fr = exp2(-(double)j / (double)a.half * log2_theta);  // 1/theta^(2j/rot_dim)
+      const double rev = (double)((tok0 + t) % a.seq) * fr * kInv2Pi;
+      float s, c;
+      sincospif(2.0f * (float)(rev - rint(rev)), &s, &c);
+      cs[i] = c;
+      sn[i] = a.sin_sign * s;
+    }
+    __syncthreads();
+    return;
+  }
   for (int j = threadIdx.x; j < a.half; j += blockDim.x) {
     const float e = (2.0f * (float)j) / (float)(2 * a.half);          // fused.py:100
     const float p = powf(a.theta, e);
