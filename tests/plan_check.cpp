@@ -114,6 +114,29 @@ int main() {
                   CHECK((size_t)br.wgs * (size_t)dim * sizeof(float) <= ws,
                         "rope partials %lld x %lld exceed workspace %zu", (long long)br.wgs,
                         (long long)dim, ws);
+                  // the ring-pipelined plan: whole rows, its own block bound, one workgroup per
+                  // CU at most, its partials within the workspace
+                  const BwdPlan rg = plan_bwd_ring(rows, dim, eb, aligned != 0, cus, prefer);
+                  if (rg.ring) {
+                    check_row_plan(rg.rp, dim, eb, aligned != 0);
+                    CHECK(ring_eligible(rg.rp, dim, eb), "ring plan not eligible dim=%lld",
+                          (long long)dim);
+                    CHECK((int64_t)rg.rp.nv * rg.rp.tpr * (16 / eb) == dim,
+                          "ring plan over a partial row dim=%lld", (long long)dim);
+                    CHECK(rg.rp.block <= kRingBlock && rg.rp.nv <= kRingMaxNV,
+                          "ring block %d nv %d", rg.rp.block, rg.rp.nv);
+                    CHECK(rg.wgs >= 1 && rg.wgs <= cus &&
+                              rg.wgs <= (rows + rg.rp.groups - 1) / rg.rp.groups,
+                          "ring wgs=%lld", (long long)rg.wgs);
+                    CHECK((size_t)rg.wgs * (size_t)dim * sizeof(float) <= ws,
+                          "ring partials %lld x %lld exceed workspace %zu", (long long)rg.wgs,
+                          (long long)dim, ws);
+                    CHECK(rg.lds_bytes <= 64 * 1024 &&
+                              (rg.lds_bytes == 0) == (rg.rp.groups == 1),
+                          "ring lds %zu", rg.lds_bytes);
+                  } else {
+                    CHECK(!ring_eligible(rg.rp, dim, eb), "eligible ring plan refused");
+                  }
                   ++plans;
                 }
               }

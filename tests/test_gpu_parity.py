@@ -166,8 +166,10 @@ def test_config_d_bf16_outliers_sampled_rows():
     x = (torch.randn(rows, d, device="cuda", generator=gen) * 2.0)
     res = (torch.randn(rows, d, device="cuda", generator=gen) * 2.0)
     for t in (x, res):
-        idx = torch.randint(0, rows * d, (rows * d // 1000,), device="cuda", generator=gen)
+        # exactly 0.1% of the entries, distinct and uniformly chosen, x50 (bench.py's recipe)
+        idx = torch.randperm(rows * d, device="cuda", generator=gen)[:rows * d // 1000]
         t.view(-1)[idx] *= 50.0
+        del idx
     x, res = x.to(torch.bfloat16), res.to(torch.bfloat16)
     w = (1 + 0.1 * torch.randn(d, device="cuda", generator=gen)).to(torch.bfloat16)
     g = torch.randn(rows, d, device="cuda", generator=gen).to(torch.bfloat16)

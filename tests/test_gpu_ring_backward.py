@@ -1,0 +1,140 @@
+"""The ring-pipelined backward (bwd_ring_kernel, the default for whole rows of up to 512 threads
+and two 16-byte chunks per thread) against the oracle, at row counts that put every pattern of
+its loop to work: rows fewer than the row slots (no steady iteration), whole rings of
+iterations, and one or two iterations past the last whole ring, with and without rows missing in
+the last one; the ring holds three rows (two with grad_h).  Its per-row arithmetic is that of
+bwd_vec_kernel, so dx must equal that kernel's bit for bit (the child process below runs it with
+VELOGRAD_BWD_RING=0); dweight groups its partial sums by other row slots, so it is held to the
+dweight tolerance."""
+
+import json
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fused_rmsnorm as ora
+from tests import _parity as P
+from velograd_amd import kernels as vk
+
+pytestmark = pytest.mark.gpu
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _inputs(rows, d, dtype, wdtype, seed, grad_h):
+    rng = np.random.default_rng(seed)
+    h = P.to_device(P.gaussian(rng, (rows, d)), dtype)
+    g = P.to_device(P.gaussian(rng, (rows, d)), dtype)
+    w = P.to_device(P.weight_vec(rng, d), wdtype)
+    gh = P.to_device(P.gaussian(rng, (rows, d)), dtype) if grad_h else None
+    _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
+    return h, g, w, inv, gh
+
+
+def _check_oracle(dx, dw, h, g, w, inv, gh, what):
+    g32, h32, w32, r32 = (P.upcast(t) for t in (g, h, w, inv))
+    xhat = h32 * r32
+    if gh is None:
+        rdx, rdw = ora.fused_rmsnorm_residual_backward(g32, xhat, w32, r32)
+    else:
+        rdx, rdw = ora.backward_with_residual_grad(g32, xhat, w32, r32, P.upcast(gh))
+    if dx.dtype == torch.float32:
+        scale = P.dx_scale(g32 * w32, xhat, r32) + (0.0 if gh is None else np.abs(P.upcast(gh)))
+        assert np.max(np.abs(P.upcast(dx) - rdx) / scale) <= P.FP32_REL_TOL, what
+    else:
+        P.dx_check(dx, rdx, g32 * w32, xhat, r32, what,
+                   grad_h=None if gh is None else P.upcast(gh))
+    P.assert_dweight(P.upcast(dw), rdw, what)
+
+
+# 256 CUs x 2 row groups of 256 threads = 512 row slots at dim 4096 bf16
+RING_ROWS = [1, 2, 300, 511, 512, 513, 1024, 1025, 1535, 1536, 1537, 2047, 2560, 16385]
+
+
+@pytest.mark.parametrize("grad_h", [False, True], ids=["ring3", "ring2-grad_h"])
+@pytest.mark.parametrize("rows", RING_ROWS)
+def test_ring_row_counts_match_oracle(rows, grad_h):
+    print(f"ring backward rows={rows} grad_h={grad_h}", flush=True)
+    h, g, w, inv, gh = _inputs(rows, 4096, torch.bfloat16, torch.bfloat16, rows, grad_h)
+    dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=gh)
+    torch.cuda.synchronize()
+    _check_oracle(dx, dw, h, g, w, inv, gh, f"rows={rows} grad_h={grad_h}")
+
+
+# (rows, dim, dtype, weight dtype, grad_h): one row group per workgroup (tpr 512), eight groups
+# of one wave (dim 512), fp32 and fp16 with an fp32 weight
+LAYOUTS = [(3000, 8192, torch.bfloat16, torch.bfloat16, False),
+           (2049, 512, torch.bfloat16, torch.float32, True),
+           (1500, 2048, torch.float32, torch.float32, False),
+           (999, 1024, torch.float16, torch.float32, True)]
+
+_CHILD = r"""
+import json, sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+from tests import _parity as P
+from velograd_amd import kernels as vk
+cases = json.loads(sys.argv[2])
+out = {}
+for i, (rows, d, dt, wdt, gh) in enumerate(cases):
+    dt, wdt = getattr(torch, dt), getattr(torch, wdt)
+    rng = np.random.default_rng(rows * 7 + d)
+    h = P.to_device(P.gaussian(rng, (rows, d)), dt)
+    g = P.to_device(P.gaussian(rng, (rows, d)), dt)
+    w = P.to_device(P.weight_vec(rng, d), wdt)
+    ghv = P.to_device(P.gaussian(rng, (rows, d)), dt) if gh else None
+    _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
+    dx, _ = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=ghv)
+    out[f"dx{i}"] = dx.view(torch.int16 if dx.element_size() == 2 else torch.int32).cpu().numpy()
+np.savez(sys.argv[3], **out)
+"""
+
+
+def test_ring_dx_equals_the_previous_kernel_bitwise(tmp_path):
+    cases = [(r, d, str(dt).split(".")[-1], str(wdt).split(".")[-1], gh)
+             for r, d, dt, wdt, gh in LAYOUTS]
+    path = str(tmp_path / "legacy.npz")
+    env = dict(os.environ, VELOGRAD_BWD_RING="0")
+    print("child process: the same backwards with VELOGRAD_BWD_RING=0", flush=True)
+    r = subprocess.run([sys.executable, "-c", _CHILD, REPO, json.dumps(cases), path], env=env,
+                       capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    legacy = np.load(path)
+    for i, (rows, d, dt, wdt, gh) in enumerate(LAYOUTS):
+        print(f"ring vs previous kernel: {rows}x{d} {dt} w={wdt} grad_h={gh}", flush=True)
+        rng = np.random.default_rng(rows * 7 + d)
+        h = P.to_device(P.gaussian(rng, (rows, d)), dt)
+        g = P.to_device(P.gaussian(rng, (rows, d)), dt)
+        w = P.to_device(P.weight_vec(rng, d), wdt)
+        ghv = P.to_device(P.gaussian(rng, (rows, d)), dt) if gh else None
+        _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
+        dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=ghv)
+        bits = dx.view(torch.int16 if dx.element_size() == 2 else torch.int32).cpu().numpy()
+        assert np.array_equal(bits, legacy[f"dx{i}"]), f"dx differs at {rows}x{d} {dt}"
+        _check_oracle(dx, dw, h, g, w, inv, ghv, f"{rows}x{d} {dt}")
+
+
+def test_ring_dres_and_in_place_grad_h():
+    """dres gets the same bits as dx; dx may be grad_h itself (accumulation in place)."""
+    from velograd_amd import _lib
+    lib = _lib.load()
+    rows, d = 2500, 4096
+    h, g, w, inv, gh = _inputs(rows, d, torch.bfloat16, torch.bfloat16, 5, True)
+    ref, _ = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=gh)
+    dres = torch.empty_like(g)
+    dx, _ = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=gh,
+                                               dresidual_out=dres)
+    assert torch.equal(dx, ref) and torch.equal(dres, ref)
+    acc = gh.clone()
+    inv1 = inv.reshape(rows).contiguous()
+    rc = lib.velograd_rmsnorm_residual_bwd(
+        g.data_ptr(), h.data_ptr(), 1, w.data_ptr(), inv1.data_ptr(), acc.data_ptr(),
+        acc.data_ptr(), None, None, None, 0, rows, d, d, d, d, d, d,
+        _lib.DTYPE_BF16, _lib.DTYPE_BF16, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "ring backward in place")
+    assert torch.equal(acc, ref)

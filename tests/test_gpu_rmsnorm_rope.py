@@ -136,27 +136,29 @@ def test_errors():
 # the norm's backward.  Truth is the composition of the two pinned float64 oracles: the inverse
 # interleaved rotation (functional.py:316-345) then the module backward (nn.py:357-383) with the
 # device's h and inv_rms.  Bound: 16 float32 ulps of each gradient pair (angles in double), plus
-# 2^-16 of the pair for the float32 rotation recurrence of the walk,
+# 2^-18 of the pair for the float32 rotation recurrence of the walk (re-evaluated directly every
+# 16 rows, so at most 15 steps of a few ulps each, whatever the walk's length),
 # propagated through dx = r (w g - xhat mean(w g xhat)) and dweight = sum g xhat; on top of it
 # the usual dx rule (1 ulp or the operand-scaled floor) and the dweight rule (1e-3).
 # ---------------------------------------------------------------------------------------------
 def _rope_grad_bound(g: np.ndarray, base: float) -> np.ndarray:
     mag = np.abs(g[..., 0::2]) + np.abs(g[..., 1::2])
-    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -16) * mag
+    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -18) * mag
     out = np.empty_like(g)
     out[..., 0::2] = b
     out[..., 1::2] = b
     return out
 
 
-def _check_rope_backward(dx, dw, g, h, w, inv, base, what, g_round=0.0):
+def _check_rope_backward(dx, dw, g, h, w, inv, base, what, g_round=0.0, positions=None):
     """`g_round`: relative rounding of the rotated-back gradient before the norm's backward
-    (the two-pass path stores it in the activation dtype; the fused pass keeps it in fp32)."""
+    (the two-pass path stores it in the activation dtype; the fused pass keeps it in fp32).
+    `positions`: the rows' positions when the tensors are a slice of rows (dw is then None)."""
     d = g.shape[-1]
     g64, h64 = P.upcast(g).astype(np.float64), P.upcast(h).astype(np.float64)
     r = P.upcast(inv).astype(np.float64)
     w64 = np.ones(d) if w is None else P.upcast(w).astype(np.float64).reshape(-1)
-    gn = ora.apply_rotary_emb(g64, base, inverse=True)
+    gn = ora.apply_rotary_emb(g64, base, inverse=True, positions=positions)
     tdx, tdw = ora.rmsnorm_module_backward(gn, h64, None if w is None else w64, r)
     xhat = h64 * r
     dg = _rope_grad_bound(g64, base) + g_round * np.abs(gn)
@@ -168,6 +170,8 @@ def _check_rope_backward(dx, dw, g, h, w, inv, base, what, g_round=0.0):
     err = np.abs(P.upcast(dx).astype(np.float64) - tdx)
     tol = ddx + P.DX_FLOOR * scale + half_ulp * np.abs(tdx) + 1e-6 * scale + SUBNORMAL_HALF[dx.dtype]
     assert np.all(err <= tol), f"{what}: dx over its bound by {float((err - tol).max()):.3e}"
+    if positions is not None:
+        return
     if w is not None:
         ddw = np.sum((np.abs(xhat) * dg).reshape(-1, d), axis=0)
         got = dw.detach().cpu().numpy().astype(np.float64)
@@ -202,6 +206,28 @@ def test_fused_backward_matches_the_oracle_composition(dtype, shape, with_w, bas
     dx2, dw2 = vk.fused_rmsnorm_residual_backward(g_back, h, w, inv, saved_is_h=True)
     g_round = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}[dtype]
     _check_rope_backward(dx2, dw2, g, h, w, inv, base, f"two-pass {dtype} {shape}", g_round)
+
+
+def test_fused_backward_long_fp32_walk():
+    """fp32, one sequence of 131072 positions at dim 4096: one 1024-thread row group per
+    workgroup, so each of the 256 slots walks 512 rows of one sequence with no position wrap.
+    The rotation state is re-evaluated every 16 rows, so the last rows of the walks (and the
+    middle ones) keep the same 2^-18 recurrence bound as short walks."""
+    seq, d, base = 131072, 4096, 500000.0
+    print(f"rmsnorm_rope backward fp32 long walk: seq={seq} dim={d}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(1, seq, d, device="cuda", generator=gen)
+    g = torch.randn(1, seq, d, device="cuda", generator=gen)
+    w = 1.0 + 0.1 * torch.randn(d, device="cuda", generator=gen)
+    _, h, inv = vk.rmsnorm_rope_forward(x, w, 1e-6, base)
+    dx, _ = vk.rmsnorm_rope_backward(g, h, w, inv, base)
+    torch.cuda.synchronize()
+    del x
+    for lo, hi in ((0, 256), (seq // 2 - 256, seq // 2 + 256), (seq - 512, seq)):
+        sl = slice(lo, hi)
+        _check_rope_backward(dx[:, sl], None, g[:, sl], h[:, sl], w, inv[:, sl], base,
+                             f"fp32 long walk rows {lo}..{hi}",
+                             positions=np.arange(lo, hi))
 
 
 def test_fused_backward_is_deterministic():

@@ -128,7 +128,18 @@ struct BwdPlan {
   RowPlan rp;
   int64_t wgs;       // workgroups = dweight partial rows
   size_t lds_bytes;  // dynamic LDS of the group combine
+  bool ring = false; // the ring-pipelined kernel (plan_bwd_ring) instead of bwd_vec_kernel
 };
+
+// The ring-pipelined backward (bwd_ring_kernel): a ring of kRingPrefetch + 1 row buffers per
+// thread, so two rows are in flight while one reduces, in a branch-free steady loop.  It takes
+// whole rows only (dim == nv * tpr * V: every lane busy, no chunk guards), at most two chunks per
+// thread, and workgroups of at most kRingBlock threads (its launch bound: 256 VGPRs a lane for
+// the three row buffers), one per CU, so each row slot walks twice as many rows as in the
+// 1024-thread persistent kernel.  Measured on MI355X at 16384 x 4096 bf16: 69.2 us against 72.4.
+constexpr int kRingBlock = 512;
+constexpr int kRingMaxNV = 2;
+constexpr int kRingPrefetch = 2;
 
 inline BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
                         int prefer_nv, int max_block, int waves_per_cu,
@@ -151,6 +162,35 @@ inline BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned,
   if (wgs < 1) wgs = 1;
   b.wgs = wgs;
   b.lds_bytes = (p.vec && p.groups > 1) ? (size_t)dim * sizeof(float) : 0;
+  return b;
+}
+
+// Whether a row plan suits the ring-pipelined backward (see kRingBlock).
+inline bool ring_eligible(const RowPlan& p, int64_t dim, int elem_bytes) {
+  if (!p.vec || (elem_bytes != 2 && elem_bytes != 4)) return false;
+  return p.nv >= 1 && p.nv <= kRingMaxNV && p.tpr <= kRingBlock &&
+         (int64_t)p.nv * p.tpr * (16 / elem_bytes) == dim;
+}
+
+// Plan of the ring-pipelined backward: row groups packed into workgroups of up to kRingBlock
+// threads, one workgroup per CU.  `ring` is false (and the plan unusable) when the row layout
+// does not suit it; the caller then plans bwd_vec_kernel.
+inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
+                             int prefer_nv) {
+  BwdPlan b;
+  b.rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrder);
+  b.wgs = 0;
+  b.lds_bytes = 0;
+  b.ring = ring_eligible(b.rp, dim, elem_bytes);
+  if (!b.ring) return b;
+  RowPlan& p = b.rp;
+  p.groups = kRingBlock / p.tpr;
+  p.block = p.tpr * p.groups;
+  const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
+  int64_t wgs = cus > 0 ? cus : 1;
+  if (wgs > wgs_needed) wgs = wgs_needed;
+  b.wgs = wgs;
+  b.lds_bytes = p.groups > 1 ? (size_t)dim * sizeof(float) : 0;
   return b;
 }
 
@@ -186,6 +226,8 @@ inline size_t bwd_workspace_bytes(int64_t rows, int64_t dim, int cus, int prefer
       const int64_t nr = plan_bwd_rope(rows, dim, sizes[si], al != 0, cus, prefer_nv, max_block,
                                        waves_per_cu).wgs;
       if (nr > most) most = nr;
+      const BwdPlan rg = plan_bwd_ring(rows, dim, sizes[si], al != 0, cus, prefer_nv);
+      if (rg.ring && rg.wgs > most) most = rg.wgs;
     }
   }
   return (size_t)most * (size_t)dim * sizeof(float);

@@ -18,6 +18,9 @@
 //                       row's loads in flight while the current row reduces; the weight chunk and
 //                       the fp32 dweight column accumulators stay in registers for the whole walk;
 //                       each slot finally writes one fp32 partial row (no atomics).
+//   bwd_ring_kernel     the same walk for whole rows with a ring of three row buffers (two rows
+//                       in flight while one reduces) in a branch-free steady loop, 512-thread
+//                       workgroups, one per CU: the backward's default where the rows suit it.
 //   dweight_reduce      stage 2: sums the partial rows in a fixed order -> dweight[dim].
 //   *_generic_kernel    any dim and any alignment: the same arithmetic with scalar accesses.
 // Row sums: DPP inside each 16-lane row of the wave, readlane across the four rows, LDS only
@@ -680,6 +683,8 @@ constexpr int kGradH = 2;
 // F.apply_rotary_emb(attention_norm(x)), models/llama.py:48-49), rotated back in registers
 // before use: the backward of the rotation (functional.py:316-345) fused into the norm's.
 constexpr int kRopeG = 4;
+// Rows of the RoPE-gradient walk between direct evaluations of the rotation state.
+constexpr int kRopeAnchor = 16;
 
 template <int DT, int WDT, int NV, int FLAGS>
 __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(NV)
@@ -708,10 +713,11 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
   const bool has_dres = a.dres != nullptr;
 
   // RoPE: each thread holds (cos, sin) of its pairs at the current row's position and advances
-  // them by the rotation through nslots positions (the walk's row step) from the LDS table; where
-  // the position wraps to a new outer index they are evaluated directly.  Float32 state: each
-  // step adds about an ulp, far below the output rounding of bf16/fp16 and inside the fp32 dx
-  // tolerance for the walks' lengths.
+  // them by the rotation through nslots positions (the walk's row step) from the LDS table; they
+  // are evaluated directly where the position wraps to a new outer index and on every
+  // kRopeAnchor-th row of the walk.  Float32 state: each step adds about an ulp, so re-anchoring
+  // keeps the drift under kRopeAnchor ulps however long the walk (the sequence length over the
+  // slot count), far below the output rounding of bf16/fp16 and the fp32 dx tolerance.
   float rc[NR][P], rs[NR][P];
   if constexpr (ROPE) {
     for (int q = threadIdx.x; q < a.dim / 2; q += blockDim.x) {
@@ -871,11 +877,13 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
 
     if constexpr (ROPE) {
       pos += nslots;
-      if (pos < a.rope_seq) {
-        rope_step();
-      } else {
+      if (pos >= a.rope_seq) {
         pos = nrow % a.rope_seq;
         rope_start(pos);
+      } else if ((it + 1) % kRopeAnchor == 0) {
+        rope_start(pos);
+      } else {
+        rope_step();
       }
     }
     row = nrow;
@@ -917,6 +925,180 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
           for (int i = 0; i < V; ++i)
             comb[c * V + i] = (gi == 0) ? acc[k][i] : comb[c * V + i] + acc[k][i];
         }
+      }
+    }
+    __syncthreads();
+  }
+  for (int q = threadIdx.x; q < a.dim / 4; q += blockDim.x)
+    store16<VELOGRAD_DTYPE_F32>(prow, 4 * (int64_t)q, *reinterpret_cast<const u32x4*>(comb + 4 * q));
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward, whole rows, ring-pipelined (launch_plan.h: plan_bwd_ring).  Each row slot walks rows
+// slot, slot + S, ... as in bwd_vec_kernel, but keeps a ring of PF + 1 = 3 row buffers (2 with
+// grad_h): while a row reduces, the next two rows' loads are in flight.  Rows are whole (dim == NV * tpr * V),
+// and the steady loop covers only iterations in which every slot has a row, loading prefetch
+// rows past the end from the last row instead (never used), so it is free of branches around
+// memory operations: the wait for a row's data then counts exactly the later loads and stores
+// instead of draining them, which a guarded loop forces.  The loop is unrolled by the ring
+// length so the buffers are indexed at compile time.  kRingDres: dres is written too.
+// ------------------------------------------------------------------------------------------
+constexpr int kRingDres = 8;
+
+template <int DT, int WDT, int NV, int FLAGS>
+__global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const BwdArgs a) {
+  using C = Codec<DT>;
+  constexpr int V = C::kVec;
+  constexpr bool SAVED_IS_H = (FLAGS & kSavedIsH) != 0;
+  constexpr bool HAS_GH = (FLAGS & kGradH) != 0;
+  constexpr bool HAS_DRES = (FLAGS & kRingDres) != 0;
+  constexpr int NH = HAS_GH ? NV : 1;  // grad_h chunks (a dummy slot when absent)
+  // With grad_h a third stream fills the ring: one row ahead keeps it within 256 VGPRs.
+  constexpr int PF = HAS_GH ? 1 : vg_plan::kRingPrefetch;
+  constexpr int R = PF + 1;
+  static_assert((FLAGS & kRopeG) == 0, "the RoPE gradient runs in bwd_vec_kernel");
+  __shared__ float red[2][kMaxWavesPerRow];
+  extern __shared__ __align__(16) float dyn_lds[];  // dim floats: the row groups' combine
+
+  const int tpr = a.tpr;
+  const int grp = threadIdx.x / tpr;
+  const int lt = threadIdx.x - grp * tpr;
+  const int groups = blockDim.x / tpr;
+  const int64_t slot = (int64_t)blockIdx.x * groups + grp;
+  const int64_t nslots = (int64_t)gridDim.x * groups;
+  const bool has_w = a.w != nullptr;
+  const int64_t last = a.rows - 1;
+
+  WeightChunk<DT, WDT> wc[NV];
+  float acc[NV][V];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    wc[k].load(has_w ? a.w : nullptr, (int64_t)(lt + k * tpr) * V);
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[k][i] = 0.0f;
+  }
+
+  u32x4 gr[R][NV], sr[R][NV], hr[R][NH];
+  float rr[R];
+  // Row `row`'s g, saved, grad_h chunks and inv_rms; rows past the end read the last row.
+  auto load_row = [&](int64_t row, u32x4* gv, u32x4* sv, u32x4* hv, float& r) {
+    const int64_t rw = row < a.rows ? row : last;
+    r = a.inv_rms[rw];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int64_t col = (int64_t)(lt + k * tpr) * V;
+      gv[k] = load16_stream<DT>(a.g, rw * a.ld_g + col);
+      sv[k] = load16_stream<DT>(a.saved, rw * a.ld_s + col);
+      if constexpr (HAS_GH) hv[k] = load16_stream<DT>(a.gh, rw * a.ld_gh + col);
+    }
+  };
+  auto decode = [&](const u32x4* gv, const u32x4* sv, float r, int k, float* gf, float* xh,
+                    float* wf) {
+    C::unpack(gv[k], gf);
+    C::unpack(sv[k], xh);
+    if constexpr (SAVED_IS_H) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) xh[i] = xh[i] * r;
+    }
+    wc[k].unpack(has_w, wf);
+  };
+  // The backward of one row (as bwd_vec_kernel's loop body); `ok` = the row exists.
+  auto process = [&](u32x4* gv, u32x4* sv, const u32x4* hv, float r, int64_t row, bool ok,
+                     int it) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      float gf[V], xh[V], wf[V];
+      decode(gv, sv, r, k, gf, xh, wf);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float gw = gf[i] * wf[i];
+        s += gw * xh[i];
+      }
+    }
+    s = row_sum(s, tpr, grp, red[it & 1]);
+    const float m = s / (float)a.dim;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      forget(gv[k]);
+      forget(sv[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int64_t col = (int64_t)(lt + k * tpr) * V;
+      float gf[V], xh[V], wf[V];
+      decode(gv, sv, r, k, gf, xh, wf);
+      float d[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float gw = gf[i] * wf[i];
+        d[i] = r * (gw - xh[i] * m);
+      }
+      if constexpr (HAS_GH) {
+        float ghf[V];
+        C::unpack(hv[k], ghf);
+#pragma unroll
+        for (int i = 0; i < V; ++i) d[i] = d[i] + ghf[i];
+      }
+      const u32x4 pv = C::pack(d);
+      if (ok) {
+        store16_stream<DT>(a.dx, row * a.ld_dx + col, pv);
+        if constexpr (HAS_DRES) store16_stream<DT>(a.dres, row * a.ld_dres + col, pv);
+      }
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[k][i] += ok ? gf[i] * xh[i] : 0.0f;
+    }
+  };
+
+  // Row j of the walk sits in buffer j % R; processing row j first issues row j + PF's loads
+  // into buffer (j + PF) % R, the one row j - 1 has just released.
+  const int full = (int)(a.rows / nslots);  // iterations in which every slot has a row
+#pragma unroll
+  for (int j = 0; j < PF; ++j) load_row(slot + (int64_t)j * nslots, gr[j], sr[j], hr[j], rr[j]);
+  int it = 0;
+  for (; it + R <= full; it += R) {
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const int nb = (u + PF) % R;
+      load_row(slot + (int64_t)(it + u + PF) * nslots, gr[nb], sr[nb], hr[nb], rr[nb]);
+      process(gr[u], sr[u], hr[u], rr[u], slot + (int64_t)(it + u) * nslots, true, it + u);
+    }
+  }
+  // The last (up to R) iterations, some of whose slots may have no row.
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    if (it + u < a.iters) {
+      const int nb = (u + PF) % R;
+      if (it + u + PF < a.iters)
+        load_row(slot + (int64_t)(it + u + PF) * nslots, gr[nb], sr[nb], hr[nb], rr[nb]);
+      const int64_t row = slot + (int64_t)(it + u) * nslots;
+      process(gr[u], sr[u], hr[u], rr[u], row, row < a.rows, it + u);
+    }
+  }
+
+  if (a.partial == nullptr) return;
+  // One fp32 partial row per workgroup; row groups added in group order through LDS.
+  float* prow = a.partial + (int64_t)blockIdx.x * a.dim;
+  if (groups == 1) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = lt + k * tpr;
+#pragma unroll
+      for (int q = 0; q < V / 4; ++q)
+        store16<VELOGRAD_DTYPE_F32>(prow, (int64_t)c * V + 4 * q,
+                                    Codec<VELOGRAD_DTYPE_F32>::pack(&acc[k][4 * q]));
+    }
+    return;
+  }
+  float* comb = dyn_lds;
+  for (int gi = 0; gi < groups; ++gi) {
+    if (grp == gi) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int c = lt + k * tpr;
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          comb[c * V + i] = (gi == 0) ? acc[k][i] : comb[c * V + i] + acc[k][i];
       }
     }
     __syncthreads();
@@ -1033,6 +1215,7 @@ struct Tuning {
   int bwd_nv;             // same, backward
   int bwd_waves_per_cu;   // resident waves per CU targeted by the persistent backward grid
   int bwd_block;          // upper bound on backward workgroup size (row groups per workgroup)
+  int bwd_ring;           // 1: the ring-pipelined backward where the rows suit it
 };
 
 const Tuning& tuning() {
@@ -1041,6 +1224,7 @@ const Tuning& tuning() {
       env_int("VELOGRAD_BWD_NV", 0, 0, kMaxNV),
       env_int("VELOGRAD_BWD_WAVES_PER_CU", 16, 1, 64),
       env_int("VELOGRAD_BWD_BLOCK", 1024, 64, 1024),
+      env_int("VELOGRAD_BWD_RING", 1, 0, 1),
   };
   return t;
 }
@@ -1053,6 +1237,10 @@ RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned, bool one_stream) {
 
 BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus, bool rope) {
   const Tuning& t = tuning();
+  if (!rope && t.bwd_ring) {
+    const BwdPlan r = vg_plan::plan_bwd_ring(rows, dim, elem_bytes, aligned, cus, t.bwd_nv);
+    if (r.ring) return r;
+  }
   if (rope)
     return vg_plan::plan_bwd_rope(rows, dim, elem_bytes, aligned, cus, t.bwd_nv, t.bwd_block,
                                   t.bwd_waves_per_cu);
@@ -1097,6 +1285,15 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
 }
 
 template <int DT, int WDT, int F>
+void launch_bwd_ring(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
+  const dim3 grid((uint32_t)b.wgs), block(b.rp.block);
+  if (b.rp.nv == 1)
+    hipLaunchKernelGGL((bwd_ring_kernel<DT, WDT, 1, F>), grid, block, b.lds_bytes, st, a);
+  else
+    hipLaunchKernelGGL((bwd_ring_kernel<DT, WDT, 2, F>), grid, block, b.lds_bytes, st, a);
+}
+
+template <int DT, int WDT, int F>
 void launch_bwd_flags(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
   const RowPlan& p = b.rp;
   const dim3 grid((uint32_t)b.wgs);
@@ -1105,6 +1302,15 @@ void launch_bwd_flags(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
   if (!p.vec) {
     hipLaunchKernelGGL((bwd_generic_kernel<DT, WDT, F>), grid, block, 0, st, a);
     return;
+  }
+  if constexpr ((F & kRopeG) == 0) {
+    if (b.ring) {
+      if (a.dres != nullptr)
+        launch_bwd_ring<DT, WDT, F | kRingDres>(a, b, st);
+      else
+        launch_bwd_ring<DT, WDT, F>(a, b, st);
+      return;
+    }
   }
   if constexpr ((F & kRopeG) != 0) {
     // NV 4 is never planned with the RoPE gradient (max_block_for_nv_rope); it is not compiled
@@ -1379,6 +1585,8 @@ int32_t run_bwd(const void* grad_y, const void* saved, int32_t saved_is_h, const
   if (rope && plan.rp.vec) plan.lds_bytes = (size_t)dim * sizeof(float);
   if (!vg_plan::row_plan_valid(plan.rp, dim, eb) || plan.wgs < 1 || plan.wgs > INT32_MAX ||
       plan.lds_bytes > 64 * 1024 ||
+      (plan.ring && (!vg_plan::ring_eligible(plan.rp, dim, eb) ||
+                     plan.rp.block > vg_plan::kRingBlock)) ||
       (rope && plan.rp.vec && plan.rp.block > vg_plan::max_block_for_nv_rope(plan.rp.nv)))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: internal launch plan rejected (dim=%lld)",
                 (long long)dim);
