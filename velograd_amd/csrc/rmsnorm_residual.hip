@@ -455,10 +455,18 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 // VALU-bound, no faster than two passes.  The walk's first angle is the double pos * freq_j
 // reduced exactly before a float sincospi (a few float32 ulps); where the position wraps to 0 (a
 // new outer index) the rotation restarts at the identity; the recurrence adds ~1e-16 per step.
+// A whole block of whole rows (the usual case) runs as straight-line code over its rows with a
+// ring of three row buffers, two rows' loads in flight while one reduces, and no branch around
+// a global memory operation (the residual and h are compile-time flags RF; the block's inv_rms
+// values wait in LDS and are stored after the walk), so each row waits for its own loads only
+// instead of draining every load and store at each row.  The last, partial block walks with
+// guards.
 // ------------------------------------------------------------------------------------------
 constexpr int kNormRopeRows = 16;
+constexpr int kRopeRes = 1;    // RF: a residual is added
+constexpr int kRopeWriteH = 2; // RF: h is stored
 
-template <int DT, int WDT, int NV>
+template <int DT, int WDT, int NV, int RF>
 __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_rope_kernel(const FwdArgs a) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
@@ -467,9 +475,9 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_rope_kernel(const Fw
   const int tpr = blockDim.x;  // one row group per workgroup
   const int lt = threadIdx.x;
   const int nchunk = a.dim / V;
-  const bool has_res = a.res != nullptr;
+  constexpr bool has_res = (RF & kRopeRes) != 0;
   const bool has_w = a.w != nullptr;
-  const bool write_h = has_res && a.h != nullptr;
+  constexpr bool write_h = has_res && (RF & kRopeWriteH) != 0;
   const int64_t row0 = (int64_t)blockIdx.x * kNormRopeRows;
   const int nrows = (int)((a.rows - row0) < kNormRopeRows ? (a.rows - row0) : kNormRopeRows);
 
@@ -516,6 +524,81 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_rope_kernel(const Fw
       sincospif(2.0f * (float)(rev - rint(rev)), &sf, &cf);
       cr[k][q] = cf;
       sr[k][q] = sf;
+    }
+  }
+
+  if constexpr (NV == 1) {
+    if (nrows == kNormRopeRows && nchunk == tpr) {
+      __shared__ float inv_lds[kNormRopeRows];
+      constexpr int RB = 3;
+      const int64_t col = (int64_t)lt * V;
+      u32x4 xb[RB], rb[RB];
+      xb[0] = xv[0];
+      rb[0] = rv[0];
+      xb[1] = load16_stream<DT>(a.x, (row0 + 1) * a.ld_x + col);
+      if constexpr (has_res) rb[1] = load16_stream<DT>(a.res, (row0 + 1) * a.ld_res + col);
+      int64_t pos = row0 % a.rope_seq;
+#pragma unroll
+      for (int it = 0; it < kNormRopeRows; ++it) {
+        const int b = it % RB;
+        const int64_t row = row0 + it;
+        if (it + 2 < kNormRopeRows) {
+          const int nb = (it + 2) % RB;
+          xb[nb] = load16_stream<DT>(a.x, (row + 2) * a.ld_x + col);
+          if constexpr (has_res) rb[nb] = load16_stream<DT>(a.res, (row + 2) * a.ld_res + col);
+        }
+        if (it > 0 && pos == 0) {
+          // a new outer index: position 0, the identity rotation
+#pragma unroll
+          for (int q = 0; q < PP; ++q) {
+            cr[0][q] = 1.0;
+            sr[0][q] = 0.0;
+          }
+        }
+        auto make_h = [&](float* hf) {
+          C::unpack(xb[b], hf);
+          if constexpr (has_res) {
+            float rf[V];
+            C::unpack(rb[b], rf);
+#pragma unroll
+            for (int i = 0; i < V; ++i) hf[i] = hf[i] + rf[i];
+          }
+        };
+        float ss = 0.0f;
+        {
+          float hf[V];
+          make_h(hf);
+#pragma unroll
+          for (int i = 0; i < V; ++i) ss += hf[i] * hf[i];
+          if constexpr (write_h) store16_stream<DT>(a.h, row * a.ld_h + col, C::pack(hf));
+        }
+        ss = row_sum(ss, tpr, 0, red[it & 1]);
+        const float mean_sq = floor_mean_sq(ss / (float)a.dim, a.ms_floor);
+        const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
+        if (lt == 0) inv_lds[it] = r;
+        forget(xb[b]);
+        if constexpr (has_res) forget(rb[b]);
+        float hf[V], wf[V], yf[V];
+        make_h(hf);
+        wc[0].unpack(has_w, wf);
+#pragma unroll
+        for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
+#pragma unroll
+        for (int q = 0; q < PP; ++q) {
+          const float cv = (float)cr[0][q], sv = (float)sr[0][q];
+          const float y0 = yf[2 * q], y1 = yf[2 * q + 1];
+          yf[2 * q] = y0 * cv - y1 * sv;                                  // functional.py:313
+          yf[2 * q + 1] = y0 * sv + y1 * cv;                              // functional.py:314
+          const double cn = cr[0][q] * cst[0][q] - sr[0][q] * sst[0][q];
+          sr[0][q] = sr[0][q] * cst[0][q] + cr[0][q] * sst[0][q];
+          cr[0][q] = cn;
+        }
+        store16_stream<DT>(a.y, row * a.ld_y + col, C::pack(yf));
+        pos = (pos + 1 == a.rope_seq) ? 0 : pos + 1;
+      }
+      // thread 0 wrote inv_lds; threads 1..15 of its wave read it in program order
+      if (lt < kNormRopeRows && a.inv_rms != nullptr) a.inv_rms[row0 + lt] = inv_lds[lt];
+      return;
     }
   }
 
@@ -1269,9 +1352,14 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
                          dim3(kGenericBlock), 0, st, a);
       return;
     }
-    hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, 1>),
-                       dim3((uint32_t)((a.rows + kNormRopeRows - 1) / kNormRopeRows)),
-                       dim3(p.tpr), 0, st, a);
+    const dim3 grid((uint32_t)((a.rows + kNormRopeRows - 1) / kNormRopeRows)), block(p.tpr);
+    if (a.res == nullptr)
+      hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, 1, 0>), grid, block, 0, st, a);
+    else if (a.h == nullptr)
+      hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, 1, kRopeRes>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, 1, kRopeRes | kRopeWriteH>), grid, block, 0,
+                         st, a);
   } else {
     const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups));
     const dim3 block(p.block);
