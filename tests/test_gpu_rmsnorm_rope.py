@@ -270,6 +270,56 @@ def test_fused_forward_is_bitwise_repeatable_on_any_stream():
             assert torch.equal(got[1], want[1]), "h"
 
 
+def test_every_output_row_is_written_on_every_call():
+    """Each forward writes every row of y and inv_rms on every call: outputs NaN-filled before
+    each of 8 calls (4 on the current stream, 4 on a side stream) at the headline shape, for the
+    fused norm + RoPE (one 64-byte inv_rms block per workgroup) and the plain forward (one float
+    per workgroup), each call equal to the first bit for bit."""
+    from velograd_amd import _lib
+    lib = _lib.load()
+    rows, d = 16384, 4096
+    rng = np.random.default_rng(5)
+    x = P.to_device(P.gaussian(rng, (rows, d)), torch.bfloat16)
+    r = P.to_device(P.gaussian(rng, (rows, d)), torch.bfloat16)
+    w = P.to_device(P.weight_vec(rng, d), torch.bfloat16)
+    y = torch.empty_like(x)
+    h = torch.empty_like(x)
+    inv = torch.empty(rows, device="cuda")
+    bf = _lib.DTYPE_BF16
+    side = torch.cuda.Stream()
+
+    def rope(res, sp):
+        return lib.velograd_rmsnorm_rope_fwd(
+            x.data_ptr(), r.data_ptr() if res else None, w.data_ptr(), y.data_ptr(),
+            h.data_ptr() if res else None, inv.data_ptr(), rows, d, d, d, d, d, 2048, bf, bf,
+            1e-5, 1e-12, 10000.0, sp)
+
+    def plain(res, sp):
+        return lib.velograd_rmsnorm_residual_fwd(
+            x.data_ptr(), r.data_ptr() if res else None, w.data_ptr(), y.data_ptr(),
+            h.data_ptr() if res else None, inv.data_ptr(), rows, d, d, d, d, d, bf, bf, 1e-5, sp)
+
+    for name, fn in (("rmsnorm_rope_fwd", rope), ("rmsnorm_residual_fwd", plain)):
+        for res in (False, True):
+            first = None
+            for call in range(8):
+                stream = side if call % 2 else torch.cuda.current_stream()
+                stream.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(stream):
+                    y.fill_(float("nan"))
+                    inv.fill_(float("nan"))
+                    _lib.check(fn(res, stream.cuda_stream), name)
+                torch.cuda.current_stream().wait_stream(stream)
+                torch.cuda.synchronize()
+                what = f"{name} res={res} call {call}"
+                assert not bool(inv.isnan().any()), f"{what}: inv_rms rows left unwritten"
+                assert not bool(y.isnan().any()), f"{what}: y rows left unwritten"
+                if first is None:
+                    first = (y.clone(), inv.clone())
+                else:
+                    assert torch.equal(y, first[0]) and torch.equal(inv, first[1]), what
+
+
 def test_backward_errors():
     g = torch.zeros(2, 4, 8, device="cuda")
     inv = torch.ones(2, 4, 1, device="cuda")

@@ -447,14 +447,18 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 }
 
 // ------------------------------------------------------------------------------------------
-// Forward with the model's RoPE on y (kOutRopeI), register-resident rows: a workgroup of one row
-// group walks kNormRopeRows consecutive rows, the next row's chunks in flight while the current
-// one reduces.  Each thread keeps the rotation (cos, sin) of its pairs in double and advances
-// it by one position per row (the rotation through freq_j, from a double sincos of freq_j), so
+// Forward with the model's RoPE on y (kOutRopeI), one 16-byte chunk per thread: a workgroup of
+// one row group walks kNormRopeRows consecutive rows, the next rows' chunks in flight while the
+// current one reduces.  Each thread keeps the rotation (cos, sin) of its pairs in double and
+// advances it by one position per row (the rotation through freq_j, from a sincos of freq_j), so
 // trigonometry runs only before the walk; evaluated per (row, pair) it made the fused pass
 // VALU-bound, no faster than two passes.  The walk's first angle is the double pos * freq_j
 // reduced exactly before a float sincospi (a few float32 ulps); where the position wraps to 0 (a
 // new outer index) the rotation restarts at the identity; the recurrence adds ~1e-16 per step.
+// The pass is bound by its vector instructions as much as by HBM, so each row's arithmetic is
+// kept short: the weight is decoded once per walk, h stays in registers across the reduction,
+// sums of products and the rotation use fused multiply-adds, and for a power-of-two dim the mean
+// is sum * (1 / dim), exact, instead of a division.
 // A whole block of whole rows (the usual case) runs as straight-line code over its rows with a
 // ring of three row buffers, two rows' loads in flight while one reduces, and no branch around
 // a global memory operation (the residual and h are compile-time flags RF; the block's inv_rms
@@ -463,215 +467,163 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 // guards.
 // ------------------------------------------------------------------------------------------
 constexpr int kNormRopeRows = 16;
-constexpr int kRopeRes = 1;    // RF: a residual is added
-constexpr int kRopeWriteH = 2; // RF: h is stored
+constexpr int kRopeRes = 1;     // RF: a residual is added
+constexpr int kRopeWriteH = 2;  // RF: h is stored
+constexpr int kRopeDimPow2 = 4; // RF: dim is a power of two
 
-template <int DT, int WDT, int NV, int RF>
-__global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_rope_kernel(const FwdArgs a) {
+template <int DT, int WDT, int RF>
+__global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const FwdArgs a) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
   constexpr int PP = V / 2;  // pairs per chunk
   __shared__ float red[2][kMaxWavesPerRow];
-  const int tpr = blockDim.x;  // one row group per workgroup
+  const int tpr = blockDim.x;  // one row group per workgroup, one chunk per thread
   const int lt = threadIdx.x;
   const int nchunk = a.dim / V;
+  const bool lane_ok = lt < nchunk;
   constexpr bool has_res = (RF & kRopeRes) != 0;
-  const bool has_w = a.w != nullptr;
   constexpr bool write_h = has_res && (RF & kRopeWriteH) != 0;
+  const bool has_w = a.w != nullptr;
   const int64_t row0 = (int64_t)blockIdx.x * kNormRopeRows;
   const int nrows = (int)((a.rows - row0) < kNormRopeRows ? (a.rows - row0) : kNormRopeRows);
+  const int64_t col = (int64_t)lt * V;
+  // 1 / dim is exact for a power of two, so sum * (1 / dim) has the bits of sum / dim
+  const float inv_dim = (RF & kRopeDimPow2) ? 1.0f / (float)a.dim : 0.0f;
 
-  WeightChunk<DT, WDT> wc[NV];
-  double cr[NV][PP], sr[NV][PP], cst[NV][PP], sst[NV][PP];
-  auto load_row = [&](int64_t row, u32x4* xv, u32x4* rv) {
+  u32x4 xv = u32x4{0u, 0u, 0u, 0u}, rv = u32x4{0u, 0u, 0u, 0u};
+  if (lane_ok) {
+    xv = load16_stream<DT>(a.x, row0 * a.ld_x + col);
+    if constexpr (has_res) rv = load16_stream<DT>(a.res, row0 * a.ld_res + col);
+  }
+  float wf[V];
+  {
+    WeightChunk<DT, WDT> wc;
+    wc.load((has_w && lane_ok) ? a.w : nullptr, col);
+    wc.unpack(has_w, wf);
+  }
+  double cr[PP], sr[PP], cst[PP], sst[PP];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int c = lt + k * tpr;
-      xv[k] = u32x4{0u, 0u, 0u, 0u};
-      rv[k] = u32x4{0u, 0u, 0u, 0u};
-      if (c < nchunk) {
-        xv[k] = load16_stream<DT>(a.x, row * a.ld_x + (int64_t)c * V);
-        if (has_res) rv[k] = load16_stream<DT>(a.res, row * a.ld_res + (int64_t)c * V);
-      }
+  for (int q = 0; q < PP; ++q) {
+    const double fd = rope_freq(lt * PP + q, a.rope_c_hi, a.rope_c_lo);
+    // the rotation through one position: double for fp32 outputs; for bf16/fp16 a float32
+    // sincos of the frequency (its error, about 1e-7 rad per step, stays far below their
+    // rounding over the walk's 16 steps) at a fraction of the cost
+    if constexpr (DT == VELOGRAD_DTYPE_F32) {
+      double sv, cv;
+      sincos(fd, &sv, &cv);
+      cst[q] = cv;
+      sst[q] = sv;
+    } else {
+      float sv, cv;
+      sincosf((float)fd, &sv, &cv);
+      cst[q] = cv;
+      sst[q] = sv;
     }
-  };
-  u32x4 xv[NV], rv[NV];
-  load_row(row0, xv, rv);
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int c = lt + k * tpr;
-    wc[k].load((has_w && c < nchunk) ? a.w : nullptr, (int64_t)c * V);
-#pragma unroll
-    for (int q = 0; q < PP; ++q) {
-      const double fd = rope_freq(c * PP + q, a.rope_c_hi, a.rope_c_lo);
-      // the rotation through one position: double for fp32 outputs; for bf16/fp16 a float32
-      // sincos of the frequency (its error, about 1e-7 rad per step, stays far below their
-      // rounding over the walk's 16 steps) at a fraction of the cost
-      if constexpr (DT == VELOGRAD_DTYPE_F32) {
-        double sv, cv;
-        sincos(fd, &sv, &cv);
-        cst[k][q] = cv;
-        sst[k][q] = sv;
-      } else {
-        float sv, cv;
-        sincosf((float)fd, &sv, &cv);
-        cst[k][q] = cv;
-        sst[k][q] = sv;
-      }
-      // the rotation at the walk's first position: double angle, reduced exactly, float sincospi
-      const double rev = (double)(row0 % a.rope_seq) * fd * kInv2PiD;
-      float sf, cf;
-      sincospif(2.0f * (float)(rev - rint(rev)), &sf, &cf);
-      cr[k][q] = cf;
-      sr[k][q] = sf;
-    }
+    // the rotation at the walk's first position: double angle, reduced exactly, float sincospi
+    const double rev = (double)(row0 % a.rope_seq) * fd * kInv2PiD;
+    float sf, cf;
+    sincospif(2.0f * (float)(rev - rint(rev)), &sf, &cf);
+    cr[q] = cf;
+    sr[q] = sf;
   }
 
-  if constexpr (NV == 1) {
-    if (nrows == kNormRopeRows && nchunk == tpr) {
-      __shared__ float inv_lds[kNormRopeRows];
-      constexpr int RB = 3;
-      const int64_t col = (int64_t)lt * V;
-      u32x4 xb[RB], rb[RB];
-      xb[0] = xv[0];
-      rb[0] = rv[0];
-      xb[1] = load16_stream<DT>(a.x, (row0 + 1) * a.ld_x + col);
-      if constexpr (has_res) rb[1] = load16_stream<DT>(a.res, (row0 + 1) * a.ld_res + col);
-      int64_t pos = row0 % a.rope_seq;
+  auto make_h = [&](const u32x4& xq, const u32x4& rq, float* hf) {
+    C::unpack(xq, hf);
+    if constexpr (has_res) {
+      float rf[V];
+      C::unpack(rq, rf);
 #pragma unroll
-      for (int it = 0; it < kNormRopeRows; ++it) {
-        const int b = it % RB;
-        const int64_t row = row0 + it;
-        if (it + 2 < kNormRopeRows) {
-          const int nb = (it + 2) % RB;
-          xb[nb] = load16_stream<DT>(a.x, (row + 2) * a.ld_x + col);
-          if constexpr (has_res) rb[nb] = load16_stream<DT>(a.res, (row + 2) * a.ld_res + col);
-        }
-        if (it > 0 && pos == 0) {
-          // a new outer index: position 0, the identity rotation
-#pragma unroll
-          for (int q = 0; q < PP; ++q) {
-            cr[0][q] = 1.0;
-            sr[0][q] = 0.0;
-          }
-        }
-        auto make_h = [&](float* hf) {
-          C::unpack(xb[b], hf);
-          if constexpr (has_res) {
-            float rf[V];
-            C::unpack(rb[b], rf);
-#pragma unroll
-            for (int i = 0; i < V; ++i) hf[i] = hf[i] + rf[i];
-          }
-        };
-        float ss = 0.0f;
-        {
-          float hf[V];
-          make_h(hf);
-#pragma unroll
-          for (int i = 0; i < V; ++i) ss += hf[i] * hf[i];
-          if constexpr (write_h) store16_stream<DT>(a.h, row * a.ld_h + col, C::pack(hf));
-        }
-        ss = row_sum(ss, tpr, 0, red[it & 1]);
-        const float mean_sq = floor_mean_sq(ss / (float)a.dim, a.ms_floor);
-        const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
-        if (lt == 0) inv_lds[it] = r;
-        forget(xb[b]);
-        if constexpr (has_res) forget(rb[b]);
-        float hf[V], wf[V], yf[V];
-        make_h(hf);
-        wc[0].unpack(has_w, wf);
-#pragma unroll
-        for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
-#pragma unroll
-        for (int q = 0; q < PP; ++q) {
-          const float cv = (float)cr[0][q], sv = (float)sr[0][q];
-          const float y0 = yf[2 * q], y1 = yf[2 * q + 1];
-          yf[2 * q] = y0 * cv - y1 * sv;                                  // functional.py:313
-          yf[2 * q + 1] = y0 * sv + y1 * cv;                              // functional.py:314
-          const double cn = cr[0][q] * cst[0][q] - sr[0][q] * sst[0][q];
-          sr[0][q] = sr[0][q] * cst[0][q] + cr[0][q] * sst[0][q];
-          cr[0][q] = cn;
-        }
-        store16_stream<DT>(a.y, row * a.ld_y + col, C::pack(yf));
-        pos = (pos + 1 == a.rope_seq) ? 0 : pos + 1;
-      }
-      // thread 0 wrote inv_lds; threads 1..15 of its wave read it in program order
-      if (lt < kNormRopeRows && a.inv_rms != nullptr) a.inv_rms[row0 + lt] = inv_lds[lt];
-      return;
+      for (int i = 0; i < V; ++i) hf[i] = hf[i] + rf[i];
     }
+  };
+  auto sum_sq = [&](const float* hf) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss = __builtin_fmaf(hf[i], hf[i], ss);
+    return ss;
+  };
+  auto inv_rms_of = [&](float ss) {
+    const float mean = (RF & kRopeDimPow2) ? ss * inv_dim : ss / (float)a.dim;
+    return 1.0f / __builtin_sqrtf(floor_mean_sq(mean, a.ms_floor) + a.eps);
+  };
+  // y = (h * r) * w turned by the current angles, then the angles advance one position
+  auto make_y = [&](const float* hf, float r, float* yf) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
+#pragma unroll
+    for (int q = 0; q < PP; ++q) {
+      const float cv = (float)cr[q], sv = (float)sr[q];
+      const float y0 = yf[2 * q], y1 = yf[2 * q + 1];
+      yf[2 * q] = __builtin_fmaf(y0, cv, -(y1 * sv));                    // functional.py:313
+      yf[2 * q + 1] = __builtin_fmaf(y0, sv, y1 * cv);                   // functional.py:314
+      const double cn = __builtin_fma(cr[q], cst[q], -(sr[q] * sst[q]));
+      sr[q] = __builtin_fma(sr[q], cst[q], cr[q] * sst[q]);
+      cr[q] = cn;
+    }
+  };
+  auto restart = [&]() {
+    // a new outer index: position 0, the identity rotation
+#pragma unroll
+    for (int q = 0; q < PP; ++q) {
+      cr[q] = 1.0;
+      sr[q] = 0.0;
+    }
+  };
+
+  if (nrows == kNormRopeRows && nchunk == tpr) {
+    __shared__ float inv_lds[kNormRopeRows];
+    constexpr int RB = 3;
+    u32x4 xb[RB], rb[RB];
+    xb[0] = xv;
+    rb[0] = rv;
+    xb[1] = load16_stream<DT>(a.x, (row0 + 1) * a.ld_x + col);
+    if constexpr (has_res) rb[1] = load16_stream<DT>(a.res, (row0 + 1) * a.ld_res + col);
+    int64_t pos = row0 % a.rope_seq;
+#pragma unroll
+    for (int it = 0; it < kNormRopeRows; ++it) {
+      const int b = it % RB;
+      const int64_t row = row0 + it;
+      if (it + 2 < kNormRopeRows) {
+        const int nb = (it + 2) % RB;
+        xb[nb] = load16_stream<DT>(a.x, (row + 2) * a.ld_x + col);
+        if constexpr (has_res) rb[nb] = load16_stream<DT>(a.res, (row + 2) * a.ld_res + col);
+      }
+      if (it > 0 && pos == 0) restart();
+      float hf[V];
+      make_h(xb[b], rb[b], hf);
+      if constexpr (write_h) store16_stream<DT>(a.h, row * a.ld_h + col, C::pack(hf));
+      const float r = inv_rms_of(row_sum(sum_sq(hf), tpr, 0, red[it & 1]));
+      if (lt == 0) inv_lds[it] = r;
+      float yf[V];
+      make_y(hf, r, yf);
+      store16_stream<DT>(a.y, row * a.ld_y + col, C::pack(yf));
+      pos = (pos + 1 == a.rope_seq) ? 0 : pos + 1;
+    }
+    // thread 0 wrote inv_lds; threads 1..15 of its wave read it in program order
+    if (lt < kNormRopeRows && a.inv_rms != nullptr) a.inv_rms[row0 + lt] = inv_lds[lt];
+    return;
   }
 
   // the position advances with the row and wraps at rope_seq (no division inside the walk)
   int64_t pos = row0 % a.rope_seq;
   for (int it = 0; it < nrows; ++it, pos = (pos + 1 == a.rope_seq) ? 0 : pos + 1) {
     const int64_t row = row0 + it;
-    if (it > 0 && pos == 0) {
-      // a new outer index: position 0, the identity rotation
-#pragma unroll
-      for (int k = 0; k < NV; ++k) {
-#pragma unroll
-        for (int q = 0; q < PP; ++q) {
-          cr[k][q] = 1.0;
-          sr[k][q] = 0.0;
-        }
-      }
+    if (it > 0 && pos == 0) restart();
+    u32x4 xn = u32x4{0u, 0u, 0u, 0u}, rn = u32x4{0u, 0u, 0u, 0u};
+    if (it + 1 < nrows && lane_ok) {
+      xn = load16_stream<DT>(a.x, (row + 1) * a.ld_x + col);
+      if constexpr (has_res) rn = load16_stream<DT>(a.res, (row + 1) * a.ld_res + col);
     }
-    u32x4 xn[NV], rn[NV];
-    if (it + 1 < nrows) load_row(row + 1, xn, rn);
-
-    auto make_h = [&](int k, float* hf) {
-      C::unpack(xv[k], hf);
-      if (has_res) {
-        float rf[V];
-        C::unpack(rv[k], rf);
-#pragma unroll
-        for (int i = 0; i < V; ++i) hf[i] = hf[i] + rf[i];
-      }
-    };
-    float ss = 0.0f;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      float hf[V];
-      make_h(k, hf);
-#pragma unroll
-      for (int i = 0; i < V; ++i) ss += hf[i] * hf[i];
-      const int c = lt + k * tpr;
-      if (write_h && c < nchunk)
-        store16_stream<DT>(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf));
-    }
-    ss = row_sum(ss, tpr, 0, red[it & 1]);
-    const float mean_sq = floor_mean_sq(ss / (float)a.dim, a.ms_floor);
-    const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
+    float hf[V];
+    make_h(xv, rv, hf);
+    if (write_h && lane_ok) store16_stream<DT>(a.h, row * a.ld_h + col, C::pack(hf));
+    const float r = inv_rms_of(row_sum(sum_sq(hf), tpr, 0, red[it & 1]));
     if (lt == 0 && a.inv_rms != nullptr) a.inv_rms[row] = r;
-
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int c = lt + k * tpr;
-      float hf[V], wf[V], yf[V];
-      make_h(k, hf);
-      wc[k].unpack(has_w, wf);
-#pragma unroll
-      for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
-#pragma unroll
-      for (int q = 0; q < PP; ++q) {
-        const float cv = (float)cr[k][q], sv = (float)sr[k][q];
-        const float y0 = yf[2 * q], y1 = yf[2 * q + 1];
-        yf[2 * q] = y0 * cv - y1 * sv;                                  // functional.py:313
-        yf[2 * q + 1] = y0 * sv + y1 * cv;                              // functional.py:314
-        const double cn = cr[k][q] * cst[k][q] - sr[k][q] * sst[k][q];
-        sr[k][q] = sr[k][q] * cst[k][q] + cr[k][q] * sst[k][q];
-        cr[k][q] = cn;
-      }
-      if (c < nchunk) store16_stream<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
-    }
-    if (it + 1 < nrows) {
-#pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        xv[k] = xn[k];
-        rv[k] = rn[k];
-      }
-    }
+    float yf[V];
+    make_y(hf, r, yf);
+    if (lane_ok) store16_stream<DT>(a.y, row * a.ld_y + col, C::pack(yf));
+    xv = xn;
+    rv = rn;
   }
 }
 
@@ -1353,13 +1305,19 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
       return;
     }
     const dim3 grid((uint32_t)((a.rows + kNormRopeRows - 1) / kNormRopeRows)), block(p.tpr);
-    if (a.res == nullptr)
-      hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, 1, 0>), grid, block, 0, st, a);
-    else if (a.h == nullptr)
-      hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, 1, kRopeRes>), grid, block, 0, st, a);
-    else
-      hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, 1, kRopeRes | kRopeWriteH>), grid, block, 0,
-                         st, a);
+    const int rf = (a.res == nullptr ? 0 : a.h == nullptr ? kRopeRes : kRopeRes | kRopeWriteH) |
+                   ((a.dim & (a.dim - 1)) == 0 ? kRopeDimPow2 : 0);
+    switch (rf) {
+#define VG_ROPE_FWD(F) \
+  case F: hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, F>), grid, block, 0, st, a); break;
+      VG_ROPE_FWD(0)
+      VG_ROPE_FWD(kRopeRes)
+      VG_ROPE_FWD(kRopeRes | kRopeWriteH)
+      VG_ROPE_FWD(kRopeDimPow2)
+      VG_ROPE_FWD(kRopeDimPow2 | kRopeRes)
+      default: VG_ROPE_FWD(kRopeDimPow2 | kRopeRes | kRopeWriteH)
+#undef VG_ROPE_FWD
+    }
   } else {
     const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups));
     const dim3 block(p.block);
