@@ -41,9 +41,12 @@ def _bound(n: np.ndarray, base: float) -> np.ndarray:
 CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 8192), False),
          (torch.float32, (3, 33, 1000), True), (torch.float16, (2, 50, 256), False),
          (torch.bfloat16, (3, 5, 6), True), (torch.float32, (4, 2, 3, 40), False),
-         # long persistent walks of the 16-bit kernel: 32 rows per slot without a position wrap,
-         # and with one every 4 rows
-         (torch.bfloat16, (1, 16384, 4096), False), (torch.float16, (8, 2048, 4096), True)]
+         # the 16-bit kernel's walks over rows b, b + G, ... (G = rows / 16 workgroups): no
+         # sequence end (G = 1024, seq 16384), returning to the walk's first position every 2 rows
+         # (seq 2048 a multiple of G) and on every row (G = 128 a multiple of seq 64), and angles
+         # evaluated afresh where a walk crosses a sequence end (G = 938, seq 3000)
+         (torch.bfloat16, (1, 16384, 4096), False), (torch.float16, (8, 2048, 4096), True),
+         (torch.bfloat16, (32, 64, 1024), True), (torch.bfloat16, (5, 3000, 4096), False)]
 
 
 @pytest.mark.parametrize("dtype,shape,with_res", CASES,

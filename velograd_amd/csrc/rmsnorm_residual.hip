@@ -27,6 +27,7 @@
 // across the waves that share a row; every order is fixed, so results are bitwise reproducible.
 
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "fp8_e4m3.h"
@@ -447,24 +448,29 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 }
 
 // ------------------------------------------------------------------------------------------
-// Forward with the model's RoPE on y (kOutRopeI), one 16-byte chunk per thread: a workgroup of
-// one row group walks kNormRopeRows consecutive rows, the next rows' chunks in flight while the
-// current one reduces.  Each thread keeps the rotation (cos, sin) of its pairs in double and
-// advances it by one position per row (the rotation through freq_j, from a sincos of freq_j), so
-// trigonometry runs only before the walk; evaluated per (row, pair) it made the fused pass
-// VALU-bound, no faster than two passes.  The walk's first angle is the double pos * freq_j
-// reduced exactly before a float sincospi (a few float32 ulps); where the position wraps to 0 (a
-// new outer index) the rotation restarts at the identity; the recurrence adds ~1e-16 per step.
+// Forward with the model's RoPE on y (kOutRopeI), one 16-byte chunk per thread.  Workgroup b of
+// G walks up to kNormRopeRows rows b, b + G, b + 2G, ...: at each step the resident workgroups
+// touch adjacent rows, one compact address front that HBM serves better than runs of
+// consecutive rows per workgroup (those spread the front over 16 rows per workgroup).  The next
+// rows' chunks are in flight while the current one reduces.  Each thread keeps the rotation
+// (cos, sin) of its pairs in double and advances it by G positions per step (the rotation
+// through G * freq_j, evaluated once per walk), so trigonometry runs only before the walk;
+// evaluated per (row, pair) it made the fused pass VALU-bound, no faster than two passes.  The
+// walk's first angle is the double pos * freq_j reduced exactly before a float sincospi (a few
+// float32 ulps), and so is the step's; the recurrence adds ~1e-16 per step.  Where a step crosses
+// the end of a sequence (row position = row % rope_seq) and G is a multiple or a divisor of
+// rope_seq, the position returns to the walk's first one and so does the rotation (kept); any
+// other crossing re-evaluates the angle at the new position.
 // The pass is bound by its vector instructions as much as by HBM, so each row's arithmetic is
 // kept short: the weight is decoded once per walk, h stays in registers across the reduction,
 // sums of products and the rotation use fused multiply-adds, and for a power-of-two dim the mean
 // is sum * (1 / dim), exact, instead of a division.
-// A whole block of whole rows (the usual case) runs as straight-line code over its rows with a
-// ring of three row buffers, two rows' loads in flight while one reduces, and no branch around
-// a global memory operation (the residual and h are compile-time flags RF; the block's inv_rms
-// values wait in LDS and are stored after the walk), so each row waits for its own loads only
-// instead of draining every load and store at each row.  The last, partial block walks with
-// guards.
+// A whole walk whose positions only advance or return to the start (the usual case) runs as
+// straight-line code over its rows with a ring of three row buffers, two rows' loads in flight
+// while one reduces, and no branch around a global memory operation (the residual and h are
+// compile-time flags RF; the walk's inv_rms values wait in LDS and are stored after it), so
+// each row waits for its own loads only instead of draining every load and store at each row.
+// Shorter walks and walks that re-evaluate angles take the guarded loop.
 // ------------------------------------------------------------------------------------------
 constexpr int kNormRopeRows = 16;
 constexpr int kRopeRes = 1;     // RF: a residual is added
@@ -484,9 +490,15 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
   constexpr bool has_res = (RF & kRopeRes) != 0;
   constexpr bool write_h = has_res && (RF & kRopeWriteH) != 0;
   const bool has_w = a.w != nullptr;
-  const int64_t row0 = (int64_t)blockIdx.x * kNormRopeRows;
-  const int nrows = (int)((a.rows - row0) < kNormRopeRows ? (a.rows - row0) : kNormRopeRows);
+  const int64_t G = gridDim.x;   // row step of the walk
+  const int64_t row0 = blockIdx.x;
+  const int64_t left = (a.rows - row0 + G - 1) / G;
+  const int nrows = (int)(left < kNormRopeRows ? left : kNormRopeRows);
   const int64_t col = (int64_t)lt * V;
+  const int64_t seq = a.rope_seq;
+  const int64_t pos0 = row0 % seq;
+  // the positions of the walk only advance by G or return to pos0
+  const bool back_to_start = (seq % G == 0) || (G % seq == 0);
   // 1 / dim is exact for a power of two, so sum * (1 / dim) has the bits of sum / dim
   const float inv_dim = (RF & kRopeDimPow2) ? 1.0f / (float)a.dim : 0.0f;
 
@@ -502,29 +514,29 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
     wc.unpack(has_w, wf);
   }
   double cr[PP], sr[PP], cst[PP], sst[PP];
+  float c0[PP], s0[PP];  // the rotation at pos0
+  // the rotation at pos: double angle, reduced exactly, float sincospi
+  auto rotation_at = [&](int64_t pos, int q, float& c, float& s) {
+    const double rev = (double)pos * rope_freq(lt * PP + q, a.rope_c_hi, a.rope_c_lo) * kInv2PiD;
+    sincospif(2.0f * (float)(rev - rint(rev)), &s, &c);
+  };
 #pragma unroll
   for (int q = 0; q < PP; ++q) {
-    const double fd = rope_freq(lt * PP + q, a.rope_c_hi, a.rope_c_lo);
-    // the rotation through one position: double for fp32 outputs; for bf16/fp16 a float32
-    // sincos of the frequency (its error, about 1e-7 rad per step, stays far below their
-    // rounding over the walk's 16 steps) at a fraction of the cost
+    // the rotation through G positions: double for fp32 outputs, else as rotation_at
     if constexpr (DT == VELOGRAD_DTYPE_F32) {
       double sv, cv;
-      sincos(fd, &sv, &cv);
+      sincos((double)G * rope_freq(lt * PP + q, a.rope_c_hi, a.rope_c_lo), &sv, &cv);
       cst[q] = cv;
       sst[q] = sv;
     } else {
       float sv, cv;
-      sincosf((float)fd, &sv, &cv);
+      rotation_at(G, q, cv, sv);
       cst[q] = cv;
       sst[q] = sv;
     }
-    // the rotation at the walk's first position: double angle, reduced exactly, float sincospi
-    const double rev = (double)(row0 % a.rope_seq) * fd * kInv2PiD;
-    float sf, cf;
-    sincospif(2.0f * (float)(rev - rint(rev)), &sf, &cf);
-    cr[q] = cf;
-    sr[q] = sf;
+    rotation_at(pos0, q, c0[q], s0[q]);
+    cr[q] = c0[q];
+    sr[q] = s0[q];
   }
 
   auto make_h = [&](const u32x4& xq, const u32x4& rq, float* hf) {
@@ -546,7 +558,7 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
     const float mean = (RF & kRopeDimPow2) ? ss * inv_dim : ss / (float)a.dim;
     return 1.0f / __builtin_sqrtf(floor_mean_sq(mean, a.ms_floor) + a.eps);
   };
-  // y = (h * r) * w turned by the current angles, then the angles advance one position
+  // y = (h * r) * w turned by the current angles
   auto make_y = [&](const float* hf, float r, float* yf) {
 #pragma unroll
     for (int i = 0; i < V; ++i) yf[i] = (hf[i] * r) * wf[i];
@@ -556,39 +568,57 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
       const float y0 = yf[2 * q], y1 = yf[2 * q + 1];
       yf[2 * q] = __builtin_fmaf(y0, cv, -(y1 * sv));                    // functional.py:313
       yf[2 * q + 1] = __builtin_fmaf(y0, sv, y1 * cv);                   // functional.py:314
-      const double cn = __builtin_fma(cr[q], cst[q], -(sr[q] * sst[q]));
-      sr[q] = __builtin_fma(sr[q], cst[q], cr[q] * sst[q]);
-      cr[q] = cn;
     }
   };
-  auto restart = [&]() {
-    // a new outer index: position 0, the identity rotation
+  // the angles of the next row of the walk: pos advances by G; past the end of the sequence it
+  // returns to pos0 (back_to_start) or, with ANCHOR, lands anywhere and is evaluated afresh
+  auto advance = [&](int64_t& pos, auto anchor) {
+    pos += G;
+    if (pos < seq) {
 #pragma unroll
-    for (int q = 0; q < PP; ++q) {
-      cr[q] = 1.0;
-      sr[q] = 0.0;
+      for (int q = 0; q < PP; ++q) {
+        const double cn = __builtin_fma(cr[q], cst[q], -(sr[q] * sst[q]));
+        sr[q] = __builtin_fma(sr[q], cst[q], cr[q] * sst[q]);
+        cr[q] = cn;
+      }
+    } else if (!decltype(anchor)::value || back_to_start) {
+      pos = pos0;
+#pragma unroll
+      for (int q = 0; q < PP; ++q) {
+        cr[q] = c0[q];
+        sr[q] = s0[q];
+      }
+    } else {
+      pos %= seq;
+#pragma unroll
+      for (int q = 0; q < PP; ++q) {
+        float c, s;
+        rotation_at(pos, q, c, s);
+        cr[q] = c;
+        sr[q] = s;
+      }
     }
   };
 
-  if (nrows == kNormRopeRows && nchunk == tpr) {
+  const bool walk_ok = back_to_start || pos0 + (int64_t)(kNormRopeRows - 1) * G < seq;
+  if (nrows == kNormRopeRows && nchunk == tpr && walk_ok) {
     __shared__ float inv_lds[kNormRopeRows];
     constexpr int RB = 3;
     u32x4 xb[RB], rb[RB];
     xb[0] = xv;
     rb[0] = rv;
-    xb[1] = load16_stream<DT>(a.x, (row0 + 1) * a.ld_x + col);
-    if constexpr (has_res) rb[1] = load16_stream<DT>(a.res, (row0 + 1) * a.ld_res + col);
-    int64_t pos = row0 % a.rope_seq;
+    xb[1] = load16_stream<DT>(a.x, (row0 + G) * a.ld_x + col);
+    if constexpr (has_res) rb[1] = load16_stream<DT>(a.res, (row0 + G) * a.ld_res + col);
+    int64_t pos = pos0;
 #pragma unroll
     for (int it = 0; it < kNormRopeRows; ++it) {
       const int b = it % RB;
-      const int64_t row = row0 + it;
+      const int64_t row = row0 + it * G;
       if (it + 2 < kNormRopeRows) {
         const int nb = (it + 2) % RB;
-        xb[nb] = load16_stream<DT>(a.x, (row + 2) * a.ld_x + col);
-        if constexpr (has_res) rb[nb] = load16_stream<DT>(a.res, (row + 2) * a.ld_res + col);
+        xb[nb] = load16_stream<DT>(a.x, (row + 2 * G) * a.ld_x + col);
+        if constexpr (has_res) rb[nb] = load16_stream<DT>(a.res, (row + 2 * G) * a.ld_res + col);
       }
-      if (it > 0 && pos == 0) restart();
       float hf[V];
       make_h(xb[b], rb[b], hf);
       if constexpr (write_h) store16_stream<DT>(a.h, row * a.ld_h + col, C::pack(hf));
@@ -597,22 +627,20 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
       float yf[V];
       make_y(hf, r, yf);
       store16_stream<DT>(a.y, row * a.ld_y + col, C::pack(yf));
-      pos = (pos + 1 == a.rope_seq) ? 0 : pos + 1;
+      if (it + 1 < kNormRopeRows) advance(pos, std::false_type{});
     }
     // thread 0 wrote inv_lds; threads 1..15 of its wave read it in program order
-    if (lt < kNormRopeRows && a.inv_rms != nullptr) a.inv_rms[row0 + lt] = inv_lds[lt];
+    if (lt < kNormRopeRows && a.inv_rms != nullptr) a.inv_rms[row0 + lt * G] = inv_lds[lt];
     return;
   }
 
-  // the position advances with the row and wraps at rope_seq (no division inside the walk)
-  int64_t pos = row0 % a.rope_seq;
-  for (int it = 0; it < nrows; ++it, pos = (pos + 1 == a.rope_seq) ? 0 : pos + 1) {
-    const int64_t row = row0 + it;
-    if (it > 0 && pos == 0) restart();
+  int64_t pos = pos0;
+  for (int it = 0; it < nrows; ++it) {
+    const int64_t row = row0 + it * G;
     u32x4 xn = u32x4{0u, 0u, 0u, 0u}, rn = u32x4{0u, 0u, 0u, 0u};
     if (it + 1 < nrows && lane_ok) {
-      xn = load16_stream<DT>(a.x, (row + 1) * a.ld_x + col);
-      if constexpr (has_res) rn = load16_stream<DT>(a.res, (row + 1) * a.ld_res + col);
+      xn = load16_stream<DT>(a.x, (row + G) * a.ld_x + col);
+      if constexpr (has_res) rn = load16_stream<DT>(a.res, (row + G) * a.ld_res + col);
     }
     float hf[V];
     make_h(xv, rv, hf);
@@ -622,6 +650,7 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
     float yf[V];
     make_y(hf, r, yf);
     if (lane_ok) store16_stream<DT>(a.y, row * a.ld_y + col, C::pack(yf));
+    if (it + 1 < nrows) advance(pos, std::true_type{});
     xv = xn;
     rv = rn;
   }
