@@ -79,8 +79,8 @@ int main() {
   }
   // Backward plans and the workspace query, on the dims the benchmarks and tests use plus a
   // spread of others, for every tuning knob value range.
-  const int64_t dims[] = {1, 4, 13, 16, 64, 100, 768, 4096, 4104, 5120, 7168, 8192, 16384,
-                          20000, 40000};
+  const int64_t dims[] = {1, 4, 13, 16, 64, 100, 512, 768, 1024, 2048, 4096, 4104, 5120, 7168,
+                          8192, 16384, 20000, 40000};
   for (int64_t dim : dims) {
     for (int64_t rows : rows_list) {
       for (int cus : cus_list) {
@@ -137,6 +137,32 @@ int main() {
                   } else {
                     CHECK(!ring_eligible(rg.rp, dim, eb), "eligible ring plan refused");
                   }
+                  // the ring-pipelined plan with the fused RoPE gradient: whole rows of one
+                  // chunk per thread, at most kRopeRingWgsPerCu workgroups per CU, its tables
+                  // and combine within 64 KiB of LDS, its partials within the workspace
+                  const BwdPlan rr = plan_bwd_rope_ring(rows, dim, eb, aligned != 0, cus);
+                  if (rr.ring) {
+                    check_row_plan(rr.rp, dim, eb, aligned != 0);
+                    CHECK(rope_ring_eligible(rr.rp, dim, eb), "rope ring plan not eligible");
+                    CHECK(rr.rp.nv == 1 && (int64_t)rr.rp.tpr * (16 / eb) == dim &&
+                              rr.rp.block <= kRingBlock,
+                          "rope ring nv %d tpr %d block %d dim=%lld", rr.rp.nv, rr.rp.tpr,
+                          rr.rp.block, (long long)dim);
+                    CHECK(rr.wgs >= 1 && rr.wgs <= (int64_t)cus * kRopeRingWgsPerCu &&
+                              rr.wgs <= (rows + rr.rp.groups - 1) / rr.rp.groups,
+                          "rope ring wgs=%lld", (long long)rr.wgs);
+                    CHECK((size_t)rr.wgs * (size_t)dim * sizeof(float) <= ws,
+                          "rope ring partials %lld x %lld exceed workspace %zu",
+                          (long long)rr.wgs, (long long)dim, ws);
+                    const size_t tables = (size_t)rr.rp.block * (16 / eb / 2) * 24;
+                    CHECK(rr.lds_bytes <= 64 * 1024 &&
+                              rr.lds_bytes == tables + (rr.rp.groups > 1 ? dim * 4 : 0),
+                          "rope ring lds %zu", rr.lds_bytes);
+                  } else {
+                    CHECK(!(aligned && eb == 2 && dim % 512 == 0 && dim <= 4096) &&
+                              !(aligned && eb == 4 && dim % 256 == 0 && dim <= 2048),
+                          "rope ring plan refused dim=%lld eb=%d", (long long)dim, eb);
+                  }
                   ++plans;
                 }
               }
@@ -146,6 +172,39 @@ int main() {
       }
     }
   }
+  // rope_walk_ok: where it holds, the RoPE ring kernel's position rule (start at slot % seq,
+  // add S per row, back to the start where that reaches seq) gives row % seq for every row of
+  // every slot's walk.
+  const int64_t slot_counts[] = {1, 2, 3, 5, 64, 100, 128, 512, 600, 1024, 4096};
+  const int64_t seqs[] = {1, 2, 3, 7, 64, 100, 300, 1000, 1024, 2048, 3000, 16384};
+  const int64_t walk_rows[] = {1, 5, 64, 1000, 5000, 16384};
+  long walks = 0;
+  for (int64_t S : slot_counts) {
+    for (int64_t seq : seqs) {
+      for (int64_t rows : walk_rows) {
+        if (!rope_walk_ok(rows, S, seq)) continue;
+        const int64_t iters = (rows + S - 1) / S;
+        for (int64_t slot = 0; slot < S && slot < rows; ++slot) {
+          const int64_t pos0 = slot % seq;
+          int64_t pos = pos0;
+          for (int64_t j = 0; j < iters; ++j) {
+            const int64_t row = slot + j * S;
+            if (row < rows)
+              CHECK(pos == row % seq, "walk S=%lld seq=%lld rows=%lld slot %lld row %lld: "
+                    "pos %lld", (long long)S, (long long)seq, (long long)rows, (long long)slot,
+                    (long long)row, (long long)pos);
+            pos += S;
+            if (pos >= seq) pos = pos0;
+          }
+          ++walks;
+        }
+      }
+    }
+  }
+  CHECK(rope_walk_ok(16384, 512, 16384) && rope_walk_ok(16384, 512, 2048) &&
+            rope_walk_ok(16448, 2048, 64) && !rope_walk_ok(6000, 512, 1000),
+        "rope_walk_ok on the test shapes");
+  printf("rope walks checked: %ld\n", walks);
   if (failures) {
     fprintf(stderr, "%d failures over %ld plans\n", failures, plans);
     return 1;

@@ -139,8 +139,9 @@ def test_errors():
 # the norm's backward.  Truth is the composition of the two pinned float64 oracles: the inverse
 # interleaved rotation (functional.py:316-345) then the module backward (nn.py:357-383) with the
 # device's h and inv_rms.  Bound: 16 float32 ulps of each gradient pair (angles in double), plus
-# 2^-18 of the pair for the float32 rotation recurrence of the walk (re-evaluated directly every
-# 16 rows, so at most 15 steps of a few ulps each, whatever the walk's length),
+# 2^-18 of the pair for the float32 rotation recurrence of bwd_vec_kernel's walk (re-evaluated
+# directly every 16 rows, so at most 15 steps of a few ulps each, whatever the walk's length; the
+# ring kernel's double recurrence stays far inside it),
 # propagated through dx = r (w g - xhat mean(w g xhat)) and dweight = sum g xhat; on top of it
 # the usual dx rule (1 ulp or the operand-scaled floor) and the dweight rule (1e-3).
 # ---------------------------------------------------------------------------------------------
@@ -187,7 +188,15 @@ def _check_rope_backward(dx, dw, g, h, w, inv, base, what, g_round=0.0, position
 BWD_CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 8192), True),
              (torch.float32, (3, 33, 1000), True), (torch.float16, (2, 50, 256), False),
              (torch.bfloat16, (3, 5, 6), True), (torch.float32, (4, 2, 3, 40), True),
-             (torch.bfloat16, (1, 16384, 4096), True), (torch.bfloat16, (8, 2048, 4096), True)]
+             (torch.bfloat16, (1, 16384, 4096), True), (torch.bfloat16, (8, 2048, 4096), True),
+             # the ring kernel (bwd_rope_ring_kernel): fp32 with two row groups per workgroup
+             # and a 16-row walk; fp16 with eight row groups and no weight, one row per slot;
+             # four row groups, a partial last iteration and a return to the walk's first
+             # position on every row; two row groups returning on every row.  Then a shape whose
+             # walks cross sequence ends at other positions: bwd_vec_kernel's re-evaluating walk
+             (torch.float32, (4, 4096, 1024), True), (torch.float16, (3, 1000, 512), False),
+             (torch.bfloat16, (257, 64, 1024), True), (torch.bfloat16, (8, 1024, 2048), True),
+             (torch.bfloat16, (6, 1000, 4096), True)]
 
 
 @pytest.mark.parametrize("dtype,shape,with_w", BWD_CASES,

@@ -194,6 +194,60 @@ inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool ali
   return b;
 }
 
+// The ring-pipelined backward with the fused RoPE gradient (bwd_rope_ring_kernel): whole rows
+// of one 16-byte chunk per thread (its rotation state, in double, takes 32 VGPRs a lane), row
+// groups packed into workgroups of kRingBlock threads, kRopeRingWgsPerCu workgroups per CU.
+// `ring` is false when the row layout does not suit it.  The kernel also needs every slot's walk
+// to advance by the slot count or return to its first position (rope_walk_ok).
+constexpr int kRopeRingWgsPerCu = 2;
+
+inline BwdPlan plan_bwd_rope_ring(int64_t rows, int64_t dim, int elem_bytes, bool aligned,
+                                  int cus) {
+  BwdPlan b;
+  b.rp = RowPlan{false, 0, kGenericBlock, 1, kGenericBlock};
+  b.wgs = 0;
+  b.lds_bytes = 0;
+  if ((elem_bytes != 2 && elem_bytes != 4) || !aligned || dim <= 0) return b;
+  const int V = 16 / elem_bytes;
+  if (dim % V != 0) return b;
+  const int64_t chunks = dim / V;
+  if (chunks % kWave != 0 || chunks > kRingBlock) return b;
+  RowPlan& p = b.rp;
+  p.vec = true;
+  p.nv = 1;
+  p.tpr = (int)chunks;
+  p.groups = kRingBlock / p.tpr;
+  p.block = p.tpr * p.groups;
+  const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
+  int64_t wgs = (int64_t)(cus > 0 ? cus : 1) * kRopeRingWgsPerCu;
+  if (wgs > wgs_needed) wgs = wgs_needed;
+  b.wgs = wgs;
+  // per thread and pair of its chunk (V / 2 pairs): the double step rotation and the float first
+  // rotation, 24 bytes; then, with several row groups, their dweight combine
+  const int pairs = V / 2;
+  b.lds_bytes = (size_t)p.block * pairs * (2 * sizeof(double) + 2 * sizeof(float)) +
+                (p.groups > 1 ? (size_t)dim * sizeof(float) : 0);
+  b.ring = true;
+  return b;
+}
+
+// Whether `slots` row slots walking `rows` rows (slot s: rows s, s + slots, ...) see positions
+// (row % seq) that only advance by `slots` or return to the walk's first one: slots is a
+// multiple or a divisor of seq, or no walk reaches the end of a sequence.
+inline bool rope_walk_ok(int64_t rows, int64_t slots, int64_t seq) {
+  if (rows <= 0 || slots <= 0 || seq <= 0) return false;
+  if (seq % slots == 0 || slots % seq == 0) return true;
+  const int64_t iters = (rows + slots - 1) / slots;
+  return iters <= seq / slots;  // iters * slots <= seq
+}
+
+// Whether a plan suits bwd_rope_ring_kernel (the facts its indexing relies on).
+inline bool rope_ring_eligible(const RowPlan& p, int64_t dim, int elem_bytes) {
+  if (!p.vec || (elem_bytes != 2 && elem_bytes != 4)) return false;
+  return p.nv == 1 && p.tpr % kWave == 0 && (int64_t)p.tpr * (16 / elem_bytes) == dim &&
+         p.block == p.tpr * p.groups && p.block <= kRingBlock;
+}
+
 // Backward plan with the fused inverse RoPE: the same layout under max_block_for_nv_rope, or the
 // generic plan where a row group does not fit that bound.
 inline BwdPlan plan_bwd_rope(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
@@ -228,6 +282,8 @@ inline size_t bwd_workspace_bytes(int64_t rows, int64_t dim, int cus, int prefer
       if (nr > most) most = nr;
       const BwdPlan rg = plan_bwd_ring(rows, dim, sizes[si], al != 0, cus, prefer_nv);
       if (rg.ring && rg.wgs > most) most = rg.wgs;
+      const BwdPlan rr = plan_bwd_rope_ring(rows, dim, sizes[si], al != 0, cus);
+      if (rr.ring && rr.wgs > most) most = rr.wgs;
     }
   }
   return (size_t)most * (size_t)dim * sizeof(float);

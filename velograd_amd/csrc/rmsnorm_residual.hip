@@ -8,7 +8,9 @@
 //             dweight = sum over rows of g * xhat,  with xhat = h * inv_rms
 // Every operation is fp32 and rounds where the NumPy reference rounds (this file is built with
 // -ffp-contract=off so no multiply-add pair is fused behind the code's back); stores round to
-// nearest even.  Only the order of the row sums differs from NumPy's pairwise summation.
+// nearest even.  Only the order of the row sums differs from NumPy's pairwise summation.  The
+// exceptions are the norm + RoPE kernels, whose walks are bound by their vector instructions:
+// they fuse multiply-adds explicitly (one rounding where the reference has two).
 //
 // Kernels
 //   fwd_vec_kernel      one row per `tpr` threads (1..16 wave64), `groups` rows per workgroup;
@@ -21,6 +23,11 @@
 //   bwd_ring_kernel     the same walk for whole rows with a ring of three row buffers (two rows
 //                       in flight while one reduces) in a branch-free steady loop, 512-thread
 //                       workgroups, one per CU: the backward's default where the rows suit it.
+//   fwd_rope_kernel     the forward with the model's interleaved RoPE on y: strided row walks
+//                       with the rotation advanced by a double recurrence.
+//   bwd_rope_ring_kernel  its backward (grad_y rotated back, then the norm's backward) in
+//                       bwd_ring_kernel's walk, one chunk per thread, two workgroups per CU;
+//                       bwd_vec_kernel with kRopeG where the rows or positions do not suit it.
 //   dweight_reduce      stage 2: sums the partial rows in a fixed order -> dweight[dim].
 //   *_generic_kernel    any dim and any alignment: the same arithmetic with scalar accesses.
 // Row sums: DPP inside each 16-lane row of the wave, readlane across the four rows, LDS only
@@ -1172,6 +1179,189 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
 }
 
 // ------------------------------------------------------------------------------------------
+// Backward with the fused RoPE gradient, ring-pipelined (launch_plan.h: plan_bwd_rope_ring):
+// whole rows of one 16-byte chunk per thread, the saved tensor h, no grad_h or dres (the
+// module's backward).  The walk, ring and steady loop are bwd_ring_kernel's: slot s walks rows
+// s, s + S, ... (S slots), three row buffers, rows past the end read the last row, no branch
+// around a memory operation in the steady loop.  Each thread keeps the rotation (cos, sin) of
+// its pairs at the current row's position in double and advances it by S positions per row with
+// the rotation through S * freq_j (a double sincos, once per walk), so the state drifts ~1e-16
+// per step and is never evaluated again; where a walk crosses the end of a sequence, S is a
+// multiple or a divisor of rope_seq (rope_walk_ok: the host plans this kernel only then, or when
+// no walk reaches a sequence end), so the position returns to the walk's first one and the
+// rotation to its first value, kept.  The walk is bound by its vector instructions as much as by
+// HBM, so the row's decoded, rotated chunk stays in registers across the reduction, the weight
+// is decoded once, sums of products use fused multiply-adds, and for a power-of-two dim the mean
+// is s * (1 / dim), exact.
+// ------------------------------------------------------------------------------------------
+template <int DT, int WDT>
+__global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(const BwdArgs a) {
+  using C = Codec<DT>;
+  constexpr int V = C::kVec;
+  constexpr int P = V / 2;  // RoPE pairs per chunk
+  constexpr int PF = vg_plan::kRingPrefetch;
+  constexpr int R = PF + 1;
+  __shared__ float red[2][kMaxWavesPerRow];
+  // Dynamic LDS: each thread's step rotations (P double pairs) and first rotations (P float
+  // pairs), pair-major so a wave reads consecutive 16- and 8-byte entries, then with several row
+  // groups dim floats for their combine (rope_ring_lds_bytes).
+  extern __shared__ __align__(16) float dyn_lds[];
+
+  const int tpr = a.tpr;
+  const int grp = threadIdx.x / tpr;
+  const int lt = threadIdx.x - grp * tpr;
+  const int groups = blockDim.x / tpr;
+  const int64_t slot = (int64_t)blockIdx.x * groups + grp;
+  const int64_t S = (int64_t)gridDim.x * groups;
+  const int64_t last = a.rows - 1;
+  const int64_t col = (int64_t)lt * V;
+  const int64_t seq = a.rope_seq;
+  const int64_t pos0 = slot % seq;
+  double2* step_lds = reinterpret_cast<double2*>(dyn_lds);               // [P][blockDim]
+  float2* first_lds = reinterpret_cast<float2*>(step_lds + P * blockDim.x);  // [P][blockDim]
+  float* comb = reinterpret_cast<float*>(first_lds + P * blockDim.x);
+  // 1 / dim is exact for a power of two, so s * (1 / dim) has the bits of s / dim
+  const bool dim_pow2 = (a.dim & (a.dim - 1)) == 0;
+  const float inv_dim = 1.0f / (float)a.dim;
+
+  float wf[V], acc[V];
+  {
+    WeightChunk<DT, WDT> wc;
+    wc.load(a.w, col);
+    wc.unpack(a.w != nullptr, wf);
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+  // one pair at a time (a double sincos holds many registers; the walk needs them)
+#pragma unroll 1
+  for (int q = 0; q < P; ++q) {
+    const double f = rope_freq(lt * P + q, a.rope_c_hi, a.rope_c_lo);
+    double sv, cv;
+    sincos((double)S * f, &sv, &cv);
+    step_lds[q * blockDim.x + threadIdx.x] = double2{cv, sv};
+    // the rotation at the walk's first position: double angle, reduced exactly, float sincospi
+    const double rev = (double)pos0 * f * kInv2PiD;
+    float s0, c0;
+    sincospif(2.0f * (float)(rev - rint(rev)), &s0, &c0);
+    first_lds[q * blockDim.x + threadIdx.x] = float2{c0, s0};
+  }
+  double cr[P], sr[P];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    const float2 f0 = first_lds[q * blockDim.x + threadIdx.x];
+    cr[q] = f0.x;
+    sr[q] = f0.y;
+  }
+  int64_t pos = pos0;
+
+  u32x4 gr[R], hr[R];
+  float rr[R];
+  // Row `row`'s grad_y and h chunks and inv_rms; rows past the end read the last row.
+  auto load_row = [&](int64_t row, u32x4& gv, u32x4& hv, float& r) {
+    const int64_t rw = row < a.rows ? row : last;
+    r = a.inv_rms[rw];
+    gv = load16_stream<DT>(a.g, rw * a.ld_g + col);
+    hv = load16_stream<DT>(a.saved, rw * a.ld_s + col);
+  };
+  // The backward of one row (bwd_vec_kernel's with kSavedIsH | kRopeG); `ok` = the row exists.
+  auto process = [&](const u32x4& gv, const u32x4& hv, float r, int64_t row, bool ok, int it) {
+    float gf[V], xh[V];
+    C::unpack(gv, gf);
+    // inverse rotation of each pair (y0, y1) -> (y0 c + y1 s, y1 c - y0 s)
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const float c = (float)cr[q], sn = (float)sr[q];
+      const float g0 = gf[2 * q], g1 = gf[2 * q + 1];
+      gf[2 * q] = __builtin_fmaf(g0, c, g1 * sn);
+      gf[2 * q + 1] = __builtin_fmaf(g1, c, -(g0 * sn));
+    }
+    C::unpack(hv, xh);
+#pragma unroll
+    for (int i = 0; i < V; ++i) xh[i] = xh[i] * r;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) s = __builtin_fmaf(gf[i] * wf[i], xh[i], s);
+    s = row_sum(s, tpr, grp, red[it & 1]);
+    const float m = dim_pow2 ? s * inv_dim : s / (float)a.dim;
+    float d[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) d[i] = r * __builtin_fmaf(-xh[i], m, gf[i] * wf[i]);
+    if (ok) store16_stream<DT>(a.dx, row * a.ld_dx + col, C::pack(d));
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      acc[i] = ok ? __builtin_fmaf(gf[i], xh[i], acc[i]) : acc[i];
+      // the row's sums are done here: its g and xhat are not held into the next row
+      asm volatile("" : "+v"(acc[i]));
+    }
+    // the next row's angles: S positions on, or the walk's first position again
+    // (each thread reads only the LDS entries it wrote, in program order: no barrier)
+    pos += S;
+    if (pos < seq) {
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const double2 st = step_lds[q * blockDim.x + threadIdx.x];
+        const double cn = __builtin_fma(cr[q], st.x, -(sr[q] * st.y));
+        sr[q] = __builtin_fma(sr[q], st.x, cr[q] * st.y);
+        cr[q] = cn;
+      }
+    } else {
+      pos = pos0;
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const float2 f0 = first_lds[q * blockDim.x + threadIdx.x];
+        cr[q] = f0.x;
+        sr[q] = f0.y;
+      }
+    }
+  };
+
+  // Row j of the walk sits in buffer j % R; processing row j first issues row j + PF's loads
+  // into buffer (j + PF) % R, the one row j - 1 has just released.
+  const int full = (int)(a.rows / S);  // iterations in which every slot has a row
+#pragma unroll
+  for (int j = 0; j < PF; ++j) load_row(slot + (int64_t)j * S, gr[j], hr[j], rr[j]);
+  int it = 0;
+  for (; it + R <= full; it += R) {
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const int nb = (u + PF) % R;
+      load_row(slot + (int64_t)(it + u + PF) * S, gr[nb], hr[nb], rr[nb]);
+      process(gr[u], hr[u], rr[u], slot + (int64_t)(it + u) * S, true, it + u);
+    }
+  }
+  // The last (up to R) iterations, some of whose slots may have no row.
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    if (it + u < a.iters) {
+      const int nb = (u + PF) % R;
+      if (it + u + PF < a.iters)
+        load_row(slot + (int64_t)(it + u + PF) * S, gr[nb], hr[nb], rr[nb]);
+      const int64_t row = slot + (int64_t)(it + u) * S;
+      process(gr[u], hr[u], rr[u], row, row < a.rows, it + u);
+    }
+  }
+
+  if (a.partial == nullptr) return;
+  // One fp32 partial row per workgroup; row groups added in group order through LDS.
+  float* prow = a.partial + (int64_t)blockIdx.x * a.dim;
+  if (groups == 1) {
+#pragma unroll
+    for (int q = 0; q < V / 4; ++q)
+      store16<VELOGRAD_DTYPE_F32>(prow, col + 4 * q, Codec<VELOGRAD_DTYPE_F32>::pack(&acc[4 * q]));
+    return;
+  }
+  for (int gi = 0; gi < groups; ++gi) {
+    if (grp == gi) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) comb[col + i] = (gi == 0) ? acc[i] : comb[col + i] + acc[i];
+    }
+    __syncthreads();
+  }
+  for (int q = threadIdx.x; q < a.dim / 4; q += blockDim.x)
+    store16<VELOGRAD_DTYPE_F32>(prow, 4 * (int64_t)q, *reinterpret_cast<const u32x4*>(comb + 4 * q));
+}
+
+// ------------------------------------------------------------------------------------------
 // Backward, any dim / alignment: one row slot per workgroup, two passes per row; the slot's
 // dweight partial row is accumulated in place (each column owned by one thread).
 // ------------------------------------------------------------------------------------------
@@ -1299,11 +1489,16 @@ RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned, bool one_stream) {
                             one_stream ? vg_plan::kFwdOrderOneStream : vg_plan::kFwdOrder);
 }
 
-BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus, bool rope) {
+BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus, bool rope,
+                 int64_t rope_seq) {
   const Tuning& t = tuning();
   if (!rope && t.bwd_ring) {
     const BwdPlan r = vg_plan::plan_bwd_ring(rows, dim, elem_bytes, aligned, cus, t.bwd_nv);
     if (r.ring) return r;
+  }
+  if (rope && t.bwd_ring) {
+    const BwdPlan r = vg_plan::plan_bwd_rope_ring(rows, dim, elem_bytes, aligned, cus);
+    if (r.ring && vg_plan::rope_walk_ok(rows, r.wgs * r.rp.groups, rope_seq)) return r;
   }
   if (rope)
     return vg_plan::plan_bwd_rope(rows, dim, elem_bytes, aligned, cus, t.bwd_nv, t.bwd_block,
@@ -1388,6 +1583,10 @@ void launch_bwd_flags(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
     }
   }
   if constexpr ((F & kRopeG) != 0) {
+    if (b.ring) {
+      hipLaunchKernelGGL((bwd_rope_ring_kernel<DT, WDT>), grid, block, lds, st, a);
+      return;
+    }
     // NV 4 is never planned with the RoPE gradient (max_block_for_nv_rope); it is not compiled
     switch (p.nv) {
       case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, F>), grid, block, lds, st, a); break;
@@ -1654,15 +1853,18 @@ int32_t run_bwd(const void* grad_y, const void* saved, int32_t saved_is_h, const
                        (!grad_h || (aligned16(grad_h) && ld_ok(ld_grad_h, eb))) &&
                        (!weight || aligned16(weight));
   const bool rope = rope_seq > 0;
-  BwdPlan plan = plan_bwd(rows, dim, eb, aligned, cus, rope);
-  // The RoPE walk keeps its step rotations (two floats per pair: dim floats) in the same dynamic
-  // LDS as the group combine, one after the other.
-  if (rope && plan.rp.vec) plan.lds_bytes = (size_t)dim * sizeof(float);
+  BwdPlan plan = plan_bwd(rows, dim, eb, aligned, cus, rope, rope_seq);
+  // bwd_vec_kernel's RoPE walk keeps its step rotations (two floats per pair: dim floats) in the
+  // same dynamic LDS as the group combine, one after the other.
+  if (rope && plan.rp.vec && !plan.ring) plan.lds_bytes = (size_t)dim * sizeof(float);
   if (!vg_plan::row_plan_valid(plan.rp, dim, eb) || plan.wgs < 1 || plan.wgs > INT32_MAX ||
       plan.lds_bytes > 64 * 1024 ||
-      (plan.ring && (!vg_plan::ring_eligible(plan.rp, dim, eb) ||
-                     plan.rp.block > vg_plan::kRingBlock)) ||
-      (rope && plan.rp.vec && plan.rp.block > vg_plan::max_block_for_nv_rope(plan.rp.nv)))
+      (plan.ring && !rope && (!vg_plan::ring_eligible(plan.rp, dim, eb) ||
+                              plan.rp.block > vg_plan::kRingBlock)) ||
+      (plan.ring && rope && (!vg_plan::rope_ring_eligible(plan.rp, dim, eb) ||
+                             !vg_plan::rope_walk_ok(rows, plan.wgs * plan.rp.groups, rope_seq))) ||
+      (rope && plan.rp.vec && !plan.ring &&
+       plan.rp.block > vg_plan::max_block_for_nv_rope(plan.rp.nv)))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: internal launch plan rejected (dim=%lld)",
                 (long long)dim);
   const int64_t slots = plan.wgs * plan.rp.groups;  // row slots walking the rows
