@@ -136,16 +136,23 @@ __device__ inline void store16(void* base, int64_t elem, const u32x4 v) {
 // Streamed activations are touched once per launch: non-temporal loads and stores keep them from
 // displacing reusable lines (weight, partial sums) in L2 and the MALL.  A stream-pattern probe
 // with the fwd (2 reads + 2 writes) and bwd (2 reads + 1 write) shapes measured +8..12% from the
-// non-temporal forms on MI355X.  Build with -DVG_STREAM_NT=0 to compare.
+// non-temporal forms on MI355X.  Build with -DVG_STREAM_NT=0 to compare, or set the loads' and
+// the stores' policy alone with VG_STREAM_NT_LOAD / VG_STREAM_NT_STORE.
 #ifndef VG_STREAM_NT
 #define VG_STREAM_NT 1
+#endif
+#ifndef VG_STREAM_NT_LOAD
+#define VG_STREAM_NT_LOAD VG_STREAM_NT
+#endif
+#ifndef VG_STREAM_NT_STORE
+#define VG_STREAM_NT_STORE VG_STREAM_NT
 #endif
 
 template <int DT>
 __device__ inline u32x4 load16_stream(const void* base, int64_t elem) {
   const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const char*>(base) +
                                                   elem * Codec<DT>::kBytes);
-#if VG_STREAM_NT
+#if VG_STREAM_NT_LOAD
   return __builtin_nontemporal_load(p);
 #else
   return *p;
@@ -155,7 +162,7 @@ __device__ inline u32x4 load16_stream(const void* base, int64_t elem) {
 template <int DT>
 __device__ inline void store16_stream(void* base, int64_t elem, const u32x4 v) {
   u32x4* p = reinterpret_cast<u32x4*>(static_cast<char*>(base) + elem * Codec<DT>::kBytes);
-#if VG_STREAM_NT
+#if VG_STREAM_NT_STORE
   __builtin_nontemporal_store(v, p);
 #else
   *p = v;
