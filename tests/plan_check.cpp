@@ -72,7 +72,9 @@ int main() {
                          aligned != 0);
           check_row_plan(plan_rows(dim, eb, aligned != 0, prefer, kBwdOrder), dim, eb,
                          aligned != 0);
-          plans += 3;
+          check_row_plan(plan_rows(dim, eb, aligned != 0, prefer, kFwdOrderEpilogue), dim, eb,
+                         aligned != 0);
+          plans += 4;
         }
       }
     }

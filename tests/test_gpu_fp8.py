@@ -80,9 +80,11 @@ def test_fp8_epilogue_matches_oracle(dtype, rows, d, wdt, with_res):
     res = P.to_device(P.gaussian(rng, (rows, d)), dtype) if with_res else None
     w = P.to_device(P.weight_vec(rng, d), wdt) if wdt is not None else None
     yq, sc, h, inv = _check(x, res, w, 1e-5, f"{dtype} {rows}x{d}")
-    # h and inv_rms are those of the plain forward, and y_fp8 * scale is y to e4m3 precision
+    # h is the plain forward's; inv_rms agrees with it to a couple of ulps (the epilogue's plan
+    # takes two chunks per thread where the plain forward takes one, so the row's sum of squares
+    # is added in another order); y_fp8 * scale is y to e4m3 precision
     y, h2, inv2 = vk.fused_rmsnorm_residual_forward(x, res, w, 1e-5)
-    assert torch.equal(inv, inv2)
+    assert P.rel_err(P.upcast(inv), P.upcast(inv2)) <= 2.0 ** -21
     if with_res:
         assert torch.equal(h, h2)
     deq = yq.cpu().float() * sc.cpu()

@@ -57,6 +57,12 @@ struct RowPlan {
 // waves for bytes per lane).
 constexpr int kFwdOrder[kMaxNV] = {1, 2, 3, 4};
 constexpr int kFwdOrderOneStream[kMaxNV] = {2, 4, 3, 1};
+// The quantised epilogues (fp8 per row, MXFP8, MXFP4) reduce each row twice (sum of squares,
+// then amax), so fewer waves per row pay off there: two chunks per thread against one ran
+// 76.9 / 301.5 / 39.9 us against 79.6 / 335.0 / 42.5 us for the per-row fp8 forward at configs
+// C / D / B (and MXFP4 at D 280 against 314); four chunks were within 1% at C and D and 2-3%
+// slower at B.
+constexpr int kFwdOrderEpilogue[kMaxNV] = {2, 4, 3, 1};
 constexpr int kBwdOrder[kMaxNV] = {2, 3, 4, 1};
 // The backward with the fused RoPE gradient prefers one chunk per thread: its rotation state
 // then fits 1024-thread workgroups (16384 x 4096 bf16: 84.0 us against 89.7 us at two chunks

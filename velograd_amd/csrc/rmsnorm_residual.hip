@@ -1483,10 +1483,13 @@ const Tuning& tuning() {
   return t;
 }
 
-// `one_stream`: no residual, so the row kernel reads x and writes y only.
-RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned, bool one_stream) {
+// `one_stream`: no residual, so the row kernel reads x and writes y only.  `epilogue`: a
+// quantised output (fp8 per row, MX), whose two row reductions prefer fewer waves per row.
+RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned, bool one_stream, bool epilogue) {
   return vg_plan::plan_rows(dim, elem_bytes, aligned, tuning().fwd_nv,
-                            one_stream ? vg_plan::kFwdOrderOneStream : vg_plan::kFwdOrder);
+                            epilogue     ? vg_plan::kFwdOrderEpilogue
+                            : one_stream ? vg_plan::kFwdOrderOneStream
+                                         : vg_plan::kFwdOrder);
 }
 
 BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus, bool rope,
@@ -1751,7 +1754,8 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
                        (!h || (aligned16(h) && ld_ok(ld_h, eb))) && (!weight || aligned16(weight));
   // The fused norm + RoPE kernel holds one chunk per thread, so it keeps the residual order
   // (one chunk first) either way.
-  const RowPlan p = plan_fwd(dim, eb, aligned, residual == nullptr && out != kOutRopeI);
+  const RowPlan p = plan_fwd(dim, eb, aligned, residual == nullptr && out != kOutRopeI,
+                            out == kOutFp8Row || mx);
   if (!vg_plan::row_plan_valid(p, dim, eb))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: internal launch plan rejected (dim=%lld)",
                 what, (long long)dim);
