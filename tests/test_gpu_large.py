@@ -83,9 +83,10 @@ def test_norm_rope_backward_beyond_2_pow_31_elements(big):
     w64 = P.upcast(w).astype(np.float64)
     gn = ora.apply_rotary_emb(g64, 10000.0, inverse=True, positions=rows)
     rdx, _ = ora.rmsnorm_module_backward(gn, h64, w64, r64)
-    # angles in double: 16 float32 ulps of the pair at any position, plus 2^-12 for the float32
-    # rotation recurrence over this walk's 512 steps per row slot
-    dg = np.repeat((P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -12)
+    # angles in double: 16 float32 ulps of the pair at any position, plus 2^-18 for the float32
+    # rotation recurrence (8192-wide rows take bwd_vec_kernel's walk, which evaluates the
+    # rotation afresh every 16 rows however long the walk)
+    dg = np.repeat((P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -18)
                    * (np.abs(g64[:, 0::2]) + np.abs(g64[:, 1::2])), 2, axis=1)
     xhat = h64 * r64
     tol = r64 * (np.abs(w64) * dg + np.abs(xhat) * np.mean(np.abs(w64 * xhat) * dg, axis=-1,
