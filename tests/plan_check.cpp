@@ -207,6 +207,14 @@ int main() {
             rope_walk_ok(16448, 2048, 64) && !rope_walk_ok(6000, 512, 1000),
         "rope_walk_ok on the test shapes");
   printf("rope walks checked: %ld\n", walks);
+  // Where the forward stores h: after the reduction for the measured bf16 rows of 2048, 3072
+  // and 4096 (whole rows of at most 512 threads), before it for 5120, 7168 and 8192, and never
+  // on the generic path.
+  for (int64_t dim : {2048, 3072, 4096, 5120, 7168, 8192}) {
+    const RowPlan p = plan_rows(dim, 2, true, 0, kFwdOrder);
+    CHECK(fwd_late_h(p) == (dim <= 4096), "fwd_late_h dim=%lld tpr=%d", (long long)dim, p.tpr);
+  }
+  CHECK(!fwd_late_h(plan_rows(4096, 2, false, 0, kFwdOrder)), "fwd_late_h on the generic plan");
   if (failures) {
     fprintf(stderr, "%d failures over %ld plans\n", failures, plans);
     return 1;

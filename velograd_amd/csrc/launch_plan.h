@@ -113,6 +113,16 @@ inline RowPlan plan_rows(int64_t dim, int elem_bytes, bool aligned, int prefer_n
   return p;
 }
 
+// Where the register-resident forward stores h: after the row reduction, beside y, when a row
+// takes at most kLateHMaxTpr threads; before it otherwise.  Measured on MI355X (bf16, A/B in
+// one process, batched launches over rotating buffer sets, 6 rounds): after is faster at dim
+// 2048 (86.6 against 87.5 us for 32768 rows) and 4096 (86.0 against 86.8 us at 16384 rows;
+// 44.9 against 45.2 at 8192), equal at 3072 (65.2 / 65.1 us), slower at 5120 (110.7 against
+// 109.5) and 8192 (179.1 against 172.7).
+constexpr int kLateHMaxTpr = 512;
+
+inline bool fwd_late_h(const RowPlan& p) { return p.vec && p.tpr <= kLateHMaxTpr; }
+
 // The facts the kernels' indexing relies on; the C entry points refuse to launch a plan that
 // breaks one of them.
 inline bool row_plan_valid(const RowPlan& p, int64_t dim, int elem_bytes) {

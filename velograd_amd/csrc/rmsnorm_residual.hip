@@ -222,6 +222,7 @@ constexpr int kOutFp8Row = 1;  // y as e4m3 codes with one fp32 scale per row
 constexpr int kOutMxE4M3 = 2;  // MXFP8: e4m3 codes, one E8M0 scale per 32 elements
 constexpr int kOutMxE2M1 = 3;  // MXFP4: e2m1 nibbles (two per byte), one E8M0 scale per 32
 constexpr int kOutRopeI = 4;   // y rotated by the reference model's interleaved RoPE
+constexpr int kOutDtypeLateH = 5;  // as kOutDtype, with h stored after the row reduction
 
 // The reference model's RoPE applied to y in registers (python/velograd/functional.py:287-315;
 // models/llama.py:48-49 rotates the normalised attention input): the pair (y_2i, y_2i+1) of a
@@ -318,6 +319,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
   };
 
   const bool write_h = has_res && a.h != nullptr;
+  constexpr bool kLateH = OUT == kOutDtypeLateH;
   float ss = 0.0f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -326,7 +328,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 #pragma unroll
     for (int i = 0; i < V; ++i) ss += hf[i] * hf[i];
     const int c = lt + k * tpr;
-    if (write_h && row_ok && c < nchunk)
+    if (!kLateH && write_h && row_ok && c < nchunk)
       store16_stream<DT>(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf));
   }
 
@@ -351,11 +353,16 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
   };
 
   static_assert(OUT != kOutRopeI, "the RoPE output runs in fwd_rope_kernel");
-  if constexpr (OUT == kOutDtype) {
+  if constexpr (OUT == kOutDtype || OUT == kOutDtypeLateH) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = lt + k * tpr;
       if (row_ok && c < nchunk) {
+        if (kLateH && write_h) {
+          float hf[V];
+          make_h(k, hf);
+          store16_stream<DT>(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf));
+        }
         float yf[V];
         make_y(k, yf);
         store16_stream<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
@@ -1548,6 +1555,22 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
   } else {
     const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups));
     const dim3 block(p.block);
+    if constexpr (OUT == kOutDtype) {
+      if (vg_plan::fwd_late_h(p)) {
+        switch (p.nv) {
+#define VG_LATE_H(N)                                                                          \
+  case N:                                                                                     \
+    hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, N, kOutDtypeLateH>), grid, block, 0, st, a); \
+    break;
+          VG_LATE_H(1)
+          VG_LATE_H(2)
+          VG_LATE_H(3)
+          default: VG_LATE_H(4)
+#undef VG_LATE_H
+        }
+        return;
+      }
+    }
     switch (p.nv) {
       case 1: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 1, OUT>), grid, block, 0, st, a); break;
       case 2: hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 2, OUT>), grid, block, 0, st, a); break;
