@@ -111,7 +111,10 @@ def assert_dweight(got: np.ndarray, ref: np.ndarray, what: str = "dweight"):
 # Seeded inputs (numpy default_rng in fp32, cast to the target dtype with torch RNE).
 # ---------------------------------------------------------------------------------------------
 def gaussian(rng: np.random.Generator, shape, std: float = 1.0) -> np.ndarray:
-    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+    a = rng.standard_normal(shape, dtype=np.float32)
+    if std != 1.0:
+        a *= np.float32(std)  # in place: the same float32 products, no extra copy
+    return a
 
 
 def weight_vec(rng: np.random.Generator, d: int) -> np.ndarray:
@@ -119,13 +122,14 @@ def weight_vec(rng: np.random.Generator, d: int) -> np.ndarray:
 
 
 def with_outliers(rng: np.random.Generator, a: np.ndarray, frac: float = 1e-3,
-                  factor: float = 50.0) -> np.ndarray:
+                  factor: float = 50.0, inplace: bool = False) -> np.ndarray:
+    """`a` with round(frac * size) distinct, uniformly chosen entries scaled by `factor`."""
     n = a.size
     k = max(1, int(round(n * frac)))
     idx = rng.choice(n, size=k, replace=False)
-    out = a.copy().reshape(-1)
-    out[idx] *= np.float32(factor)
-    return out.reshape(a.shape)
+    out = a if inplace else a.copy()
+    out.reshape(-1)[idx] *= np.float32(factor)
+    return out
 
 
 def to_device(a: np.ndarray, dtype: torch.dtype, device="cuda") -> torch.Tensor:
