@@ -139,9 +139,9 @@ def test_errors():
 # the norm's backward.  Truth is the composition of the two pinned float64 oracles: the inverse
 # interleaved rotation (functional.py:316-345) then the module backward (nn.py:357-383) with the
 # device's h and inv_rms.  Bound: 16 float32 ulps of each gradient pair (angles in double), plus
-# 2^-18 of the pair for the float32 rotation recurrence of bwd_vec_kernel's walk (re-evaluated
-# directly every 16 rows, so at most 15 steps of a few ulps each, whatever the walk's length; the
-# ring kernel's double recurrence stays far inside it),
+# 2^-18 of the pair for the float32 rotation recurrence of the backward walks (bwd_vec_kernel's
+# and bwd_rope_ring_kernel's, each re-evaluated directly every 16 rows and at sequence ends, so
+# at most 15 steps of about 3 float32 ulps each, whatever the walk's length),
 # propagated through dx = r (w g - xhat mean(w g xhat)) and dweight = sum g xhat; on top of it
 # the usual dx rule (1 ulp or the operand-scaled floor) and the dweight rule (1e-3).
 # ---------------------------------------------------------------------------------------------
@@ -239,6 +239,30 @@ def test_fused_backward_long_fp32_walk():
         sl = slice(lo, hi)
         _check_rope_backward(dx[:, sl], None, g[:, sl], h[:, sl], w, inv[:, sl], base,
                              f"fp32 long walk rows {lo}..{hi}",
+                             positions=np.arange(lo, hi))
+
+
+@pytest.mark.parametrize("dtype,seq,d", [(torch.bfloat16, 131072, 4096),
+                                         (torch.float32, 65536, 2048)])
+def test_fused_backward_long_ring_walk(dtype, seq, d):
+    """The ring kernel (rows of 512 chunks: bf16 dim 4096, fp32 dim 2048) over one sequence of
+    seq positions: each of its 512 slots walks seq / 512 rows (256, 128) with no position wrap,
+    re-evaluating its rotations every 16 rows; rows at the start, middle and end of the walks
+    keep the 2^-18 recurrence bound."""
+    base = 500000.0
+    print(f"rmsnorm_rope backward ring long walk: {dtype} seq={seq} dim={d}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    x = torch.randn(1, seq, d, device="cuda", generator=gen).to(dtype)
+    g = torch.randn(1, seq, d, device="cuda", generator=gen).to(dtype)
+    w = (1.0 + 0.1 * torch.randn(d, device="cuda", generator=gen)).to(dtype)
+    _, h, inv = vk.rmsnorm_rope_forward(x, w, 1e-6, base)
+    dx, _ = vk.rmsnorm_rope_backward(g, h, w, inv, base)
+    torch.cuda.synchronize()
+    del x
+    for lo, hi in ((0, 1024), (seq // 2 - 512, seq // 2 + 512), (seq - 1024, seq)):
+        sl = slice(lo, hi)
+        _check_rope_backward(dx[:, sl], None, g[:, sl], h[:, sl], w, inv[:, sl], base,
+                             f"{dtype} ring long walk rows {lo}..{hi}",
                              positions=np.arange(lo, hi))
 
 

@@ -211,7 +211,7 @@ inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool ali
 }
 
 // The ring-pipelined backward with the fused RoPE gradient (bwd_rope_ring_kernel): whole rows
-// of one 16-byte chunk per thread (its rotation state, in double, takes 32 VGPRs a lane), row
+// of one 16-byte chunk per thread (its rotation state and tables keep it at 128 VGPRs), row
 // groups packed into workgroups of kRingBlock threads, kRopeRingWgsPerCu workgroups per CU.
 // `ring` is false when the row layout does not suit it.  The kernel also needs every slot's walk
 // to advance by the slot count or return to its first position (rope_walk_ok).
@@ -238,10 +238,10 @@ inline BwdPlan plan_bwd_rope_ring(int64_t rows, int64_t dim, int elem_bytes, boo
   int64_t wgs = (int64_t)(cus > 0 ? cus : 1) * kRopeRingWgsPerCu;
   if (wgs > wgs_needed) wgs = wgs_needed;
   b.wgs = wgs;
-  // per thread and pair of its chunk (V / 2 pairs): the double step rotation and the float first
-  // rotation, 24 bytes; then, with several row groups, their dweight combine
+  // per thread and pair of its chunk (V / 2 pairs): the double frequency and the float step and
+  // first rotations, 24 bytes; then, with several row groups, their dweight combine
   const int pairs = V / 2;
-  b.lds_bytes = (size_t)p.block * pairs * (2 * sizeof(double) + 2 * sizeof(float)) +
+  b.lds_bytes = (size_t)p.block * pairs * (sizeof(double) + 4 * sizeof(float)) +
                 (p.groups > 1 ? (size_t)dim * sizeof(float) : 0);
   b.ring = true;
   return b;

@@ -1191,15 +1191,18 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
 // module's backward).  The walk, ring and steady loop are bwd_ring_kernel's: slot s walks rows
 // s, s + S, ... (S slots), three row buffers, rows past the end read the last row, no branch
 // around a memory operation in the steady loop.  Each thread keeps the rotation (cos, sin) of
-// its pairs at the current row's position in double and advances it by S positions per row with
-// the rotation through S * freq_j (a double sincos, once per walk), so the state drifts ~1e-16
-// per step and is never evaluated again; where a walk crosses the end of a sequence, S is a
-// multiple or a divisor of rope_seq (rope_walk_ok: the host plans this kernel only then, or when
-// no walk reaches a sequence end), so the position returns to the walk's first one and the
-// rotation to its first value, kept.  The walk is bound by its vector instructions as much as by
-// HBM, so the row's decoded, rotated chunk stays in registers across the reduction, the weight
-// is decoded once, sums of products use fused multiply-adds, and for a power-of-two dim the mean
-// is s * (1 / dim), exact.
+// its pairs at the current row's position in float32 and advances it by S positions per row with
+// the rotation through S * freq_j (formed in double once per walk, rounded to float).  Where a
+// walk crosses the end of a sequence, S is a multiple or a divisor of rope_seq (rope_walk_ok: the
+// host plans this kernel only then, or when no walk reaches a sequence end), so the position
+// returns to the walk's first one and the rotation to its first value, kept; a walk that goes
+// kRopeAnchorRows rows without such a return evaluates its angles afresh (double angle, exact
+// reduction, float sincospi), so no state is more than kRopeAnchorRows - 1 float steps from an
+// exact value (about 3 * 2^-24 of the pair per step).  The row group is a whole number of
+// waves, so slots, rows and positions are wave-uniform and the walk's bookkeeping is scalar.  The
+// walk is bound by its vector instructions as much as by HBM, so the row's decoded, rotated chunk
+// stays in registers across the reduction, the weight is decoded once, sums of products use
+// fused multiply-adds, and for a power-of-two dim the mean is s * (1 / dim), exact.
 // ------------------------------------------------------------------------------------------
 template <int DT, int WDT>
 __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(const BwdArgs a) {
@@ -1208,14 +1211,15 @@ __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(c
   constexpr int P = V / 2;  // RoPE pairs per chunk
   constexpr int PF = vg_plan::kRingPrefetch;
   constexpr int R = PF + 1;
+  constexpr int kRopeAnchorRows = 16;
   __shared__ float red[2][kMaxWavesPerRow];
-  // Dynamic LDS: each thread's step rotations (P double pairs) and first rotations (P float
-  // pairs), pair-major so a wave reads consecutive 16- and 8-byte entries, then with several row
-  // groups dim floats for their combine (rope_ring_lds_bytes).
+  // Dynamic LDS: each thread's pair frequencies (P doubles), step rotations and first rotations
+  // (P float pairs each), pair-major so a wave reads consecutive 8-byte entries, then with
+  // several row groups dim floats for their combine (plan_bwd_rope_ring's lds_bytes).
   extern __shared__ __align__(16) float dyn_lds[];
 
   const int tpr = a.tpr;
-  const int grp = threadIdx.x / tpr;
+  const int grp = __builtin_amdgcn_readfirstlane((int)threadIdx.x / tpr);
   const int lt = threadIdx.x - grp * tpr;
   const int groups = blockDim.x / tpr;
   const int64_t slot = (int64_t)blockIdx.x * groups + grp;
@@ -1224,8 +1228,9 @@ __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(c
   const int64_t col = (int64_t)lt * V;
   const int64_t seq = a.rope_seq;
   const int64_t pos0 = slot % seq;
-  double2* step_lds = reinterpret_cast<double2*>(dyn_lds);               // [P][blockDim]
-  float2* first_lds = reinterpret_cast<float2*>(step_lds + P * blockDim.x);  // [P][blockDim]
+  double* freq_lds = reinterpret_cast<double*>(dyn_lds);                   // [P][blockDim]
+  float2* step_lds = reinterpret_cast<float2*>(freq_lds + P * blockDim.x);  // [P][blockDim]
+  float2* first_lds = step_lds + P * blockDim.x;                            // [P][blockDim]
   float* comb = reinterpret_cast<float*>(first_lds + P * blockDim.x);
   // 1 / dim is exact for a power of two, so s * (1 / dim) has the bits of s / dim
   const bool dim_pow2 = (a.dim & (a.dim - 1)) == 0;
@@ -1243,16 +1248,17 @@ __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(c
 #pragma unroll 1
   for (int q = 0; q < P; ++q) {
     const double f = rope_freq(lt * P + q, a.rope_c_hi, a.rope_c_lo);
+    freq_lds[q * blockDim.x + threadIdx.x] = f;
     double sv, cv;
     sincos((double)S * f, &sv, &cv);
-    step_lds[q * blockDim.x + threadIdx.x] = double2{cv, sv};
+    step_lds[q * blockDim.x + threadIdx.x] = float2{(float)cv, (float)sv};
     // the rotation at the walk's first position: double angle, reduced exactly, float sincospi
     const double rev = (double)pos0 * f * kInv2PiD;
     float s0, c0;
     sincospif(2.0f * (float)(rev - rint(rev)), &s0, &c0);
     first_lds[q * blockDim.x + threadIdx.x] = float2{c0, s0};
   }
-  double cr[P], sr[P];
+  float cr[P], sr[P];
 #pragma unroll
   for (int q = 0; q < P; ++q) {
     const float2 f0 = first_lds[q * blockDim.x + threadIdx.x];
@@ -1260,6 +1266,7 @@ __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(c
     sr[q] = f0.y;
   }
   int64_t pos = pos0;
+  int since = 0;  // float steps taken since the state was last exact
 
   u32x4 gr[R], hr[R];
   float rr[R];
@@ -1277,7 +1284,7 @@ __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(c
     // inverse rotation of each pair (y0, y1) -> (y0 c + y1 s, y1 c - y0 s)
 #pragma unroll
     for (int q = 0; q < P; ++q) {
-      const float c = (float)cr[q], sn = (float)sr[q];
+      const float c = cr[q], sn = sr[q];
       const float g0 = gf[2 * q], g1 = gf[2 * q + 1];
       gf[2 * q] = __builtin_fmaf(g0, c, g1 * sn);
       gf[2 * q + 1] = __builtin_fmaf(g1, c, -(g0 * sn));
@@ -1300,24 +1307,34 @@ __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(c
       // the row's sums are done here: its g and xhat are not held into the next row
       asm volatile("" : "+v"(acc[i]));
     }
-    // the next row's angles: S positions on, or the walk's first position again
-    // (each thread reads only the LDS entries it wrote, in program order: no barrier)
+    // the next row's angles: the walk's first position again, evaluated afresh after
+    // kRopeAnchorRows - 1 steps, or one float step of S positions on (each thread reads only the
+    // LDS entries it wrote, in program order: no barrier)
     pos += S;
-    if (pos < seq) {
-#pragma unroll
-      for (int q = 0; q < P; ++q) {
-        const double2 st = step_lds[q * blockDim.x + threadIdx.x];
-        const double cn = __builtin_fma(cr[q], st.x, -(sr[q] * st.y));
-        sr[q] = __builtin_fma(sr[q], st.x, cr[q] * st.y);
-        cr[q] = cn;
-      }
-    } else {
+    ++since;
+    if (pos >= seq) {
       pos = pos0;
+      since = 0;
 #pragma unroll
       for (int q = 0; q < P; ++q) {
         const float2 f0 = first_lds[q * blockDim.x + threadIdx.x];
         cr[q] = f0.x;
         sr[q] = f0.y;
+      }
+    } else if (since == kRopeAnchorRows) {
+      since = 0;
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const double rev = (double)pos * freq_lds[q * blockDim.x + threadIdx.x] * kInv2PiD;
+        sincospif(2.0f * (float)(rev - rint(rev)), &sr[q], &cr[q]);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const float2 st = step_lds[q * blockDim.x + threadIdx.x];
+        const float cn = __builtin_fmaf(cr[q], st.x, -(sr[q] * st.y));
+        sr[q] = __builtin_fmaf(sr[q], st.x, cr[q] * st.y);
+        cr[q] = cn;
       }
     }
   };
