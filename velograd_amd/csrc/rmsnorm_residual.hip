@@ -467,11 +467,13 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 // touch adjacent rows, one compact address front that HBM serves better than runs of
 // consecutive rows per workgroup (those spread the front over 16 rows per workgroup).  The next
 // rows' chunks are in flight while the current one reduces.  Each thread keeps the rotation
-// (cos, sin) of its pairs in double and advances it by G positions per step (the rotation
-// through G * freq_j, evaluated once per walk), so trigonometry runs only before the walk;
-// evaluated per (row, pair) it made the fused pass VALU-bound, no faster than two passes.  The
-// walk's first angle is the double pos * freq_j reduced exactly before a float sincospi (a few
-// float32 ulps), and so is the step's; the recurrence adds ~1e-16 per step.  Where a step crosses
+// (cos, sin) of its pairs (in double for fp32 outputs, in float32 for bf16/fp16 ones) and
+// advances it by G positions per step (the rotation through G * freq_j, evaluated once per walk),
+// so trigonometry runs only before the walk; evaluated per (row, pair) it made the fused pass
+// VALU-bound, no faster than two passes.  The walk's first angle is the double pos * freq_j
+// reduced exactly before a float sincospi (a few float32 ulps), and so is the step's; the
+// recurrence adds ~1e-16 per step in double, about 3 float32 ulps of the pair in float32, over
+// at most kNormRopeRows - 1 steps from an exact value.  Where a step crosses
 // the end of a sequence (row position = row % rope_seq) and G is a multiple or a divisor of
 // rope_seq, the position returns to the walk's first one and so does the rotation (kept); any
 // other crossing re-evaluates the angle at the new position.
@@ -527,7 +529,15 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
     wc.load((has_w && lane_ok) ? a.w : nullptr, col);
     wc.unpack(has_w, wf);
   }
-  double cr[PP], sr[PP], cst[PP], sst[PP];
+  // The rotation state: double for fp32 outputs; float32 for bf16/fp16 ones, whose walks of at
+  // most kNormRopeRows rows from an exact start stay within ~45 float32 ulps of the pair, far
+  // below their output's rounding.
+  using RotT = std::conditional_t<DT == VELOGRAD_DTYPE_F32, double, float>;
+  auto rot_fma = [](RotT x, RotT y, RotT z) {
+    if constexpr (DT == VELOGRAD_DTYPE_F32) return __builtin_fma(x, y, z);
+    else return __builtin_fmaf(x, y, z);
+  };
+  RotT cr[PP], sr[PP], cst[PP], sst[PP];
   float c0[PP], s0[PP];  // the rotation at pos0
   // the rotation at pos: double angle, reduced exactly, float sincospi
   auto rotation_at = [&](int64_t pos, int q, float& c, float& s) {
@@ -591,8 +601,8 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
     if (pos < seq) {
 #pragma unroll
       for (int q = 0; q < PP; ++q) {
-        const double cn = __builtin_fma(cr[q], cst[q], -(sr[q] * sst[q]));
-        sr[q] = __builtin_fma(sr[q], cst[q], cr[q] * sst[q]);
+        const RotT cn = rot_fma(cr[q], cst[q], -(sr[q] * sst[q]));
+        sr[q] = rot_fma(sr[q], cst[q], cr[q] * sst[q]);
         cr[q] = cn;
       }
     } else if (!decltype(anchor)::value || back_to_start) {
