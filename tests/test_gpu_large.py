@@ -63,6 +63,42 @@ def test_forward_backward_beyond_2_pow_31_elements(big):
     torch.cuda.synchronize()
 
 
+def test_dim_4096_beyond_2_pow_31_elements(big):
+    """The same tensors as 524294 rows of 4096: the forward that stores h after the row
+    reduction (rows of 512 threads) and the ring backward with two row groups per workgroup,
+    checked on the rows either side of the 2^31-element boundary (row 524288) and the last row,
+    and dweight over all rows against a float64 sum."""
+    x, res, w8 = big
+    rows, d = ROWS * D // 4096, 4096
+    check = [0, 1, 524287, 524288, 524289, rows - 1]
+    _say(f"large fwd/bwd {rows}x{d} bf16")
+    x4, r4 = x.view(rows, d), res.view(rows, d)
+    w = w8[:d].contiguous()
+    y, h, inv = vk.fused_rmsnorm_residual_forward(x4, r4, w, 1e-5)
+    w32 = P.upcast(w)
+    xs, rs = x4[check].float().cpu().numpy(), r4[check].float().cpu().numpy()
+    ry, rh, rinv = ora.fused_rmsnorm_residual_forward(xs, rs, w32, 1e-5)
+    P.assert_within_ulp(y[check], ry, 1, "y")
+    P.assert_within_ulp(h[check], rh, 0, "h")
+    assert P.rel_err(inv[check].float().cpu().numpy(), rinv) <= P.FP32_REL_TOL
+    del y
+
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    g = torch.randn(rows, d, device="cuda", dtype=torch.bfloat16, generator=gen)
+    dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True)
+    g32 = g[check].float().cpu().numpy()
+    h32 = h[check].float().cpu().numpy()
+    inv32 = inv[check].float().cpu().numpy()
+    rdx, _ = ora.backward_from_h(g32, h32, w32, inv32)
+    P.dx_check(dx[check], rdx, g32 * w32, h32 * inv32, inv32, "dx")
+    ref = torch.zeros(d, dtype=torch.float64, device="cuda")
+    for r0 in range(0, rows, 32768):
+        sl = slice(r0, min(rows, r0 + 32768))
+        ref += (g[sl].double() * (h[sl].double() * inv[sl].double())).sum(0)
+    P.assert_dweight(dw.double().cpu().numpy(), ref.cpu().numpy())
+    torch.cuda.synchronize()
+
+
 def test_norm_rope_backward_beyond_2_pow_31_elements(big):
     """The one-pass norm + RoPE backward over one sequence of 262147 positions: dx on the rows
     next to the 2^31-element boundary against the oracle composition at their positions (the
