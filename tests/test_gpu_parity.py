@@ -288,6 +288,43 @@ def test_broadcast_residual_row():
     assert np.array_equal(P.upcast(h), rh) and P.rel_err(P.upcast(y), ry) <= P.FP32_REL_TOL
 
 
+def test_one_dimensional_inputs():
+    """A single row given as a 1-D vector, as NumPy's axis=-1 reductions allow (fused.py:41-42,
+    59-65): y and h shaped like x, inv_rms of shape (1,), dx like grad_y, dweight [D]; the
+    array-like wrapper returns a 1-D float32 ndarray."""
+    rng = np.random.default_rng(31)
+    for d, dtype in ((4096, torch.bfloat16), (1000, torch.float32), (7, torch.float32)):
+        x32, r32, g32 = (P.gaussian(rng, (d,)) for _ in range(3))
+        w32 = P.weight_vec(rng, d)
+        x, r, w, g = (P.to_device(a, dtype) for a in (x32, r32, w32, g32))
+        y, h, inv = vk.fused_rmsnorm_residual_forward(x, r, w, 1e-5)
+        assert y.shape == (d,) and h.shape == (d,) and inv.shape == (1,)
+        ry, rh, rinv = ora.fused_rmsnorm_residual_forward(P.upcast(x), P.upcast(r), P.upcast(w),
+                                                          1e-5)
+        assert rinv.shape == (1,)
+        if dtype == torch.float32:
+            assert np.array_equal(P.upcast(h), rh)
+            assert P.rel_err(P.upcast(y), ry) <= P.FP32_REL_TOL
+        else:
+            P.assert_within_ulp(h, rh, 0, f"1-D h d={d}")
+            P.assert_within_ulp(y, ry, 1, f"1-D y d={d}")
+        assert P.rel_err(P.upcast(inv), rinv) <= P.FP32_REL_TOL
+        dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True)
+        assert dx.shape == (d,) and dw.shape == (d,) and dw.dtype == torch.float32
+        g2, w2 = P.upcast(g).reshape(1, d), P.upcast(w)
+        xhat = P.upcast(h).reshape(1, d) * P.upcast(inv).reshape(1, 1)
+        rdx, rdw = ora.fused_rmsnorm_residual_backward(g2, xhat, w2, P.upcast(inv).reshape(1, 1))
+        if dtype == torch.float32:
+            P.assert_dx_fp32(dx.view(1, d), rdx, g2 * w2, xhat, P.upcast(inv).reshape(1, 1))
+        else:
+            P.dx_check(dx.view(1, d), rdx, g2 * w2, xhat, P.upcast(inv).reshape(1, 1),
+                       f"1-D dx d={d}")
+        P.assert_dweight(P.upcast(dw), rdw, f"1-D dweight d={d}")
+    out = vk.fused_rmsnorm_residual(x32, r32, w32, eps=1e-5)
+    assert isinstance(out, np.ndarray) and out.shape == (7,) and out.dtype == np.float32
+    assert P.rel_err(out, ora.fused_rmsnorm_residual(x32, r32, w32, eps=1e-5)) <= P.FP32_REL_TOL
+
+
 def test_empty_inputs():
     x = torch.empty(0, 4096, device="cuda", dtype=torch.bfloat16)
     w = torch.ones(4096, device="cuda", dtype=torch.bfloat16)
