@@ -4,6 +4,7 @@
 //   * the register-resident plan covers every 16-byte chunk of a row exactly once, with whole
 //     wave64s per row, and its workgroup fits the kernel's launch bound for that NV;
 //   * the backward's workgroups, LDS and partial rows fit the workspace the size query reports.
+#include <algorithm>
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -140,7 +141,8 @@ int main() {
                     CHECK(!ring_eligible(rg.rp, dim, eb), "eligible ring plan refused");
                   }
                   // the ring-pipelined plan with the fused RoPE gradient: whole rows of one
-                  // chunk per thread, at most kRopeRingWgsPerCu workgroups per CU, its tables
+                  // chunk per thread, one workgroup per CU for 512-thread workgroups and two
+                  // for smaller ones (or as many as there are row groups' rows), its tables
                   // and combine within 64 KiB of LDS, its partials within the workspace
                   const BwdPlan rr = plan_bwd_rope_ring(rows, dim, eb, aligned != 0, cus);
                   if (rr.ring) {
@@ -150,9 +152,11 @@ int main() {
                               rr.rp.block <= kRingBlock,
                           "rope ring nv %d tpr %d block %d dim=%lld", rr.rp.nv, rr.rp.tpr,
                           rr.rp.block, (long long)dim);
-                    CHECK(rr.wgs >= 1 && rr.wgs <= (int64_t)cus * kRopeRingWgsPerCu &&
-                              rr.wgs <= (rows + rr.rp.groups - 1) / rr.rp.groups,
-                          "rope ring wgs=%lld", (long long)rr.wgs);
+                    const int64_t per_cu = rr.rp.block == kRingBlock ? 1 : 2;
+                    const int64_t need = (rows + rr.rp.groups - 1) / rr.rp.groups;
+                    CHECK(rr.wgs == std::min<int64_t>((int64_t)(cus > 0 ? cus : 1) * per_cu, need) &&
+                              rr.wgs <= (int64_t)cus * kRopeRingMaxWgsPerCu,
+                          "rope ring wgs=%lld block %d", (long long)rr.wgs, rr.rp.block);
                     CHECK((size_t)rr.wgs * (size_t)dim * sizeof(float) <= ws,
                           "rope ring partials %lld x %lld exceed workspace %zu",
                           (long long)rr.wgs, (long long)dim, ws);

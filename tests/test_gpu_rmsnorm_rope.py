@@ -189,13 +189,15 @@ BWD_CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 81
              (torch.float32, (3, 33, 1000), True), (torch.float16, (2, 50, 256), False),
              (torch.bfloat16, (3, 5, 6), True), (torch.float32, (4, 2, 3, 40), True),
              (torch.bfloat16, (1, 16384, 4096), True), (torch.bfloat16, (8, 2048, 4096), True),
-             # the ring kernel (bwd_rope_ring_kernel): fp32 with two row groups per workgroup
-             # and a 16-row walk; fp16 with eight row groups and no weight, one row per slot;
-             # four row groups, a partial last iteration and a return to the walk's first
-             # position on every row; two row groups returning on every row.  Then a shape whose
-             # walks cross sequence ends at other positions: bwd_vec_kernel's re-evaluating walk
+             # the ring kernel (bwd_rope_ring_kernel, one 512-thread workgroup per CU): fp32
+             # with two row groups per workgroup and a 32-row walk; fp16 with eight row groups
+             # and no weight, one or two rows per slot; four row groups, a partial last
+             # iteration and a return to the walk's first position on every row; two row groups
+             # returning on every second row; 384-thread workgroups, two per CU.  Then a shape
+             # whose walks cross sequence ends at other positions: bwd_vec_kernel's walk
              (torch.float32, (4, 4096, 1024), True), (torch.float16, (3, 1000, 512), False),
              (torch.bfloat16, (257, 64, 1024), True), (torch.bfloat16, (8, 1024, 2048), True),
+             (torch.bfloat16, (2, 1024, 3072), True),
              (torch.bfloat16, (6, 1000, 4096), True)]
 
 
@@ -246,9 +248,9 @@ def test_fused_backward_long_fp32_walk():
                                          (torch.float32, 65536, 2048)])
 def test_fused_backward_long_ring_walk(dtype, seq, d):
     """The ring kernel (rows of 512 chunks: bf16 dim 4096, fp32 dim 2048) over one sequence of
-    seq positions: each of its 512 slots walks seq / 512 rows (256, 128) with no position wrap,
-    re-evaluating its rotations every 16 rows; rows at the start, middle and end of the walks
-    keep the 2^-18 recurrence bound."""
+    seq positions: each of its 256 slots (one workgroup per CU) walks seq / 256 rows (512, 256)
+    with no position wrap, re-evaluating its rotations every 16 rows; rows at the start, middle
+    and end of the walks keep the 2^-18 recurrence bound."""
     base = 500000.0
     print(f"rmsnorm_rope backward ring long walk: {dtype} seq={seq} dim={d}", flush=True)
     gen = torch.Generator(device="cuda").manual_seed(13)

@@ -212,10 +212,21 @@ inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool ali
 
 // The ring-pipelined backward with the fused RoPE gradient (bwd_rope_ring_kernel): whole rows
 // of one 16-byte chunk per thread (its rotation state and tables keep it at 128 VGPRs), row
-// groups packed into workgroups of kRingBlock threads, kRopeRingWgsPerCu workgroups per CU.
-// `ring` is false when the row layout does not suit it.  The kernel also needs every slot's walk
-// to advance by the slot count or return to its first position (rope_walk_ok).
-constexpr int kRopeRingWgsPerCu = 2;
+// groups packed into workgroups of up to kRingBlock threads, rope_ring_wgs_per_cu of them per
+// CU.  `ring` is false when the row layout does not suit it.  The kernel also needs every slot's
+// walk to advance by the slot count or return to its first position (rope_walk_ok).
+constexpr int kRopeRingMaxWgsPerCu = 2;
+
+// One workgroup per CU when it fills kRingBlock threads (eight waves), else two (a 320- to
+// 448-thread workgroup alone would leave the CU five to seven waves).  Measured on MI355X (bf16,
+// A/B in one process, 4 rounds): one 512-thread workgroup per CU against two runs 16384 x 4096 in
+// 71.8 us against 79.0 (and 72.0 against 79.2 as 8 sequences of 2048), 8192 x 4096 in 41.7
+// against 45.1 and 32768 x 2048 in 71.8 against 77.6 (half the partial rows, and twice as many
+// rows per walk over the same resident waves); 384-thread workgroups (16384 x 3072) run 61.5 us
+// two per CU against 63.4 alone.
+inline int rope_ring_wgs_per_cu(int block) {
+  return block >= kRingBlock ? 1 : kRopeRingMaxWgsPerCu;
+}
 
 inline BwdPlan plan_bwd_rope_ring(int64_t rows, int64_t dim, int elem_bytes, bool aligned,
                                   int cus) {
@@ -235,7 +246,7 @@ inline BwdPlan plan_bwd_rope_ring(int64_t rows, int64_t dim, int elem_bytes, boo
   p.groups = kRingBlock / p.tpr;
   p.block = p.tpr * p.groups;
   const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
-  int64_t wgs = (int64_t)(cus > 0 ? cus : 1) * kRopeRingWgsPerCu;
+  int64_t wgs = (int64_t)(cus > 0 ? cus : 1) * rope_ring_wgs_per_cu(p.block);
   if (wgs > wgs_needed) wgs = wgs_needed;
   b.wgs = wgs;
   // per thread and pair of its chunk (V / 2 pairs): the double frequency and the float step and

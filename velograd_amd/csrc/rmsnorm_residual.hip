@@ -24,9 +24,10 @@
 //                       in flight while one reduces) in a branch-free steady loop, 512-thread
 //                       workgroups, one per CU: the backward's default where the rows suit it.
 //   fwd_rope_kernel     the forward with the model's interleaved RoPE on y: strided row walks
-//                       with the rotation advanced by a double recurrence.
+//                       with the rotation advanced by a recurrence.
 //   bwd_rope_ring_kernel  its backward (grad_y rotated back, then the norm's backward) in
-//                       bwd_ring_kernel's walk, one chunk per thread, two workgroups per CU;
+//                       bwd_ring_kernel's walk, one chunk per thread, one 512-thread workgroup
+//                       per CU (two of a smaller size);
 //                       bwd_vec_kernel with kRopeG where the rows or positions do not suit it.
 //   dweight_reduce      stage 2: sums the partial rows in a fixed order -> dweight[dim].
 //   *_generic_kernel    any dim and any alignment: the same arithmetic with scalar accesses.
