@@ -82,8 +82,9 @@ int main() {
   }
   // Backward plans and the workspace query, on the dims the benchmarks and tests use plus a
   // spread of others, for every tuning knob value range.
-  const int64_t dims[] = {1, 4, 13, 16, 64, 100, 512, 768, 1024, 2048, 4096, 4104, 5120, 7168,
-                          8192, 16384, 20000, 40000};
+  const int64_t dims[] = {1,    4,    13,   16,   64,    100,   512,   768,  1024, 2048,
+                          2560, 3072, 4096, 4104, 5120,  6144,  7168,  8192, 9216, 16384,
+                          20000, 40000};
   for (int64_t dim : dims) {
     for (int64_t rows : rows_list) {
       for (int cus : cus_list) {
@@ -141,18 +142,21 @@ int main() {
                     CHECK(!ring_eligible(rg.rp, dim, eb), "eligible ring plan refused");
                   }
                   // the ring-pipelined plan with the fused RoPE gradient: whole rows of one
-                  // chunk per thread, one workgroup per CU for 512-thread workgroups and two
-                  // for smaller ones (or as many as there are row groups' rows), its tables
-                  // and combine within 64 KiB of LDS, its partials within the workspace
+                  // chunk per thread (two for rows of 513 to 1024 chunks), one workgroup per
+                  // CU, two for one chunk per thread in workgroups under 512 threads (or as
+                  // many as there are row groups' rows), its tables and combine within 64 KiB
+                  // of LDS, its partials within the workspace
                   const BwdPlan rr = plan_bwd_rope_ring(rows, dim, eb, aligned != 0, cus);
                   if (rr.ring) {
                     check_row_plan(rr.rp, dim, eb, aligned != 0);
                     CHECK(rope_ring_eligible(rr.rp, dim, eb), "rope ring plan not eligible");
-                    CHECK(rr.rp.nv == 1 && (int64_t)rr.rp.tpr * (16 / eb) == dim &&
+                    const int64_t chunks = dim / (16 / eb);
+                    CHECK(rr.rp.nv == (chunks <= kRingBlock ? 1 : 2) &&
+                              (int64_t)rr.rp.nv * rr.rp.tpr * (16 / eb) == dim &&
                               rr.rp.block <= kRingBlock,
                           "rope ring nv %d tpr %d block %d dim=%lld", rr.rp.nv, rr.rp.tpr,
                           rr.rp.block, (long long)dim);
-                    const int64_t per_cu = rr.rp.block == kRingBlock ? 1 : 2;
+                    const int64_t per_cu = rr.rp.nv == 1 && rr.rp.block < kRingBlock ? 2 : 1;
                     const int64_t need = (rows + rr.rp.groups - 1) / rr.rp.groups;
                     CHECK(rr.wgs == std::min<int64_t>((int64_t)(cus > 0 ? cus : 1) * per_cu, need) &&
                               rr.wgs <= (int64_t)cus * kRopeRingMaxWgsPerCu,
@@ -160,13 +164,17 @@ int main() {
                     CHECK((size_t)rr.wgs * (size_t)dim * sizeof(float) <= ws,
                           "rope ring partials %lld x %lld exceed workspace %zu",
                           (long long)rr.wgs, (long long)dim, ws);
-                    const size_t tables = (size_t)rr.rp.block * (16 / eb / 2) * 24;
+                    const size_t tables = rr.rp.nv == 1
+                                              ? (size_t)rr.rp.block * (16 / eb / 2) * 24
+                                              : (size_t)rr.rp.block * (16 / eb) * 8;
                     CHECK(rr.lds_bytes <= 64 * 1024 &&
                               rr.lds_bytes == tables + (rr.rp.groups > 1 ? dim * 4 : 0),
                           "rope ring lds %zu", rr.lds_bytes);
                   } else {
                     CHECK(!(aligned && eb == 2 && dim % 512 == 0 && dim <= 4096) &&
-                              !(aligned && eb == 4 && dim % 256 == 0 && dim <= 2048),
+                              !(aligned && eb == 4 && dim % 256 == 0 && dim <= 2048) &&
+                              !(aligned && eb == 2 && dim % 1024 == 0 && dim <= 8192) &&
+                              !(aligned && eb == 4 && dim % 512 == 0 && dim <= 4096),
                           "rope ring plan refused dim=%lld eb=%d", (long long)dim, eb);
                   }
                   ++plans;

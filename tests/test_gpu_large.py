@@ -99,42 +99,41 @@ def test_dim_4096_beyond_2_pow_31_elements(big):
     torch.cuda.synchronize()
 
 
-def test_norm_rope_backward_beyond_2_pow_31_elements(big):
-    """The one-pass norm + RoPE backward over one sequence of 262147 positions: dx on the rows
-    next to the 2^31-element boundary against the oracle composition at their positions (the
-    rotation's inverse, then the module backward, both float64), the full dweight against a
-    float64 sum of (rotated-back g) * xhat computed by torch on the device in row blocks, with
-    the angles pos * base^(-2i/dim) in float64 (functional.py:302-303, 316-345)."""
-    x, _, w = big
-    _say(f"large norm+rope backward {ROWS}x{D} bf16")
-    x3 = x.view(1, ROWS, D)
+def _check_norm_rope_backward_large(x3, w, check, seed):
+    """The one-pass norm + RoPE backward over x3 = [1, rows, dim] (one sequence): dx on the `check`
+    rows against the oracle composition at their positions (the rotation's inverse, then the
+    module backward, both float64), the full dweight against a float64 sum of (rotated-back g) *
+    xhat computed by torch on the device in row blocks, with the angles pos * base^(-2i/dim) in
+    float64 (functional.py:302-303, 316-345)."""
+    rows, d = x3.shape[1], x3.shape[2]
     _, h, inv = vk.rmsnorm_rope_forward(x3, w, 1e-6, 10000.0)
-    gen = torch.Generator(device="cuda").manual_seed(2)
-    g = torch.randn(1, ROWS, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    g = torch.randn(1, rows, d, device="cuda", dtype=torch.bfloat16, generator=gen)
     dx, dw = vk.rmsnorm_rope_backward(g, h, w, inv, 10000.0)
-    rows = np.array(CHECK_ROWS)
-    g64 = g[0, CHECK_ROWS].double().cpu().numpy()
-    h64 = h[0, CHECK_ROWS].double().cpu().numpy()
-    r64 = inv[0, CHECK_ROWS].double().cpu().numpy()
+    pos = np.array(check)
+    g64 = g[0, check].double().cpu().numpy()
+    h64 = h[0, check].double().cpu().numpy()
+    r64 = inv[0, check].double().cpu().numpy()
     w64 = P.upcast(w).astype(np.float64)
-    gn = ora.apply_rotary_emb(g64, 10000.0, inverse=True, positions=rows)
+    gn = ora.apply_rotary_emb(g64, 10000.0, inverse=True, positions=pos)
     rdx, _ = ora.rmsnorm_module_backward(gn, h64, w64, r64)
     # angles in double: 16 float32 ulps of the pair at any position, plus 2^-18 for the float32
-    # rotation recurrence (8192-wide rows take bwd_vec_kernel's walk, which evaluates the
-    # rotation afresh every 16 rows however long the walk)
+    # rotation recurrence of the backward walks, which evaluate the rotation afresh every 16 rows
+    # however long the walk
     dg = np.repeat((P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -18)
                    * (np.abs(g64[:, 0::2]) + np.abs(g64[:, 1::2])), 2, axis=1)
     xhat = h64 * r64
     tol = r64 * (np.abs(w64) * dg + np.abs(xhat) * np.mean(np.abs(w64 * xhat) * dg, axis=-1,
                                                            keepdims=True))
     tol += P.DX_FLOOR * P.dx_scale(gn * w64, xhat, r64) + 2.0 ** -8 * np.abs(rdx)
-    err = np.abs(dx[0, CHECK_ROWS].double().cpu().numpy() - rdx)
+    err = np.abs(dx[0, check].double().cpu().numpy() - rdx)
     assert np.all(err <= tol), float((err - tol).max())
     del dx
-    ref = torch.zeros(D, dtype=torch.float64, device="cuda")
-    inv_freq = 10000.0 ** (-torch.arange(0, D, 2, dtype=torch.float64, device="cuda") / D)
-    for r0 in range(0, ROWS, 16384):
-        r1 = min(ROWS, r0 + 16384)
+    ref = torch.zeros(d, dtype=torch.float64, device="cuda")
+    inv_freq = 10000.0 ** (-torch.arange(0, d, 2, dtype=torch.float64, device="cuda") / d)
+    step = (1 << 27) // d
+    for r0 in range(0, rows, step):
+        r1 = min(rows, r0 + step)
         ang = torch.arange(r0, r1, dtype=torch.float64, device="cuda")[:, None] * inv_freq
         c, sn = torch.cos(ang), torch.sin(ang)
         gb = g[0, r0:r1].double()
@@ -145,6 +144,30 @@ def test_norm_rope_backward_beyond_2_pow_31_elements(big):
     P.assert_dweight(dw.double().cpu().numpy(), ref.cpu().numpy())
     del g
     torch.cuda.synchronize()
+
+
+def test_norm_rope_backward_beyond_2_pow_31_elements(big):
+    """One sequence of 262147 positions at dim 8192: its walks cross the sequence end away from
+    their first position, so bwd_vec_kernel's re-evaluating walk runs."""
+    x, _, w = big
+    _say(f"large norm+rope backward {ROWS}x{D} bf16")
+    _check_norm_rope_backward_large(x.view(1, ROWS, D), w, CHECK_ROWS, 2)
+
+
+@pytest.mark.parametrize("rows,d", [(262400, 8192), (524544, 4096)])
+def test_norm_rope_ring_backward_beyond_2_pow_31_elements(rows, d):
+    """The ring kernel (two chunks per thread at dim 8192, one at 4096) over one sequence whose
+    length is a multiple of its 256 slots, past 2^31 elements: rows either side of the boundary
+    (2^31 / dim) and the last rows."""
+    assert rows * d > 2 ** 31
+    _say(f"large norm+rope ring backward {rows}x{d} bf16")
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(1, rows, d, device="cuda", dtype=torch.bfloat16, generator=gen)
+    w = (1 + 0.1 * torch.randn(d, device="cuda", generator=gen)).to(torch.bfloat16)
+    b = 2 ** 31 // d
+    _check_norm_rope_backward_large(x, w, [0, 1, b - 1, b, b + 1, rows - 1], 6)
+    del x
+    torch.cuda.empty_cache()
 
 
 def test_quantised_forwards_beyond_2_pow_31_bytes(big):

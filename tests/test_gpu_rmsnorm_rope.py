@@ -198,7 +198,12 @@ BWD_CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 81
              (torch.float32, (4, 4096, 1024), True), (torch.float16, (3, 1000, 512), False),
              (torch.bfloat16, (257, 64, 1024), True), (torch.bfloat16, (8, 1024, 2048), True),
              (torch.bfloat16, (2, 1024, 3072), True),
-             (torch.bfloat16, (6, 1000, 4096), True)]
+             # two chunks per thread (rows of 513 to 1024 chunks): 320-, 448- and 512-thread
+             # row groups, fp32 and bf16; then the same widths where walks cross sequence ends
+             # elsewhere (bwd_vec_kernel)
+             (torch.bfloat16, (2, 1024, 5120), True), (torch.bfloat16, (4, 512, 7168), False),
+             (torch.float32, (2, 1024, 2560), True), (torch.float32, (1, 4096, 4096), True),
+             (torch.bfloat16, (6, 1000, 4096), True), (torch.bfloat16, (3, 1000, 8192), True)]
 
 
 @pytest.mark.parametrize("dtype,shape,with_w", BWD_CASES,
@@ -223,10 +228,11 @@ def test_fused_backward_matches_the_oracle_composition(dtype, shape, with_w, bas
 
 
 def test_fused_backward_long_fp32_walk():
-    """fp32, one sequence of 131072 positions at dim 4096: one 1024-thread row group per
-    workgroup, so each of the 256 slots walks 512 rows of one sequence with no position wrap.
-    The rotation state is re-evaluated every 16 rows, so the last rows of the walks (and the
-    middle ones) keep the same 2^-18 recurrence bound as short walks."""
+    """fp32, one sequence of 131072 positions at dim 4096: the ring kernel with two chunks per
+    thread (512-thread row groups, one per CU), so each of the 256 slots walks 512 rows of one
+    sequence with no position wrap. The rotation state is re-evaluated every 16 rows, so the last
+    rows of the walks (and the middle ones) keep the same 2^-18 recurrence bound as short
+    walks."""
     seq, d, base = 131072, 4096, 500000.0
     print(f"rmsnorm_rope backward fp32 long walk: seq={seq} dim={d}", flush=True)
     gen = torch.Generator(device="cuda").manual_seed(11)

@@ -211,21 +211,23 @@ inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool ali
 }
 
 // The ring-pipelined backward with the fused RoPE gradient (bwd_rope_ring_kernel): whole rows
-// of one 16-byte chunk per thread (its rotation state and tables keep it at 128 VGPRs), row
-// groups packed into workgroups of up to kRingBlock threads, rope_ring_wgs_per_cu of them per
-// CU.  `ring` is false when the row layout does not suit it.  The kernel also needs every slot's
-// walk to advance by the slot count or return to its first position (rope_walk_ok).
+// of one 16-byte chunk per thread where a row has at most kRingBlock chunks (its rotation state
+// and tables keep it at 128 VGPRs), else of two (rows of up to 2 * kRingBlock chunks; 256
+// VGPRs), row groups packed into workgroups of up to kRingBlock threads, rope_ring_wgs_per_cu of
+// them per CU.  `ring` is false when the row layout does not suit it.  The kernel also needs every
+// slot's walk to advance by the slot count or return to its first position (rope_walk_ok).
 constexpr int kRopeRingMaxWgsPerCu = 2;
 
-// One workgroup per CU when it fills kRingBlock threads (eight waves), else two (a 320- to
-// 448-thread workgroup alone would leave the CU five to seven waves).  Measured on MI355X (bf16,
-// A/B in one process, 4 rounds): one 512-thread workgroup per CU against two runs 16384 x 4096 in
-// 71.8 us against 79.0 (and 72.0 against 79.2 as 8 sequences of 2048), 8192 x 4096 in 41.7
-// against 45.1 and 32768 x 2048 in 71.8 against 77.6 (half the partial rows, and twice as many
-// rows per walk over the same resident waves); 384-thread workgroups (16384 x 3072) run 61.5 us
-// two per CU against 63.4 alone.
-inline int rope_ring_wgs_per_cu(int block) {
-  return block >= kRingBlock ? 1 : kRopeRingMaxWgsPerCu;
+// One chunk per thread: one workgroup per CU when it fills kRingBlock threads (eight waves),
+// else two (a 320- to 448-thread workgroup alone would leave the CU five to seven waves).
+// Measured on MI355X (bf16, A/B in one process, 4 rounds): one 512-thread workgroup per CU
+// against two runs 16384 x 4096 in 71.8 us against 79.0 (and 72.0 against 79.2 as 8 sequences of
+// 2048), 8192 x 4096 in 41.7 against 45.1 and 32768 x 2048 in 71.8 against 77.6 (half the partial
+// rows, and twice as many rows per walk over the same resident waves); 384-thread workgroups
+// (16384 x 3072) run 61.5 us two per CU against 63.4 alone.  Two chunks per thread hold up to
+// 256 VGPRs, so one workgroup per CU.
+inline int rope_ring_wgs_per_cu(int nv, int block) {
+  return nv == 1 && block < kRingBlock ? kRopeRingMaxWgsPerCu : 1;
 }
 
 inline BwdPlan plan_bwd_rope_ring(int64_t rows, int64_t dim, int elem_bytes, bool aligned,
@@ -238,21 +240,24 @@ inline BwdPlan plan_bwd_rope_ring(int64_t rows, int64_t dim, int elem_bytes, boo
   const int V = 16 / elem_bytes;
   if (dim % V != 0) return b;
   const int64_t chunks = dim / V;
-  if (chunks % kWave != 0 || chunks > kRingBlock) return b;
+  const int nv = chunks <= kRingBlock ? 1 : 2;
+  if (chunks % ((int64_t)nv * kWave) != 0 || chunks > (int64_t)nv * kRingBlock) return b;
   RowPlan& p = b.rp;
   p.vec = true;
-  p.nv = 1;
-  p.tpr = (int)chunks;
+  p.nv = nv;
+  p.tpr = (int)(chunks / nv);
   p.groups = kRingBlock / p.tpr;
   p.block = p.tpr * p.groups;
   const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
-  int64_t wgs = (int64_t)(cus > 0 ? cus : 1) * rope_ring_wgs_per_cu(p.block);
+  int64_t wgs = (int64_t)(cus > 0 ? cus : 1) * rope_ring_wgs_per_cu(nv, p.block);
   if (wgs > wgs_needed) wgs = wgs_needed;
   b.wgs = wgs;
-  // per thread and pair of its chunk (V / 2 pairs): the double frequency and the float step and
-  // first rotations, 24 bytes; then, with several row groups, their dweight combine
-  const int pairs = V / 2;
-  b.lds_bytes = (size_t)p.block * pairs * (sizeof(double) + 4 * sizeof(float)) +
+  // per thread and pair (V / 2 pairs a chunk): with one chunk the double frequency and the float
+  // step and first rotations, 24 bytes; with two the float step rotation, 8 bytes; then, with
+  // several row groups, their dweight combine
+  const int pairs = nv * (V / 2);
+  const size_t per_pair = nv == 1 ? sizeof(double) + 4 * sizeof(float) : 2 * sizeof(float);
+  b.lds_bytes = (size_t)p.block * pairs * per_pair +
                 (p.groups > 1 ? (size_t)dim * sizeof(float) : 0);
   b.ring = true;
   return b;
@@ -271,8 +276,9 @@ inline bool rope_walk_ok(int64_t rows, int64_t slots, int64_t seq) {
 // Whether a plan suits bwd_rope_ring_kernel (the facts its indexing relies on).
 inline bool rope_ring_eligible(const RowPlan& p, int64_t dim, int elem_bytes) {
   if (!p.vec || (elem_bytes != 2 && elem_bytes != 4)) return false;
-  return p.nv == 1 && p.tpr % kWave == 0 && (int64_t)p.tpr * (16 / elem_bytes) == dim &&
-         p.block == p.tpr * p.groups && p.block <= kRingBlock;
+  return (p.nv == 1 || p.nv == 2) && p.tpr % kWave == 0 &&
+         (int64_t)p.nv * p.tpr * (16 / elem_bytes) == dim && p.block == p.tpr * p.groups &&
+         p.block <= kRingBlock;
 }
 
 // Backward plan with the fused inverse RoPE: the same layout under max_block_for_nv_rope, or the

@@ -26,8 +26,9 @@
 //   fwd_rope_kernel     the forward with the model's interleaved RoPE on y: strided row walks
 //                       with the rotation advanced by a recurrence.
 //   bwd_rope_ring_kernel  its backward (grad_y rotated back, then the norm's backward) in
-//                       bwd_ring_kernel's walk, one chunk per thread, one 512-thread workgroup
-//                       per CU (two of a smaller size);
+//                       bwd_ring_kernel's walk, one or two chunks per thread (rows of up to
+//                       1024 chunks), one workgroup per CU (two of one chunk and under 512
+//                       threads);
 //                       bwd_vec_kernel with kRopeG where the rows or positions do not suit it.
 //   dweight_reduce      stage 2: sums the partial rows in a fixed order -> dweight[dim].
 //   *_generic_kernel    any dim and any alignment: the same arithmetic with scalar accesses.
@@ -1198,7 +1199,7 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
 
 // ------------------------------------------------------------------------------------------
 // Backward with the fused RoPE gradient, ring-pipelined (launch_plan.h: plan_bwd_rope_ring):
-// whole rows of one 16-byte chunk per thread, the saved tensor h, no grad_h or dres (the
+// whole rows of NV (1 or 2) 16-byte chunks per thread, the saved tensor h, no grad_h or dres (the
 // module's backward).  The walk, ring and steady loop are bwd_ring_kernel's: slot s walks rows
 // s, s + S, ... (S slots), three row buffers, rows past the end read the last row, no branch
 // around a memory operation in the steady loop.  Each thread keeps the rotation (cos, sin) of
@@ -1206,27 +1207,38 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
 // the rotation through S * freq_j (formed in double once per walk, rounded to float).  Where a
 // walk crosses the end of a sequence, S is a multiple or a divisor of rope_seq (rope_walk_ok: the
 // host plans this kernel only then, or when no walk reaches a sequence end), so the position
-// returns to the walk's first one and the rotation to its first value, kept; a walk that goes
-// kRopeAnchorRows rows without such a return evaluates its angles afresh (double angle, exact
-// reduction, float sincospi), so no state is more than kRopeAnchorRows - 1 float steps from an
-// exact value (about 3 * 2^-24 of the pair per step).  The row group is a whole number of
-// waves, so slots, rows and positions are wave-uniform and the walk's bookkeeping is scalar.  The
-// walk is bound by its vector instructions as much as by HBM, so the row's decoded, rotated chunk
-// stays in registers across the reduction, the weight is decoded once, sums of products use
-// fused multiply-adds, and for a power-of-two dim the mean is s * (1 / dim), exact.
+// returns to the walk's first one and the rotation to its first value (kept in LDS with one
+// chunk per thread, evaluated afresh with two); a walk that goes kRopeAnchorRows rows without
+// such a return evaluates its angles afresh (double angle, exact reduction, float sincospi), so
+// no state is more than kRopeAnchorRows - 1 float steps from an exact value (about 3 * 2^-24 of
+// the pair per step).  The row group is a whole number of waves, so slots, rows and positions are
+// wave-uniform and the walk's bookkeeping is scalar.  The walk is bound by its vector
+// instructions as much as by HBM, so the row's decoded, rotated chunks stay in registers across
+// the reduction, the weight is decoded once, sums of products use fused multiply-adds, and for a
+// power-of-two dim the mean is s * (1 / dim), exact.  One chunk per thread runs within 128 VGPRs
+// (two workgroups of fewer than 512 threads fit a CU); two chunks per thread, one workgroup per
+// CU, within 256.
 // ------------------------------------------------------------------------------------------
-template <int DT, int WDT>
-__global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(const BwdArgs a) {
+template <int DT, int WDT, int NV>
+__global__ __launch_bounds__(vg_plan::kRingBlock, NV == 1 ? 4 : 2) void bwd_rope_ring_kernel(
+    const BwdArgs a) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
-  constexpr int P = V / 2;  // RoPE pairs per chunk
+  constexpr int P = V / 2;    // RoPE pairs per chunk
+  constexpr int NP = NV * P;  // RoPE pairs per thread: pair e = k * P + q of chunk lt + k * tpr
+  // One chunk per thread keeps its pair frequencies and first rotations in LDS; with two, they
+  // would not fit 64 KiB beside the step rotations, so the frequencies are formed again where
+  // the angles are evaluated and the first rotation is evaluated afresh at a return.
+  constexpr bool kTablesInLds = NV == 1;
   constexpr int PF = vg_plan::kRingPrefetch;
   constexpr int R = PF + 1;
   constexpr int kRopeAnchorRows = 16;
+  static_assert(NV == 1 || NV == 2, "the RoPE ring takes one or two chunks per thread");
   __shared__ float red[2][kMaxWavesPerRow];
-  // Dynamic LDS: each thread's pair frequencies (P doubles), step rotations and first rotations
-  // (P float pairs each), pair-major so a wave reads consecutive 8-byte entries, then with
-  // several row groups dim floats for their combine (plan_bwd_rope_ring's lds_bytes).
+  // Dynamic LDS, pair-major so a wave reads consecutive 8-byte entries: with one chunk per thread
+  // each thread's pair frequencies (doubles), then step and first rotations (float pairs); with
+  // two, the step rotations only; then with several row groups dim floats for their combine
+  // (plan_bwd_rope_ring's lds_bytes).
   extern __shared__ __align__(16) float dyn_lds[];
 
   const int tpr = a.tpr;
@@ -1236,87 +1248,122 @@ __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(c
   const int64_t slot = (int64_t)blockIdx.x * groups + grp;
   const int64_t S = (int64_t)gridDim.x * groups;
   const int64_t last = a.rows - 1;
-  const int64_t col = (int64_t)lt * V;
   const int64_t seq = a.rope_seq;
   const int64_t pos0 = slot % seq;
-  double* freq_lds = reinterpret_cast<double*>(dyn_lds);                   // [P][blockDim]
-  float2* step_lds = reinterpret_cast<float2*>(freq_lds + P * blockDim.x);  // [P][blockDim]
-  float2* first_lds = step_lds + P * blockDim.x;                            // [P][blockDim]
-  float* comb = reinterpret_cast<float*>(first_lds + P * blockDim.x);
+  const int bd = blockDim.x;
+  const int tid = threadIdx.x;
+  double* freq_lds = reinterpret_cast<double*>(dyn_lds);  // [P][bd], one chunk per thread
+  float2* step_lds = kTablesInLds ? reinterpret_cast<float2*>(freq_lds + P * bd)
+                                  : reinterpret_cast<float2*>(dyn_lds);  // [NP][bd]
+  float2* first_lds = step_lds + NP * bd;  // [P][bd], one chunk per thread
+  float* comb = reinterpret_cast<float*>(kTablesInLds ? first_lds + P * bd : first_lds);
   // 1 / dim is exact for a power of two, so s * (1 / dim) has the bits of s / dim
   const bool dim_pow2 = (a.dim & (a.dim - 1)) == 0;
   const float inv_dim = 1.0f / (float)a.dim;
+  auto col_of = [&](int k) { return (int64_t)(lt + k * tpr) * V; };
+  // pair e's frequency: base^(-2i/dim), i its pair index in the row
+  auto freq_of = [&](int e) {
+    if constexpr (kTablesInLds) return freq_lds[e * bd + tid];
+    else return rope_freq((lt + (e / P) * tpr) * P + e % P, a.rope_c_hi, a.rope_c_lo);
+  };
 
-  float wf[V], acc[V];
-  {
-    WeightChunk<DT, WDT> wc;
-    wc.load(a.w, col);
-    wc.unpack(a.w != nullptr, wf);
-  }
+  float wf[NV][V], acc[NV][V];
 #pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+  for (int k = 0; k < NV; ++k) {
+    WeightChunk<DT, WDT> wc;
+    wc.load(a.w, col_of(k));
+    wc.unpack(a.w != nullptr, wf[k]);
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[k][i] = 0.0f;
+  }
   // one pair at a time (a double sincos holds many registers; the walk needs them)
 #pragma unroll 1
-  for (int q = 0; q < P; ++q) {
-    const double f = rope_freq(lt * P + q, a.rope_c_hi, a.rope_c_lo);
-    freq_lds[q * blockDim.x + threadIdx.x] = f;
+  for (int e = 0; e < NP; ++e) {
+    const double f = rope_freq((lt + (e / P) * tpr) * P + e % P, a.rope_c_hi, a.rope_c_lo);
     double sv, cv;
     sincos((double)S * f, &sv, &cv);
-    step_lds[q * blockDim.x + threadIdx.x] = float2{(float)cv, (float)sv};
-    // the rotation at the walk's first position: double angle, reduced exactly, float sincospi
-    const double rev = (double)pos0 * f * kInv2PiD;
-    float s0, c0;
-    sincospif(2.0f * (float)(rev - rint(rev)), &s0, &c0);
-    first_lds[q * blockDim.x + threadIdx.x] = float2{c0, s0};
+    step_lds[e * bd + tid] = float2{(float)cv, (float)sv};
+    if constexpr (kTablesInLds) {
+      freq_lds[e * bd + tid] = f;
+      // the rotation at the walk's first position: double angle, reduced exactly, float sincospi
+      const double rev = (double)pos0 * f * kInv2PiD;
+      float s0, c0;
+      sincospif(2.0f * (float)(rev - rint(rev)), &s0, &c0);
+      first_lds[e * bd + tid] = float2{c0, s0};
+    }
   }
-  float cr[P], sr[P];
+  float cr[NP], sr[NP];
+  // the rotations at position p evaluated afresh: double angle, exact reduction, float sincospi
+  auto evaluate_at = [&](int64_t p) {
 #pragma unroll
-  for (int q = 0; q < P; ++q) {
-    const float2 f0 = first_lds[q * blockDim.x + threadIdx.x];
-    cr[q] = f0.x;
-    sr[q] = f0.y;
-  }
+    for (int e = 0; e < NP; ++e) {
+      const double rev = (double)p * freq_of(e) * kInv2PiD;
+      sincospif(2.0f * (float)(rev - rint(rev)), &sr[e], &cr[e]);
+    }
+  };
+  auto restore_first = [&]() {
+    if constexpr (kTablesInLds) {
+#pragma unroll
+      for (int e = 0; e < NP; ++e) {
+        const float2 f0 = first_lds[e * bd + tid];
+        cr[e] = f0.x;
+        sr[e] = f0.y;
+      }
+    } else {
+      evaluate_at(pos0);
+    }
+  };
+  restore_first();
   int64_t pos = pos0;
   int since = 0;  // float steps taken since the state was last exact
 
-  u32x4 gr[R], hr[R];
+  u32x4 gr[R][NV], hr[R][NV];
   float rr[R];
   // Row `row`'s grad_y and h chunks and inv_rms; rows past the end read the last row.
-  auto load_row = [&](int64_t row, u32x4& gv, u32x4& hv, float& r) {
+  auto load_row = [&](int64_t row, u32x4* gv, u32x4* hv, float& r) {
     const int64_t rw = row < a.rows ? row : last;
     r = a.inv_rms[rw];
-    gv = load16_stream<DT>(a.g, rw * a.ld_g + col);
-    hv = load16_stream<DT>(a.saved, rw * a.ld_s + col);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      gv[k] = load16_stream<DT>(a.g, rw * a.ld_g + col_of(k));
+      hv[k] = load16_stream<DT>(a.saved, rw * a.ld_s + col_of(k));
+    }
   };
   // The backward of one row (bwd_vec_kernel's with kSavedIsH | kRopeG); `ok` = the row exists.
-  auto process = [&](const u32x4& gv, const u32x4& hv, float r, int64_t row, bool ok, int it) {
-    float gf[V], xh[V];
-    C::unpack(gv, gf);
-    // inverse rotation of each pair (y0, y1) -> (y0 c + y1 s, y1 c - y0 s)
-#pragma unroll
-    for (int q = 0; q < P; ++q) {
-      const float c = cr[q], sn = sr[q];
-      const float g0 = gf[2 * q], g1 = gf[2 * q + 1];
-      gf[2 * q] = __builtin_fmaf(g0, c, g1 * sn);
-      gf[2 * q + 1] = __builtin_fmaf(g1, c, -(g0 * sn));
-    }
-    C::unpack(hv, xh);
-#pragma unroll
-    for (int i = 0; i < V; ++i) xh[i] = xh[i] * r;
+  auto process = [&](const u32x4* gv, const u32x4* hv, float r, int64_t row, bool ok, int it) {
+    float gf[NV][V], xh[NV][V];
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < V; ++i) s = __builtin_fmaf(gf[i] * wf[i], xh[i], s);
+    for (int k = 0; k < NV; ++k) {
+      C::unpack(gv[k], gf[k]);
+      // inverse rotation of each pair (y0, y1) -> (y0 c + y1 s, y1 c - y0 s)
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const float c = cr[k * P + q], sn = sr[k * P + q];
+        const float g0 = gf[k][2 * q], g1 = gf[k][2 * q + 1];
+        gf[k][2 * q] = __builtin_fmaf(g0, c, g1 * sn);
+        gf[k][2 * q + 1] = __builtin_fmaf(g1, c, -(g0 * sn));
+      }
+      C::unpack(hv[k], xh[k]);
+#pragma unroll
+      for (int i = 0; i < V; ++i) xh[k][i] = xh[k][i] * r;
+#pragma unroll
+      for (int i = 0; i < V; ++i) s = __builtin_fmaf(gf[k][i] * wf[k][i], xh[k][i], s);
+    }
     s = row_sum(s, tpr, grp, red[it & 1]);
     const float m = dim_pow2 ? s * inv_dim : s / (float)a.dim;
-    float d[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) d[i] = r * __builtin_fmaf(-xh[i], m, gf[i] * wf[i]);
-    if (ok) store16_stream<DT>(a.dx, row * a.ld_dx + col, C::pack(d));
+    for (int k = 0; k < NV; ++k) {
+      float d[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      acc[i] = ok ? __builtin_fmaf(gf[i], xh[i], acc[i]) : acc[i];
-      // the row's sums are done here: its g and xhat are not held into the next row
-      asm volatile("" : "+v"(acc[i]));
+      for (int i = 0; i < V; ++i) d[i] = r * __builtin_fmaf(-xh[k][i], m, gf[k][i] * wf[k][i]);
+      if (ok) store16_stream<DT>(a.dx, row * a.ld_dx + col_of(k), C::pack(d));
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        acc[k][i] = ok ? __builtin_fmaf(gf[k][i], xh[k][i], acc[k][i]) : acc[k][i];
+        // the row's sums are done here: its g and xhat are not held into the next row
+        asm volatile("" : "+v"(acc[k][i]));
+      }
     }
     // the next row's angles: the walk's first position again, evaluated afresh after
     // kRopeAnchorRows - 1 steps, or one float step of S positions on (each thread reads only the
@@ -1326,26 +1373,17 @@ __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(c
     if (pos >= seq) {
       pos = pos0;
       since = 0;
-#pragma unroll
-      for (int q = 0; q < P; ++q) {
-        const float2 f0 = first_lds[q * blockDim.x + threadIdx.x];
-        cr[q] = f0.x;
-        sr[q] = f0.y;
-      }
+      restore_first();
     } else if (since == kRopeAnchorRows) {
       since = 0;
-#pragma unroll
-      for (int q = 0; q < P; ++q) {
-        const double rev = (double)pos * freq_lds[q * blockDim.x + threadIdx.x] * kInv2PiD;
-        sincospif(2.0f * (float)(rev - rint(rev)), &sr[q], &cr[q]);
-      }
+      evaluate_at(pos);
     } else {
 #pragma unroll
-      for (int q = 0; q < P; ++q) {
-        const float2 st = step_lds[q * blockDim.x + threadIdx.x];
-        const float cn = __builtin_fmaf(cr[q], st.x, -(sr[q] * st.y));
-        sr[q] = __builtin_fmaf(sr[q], st.x, cr[q] * st.y);
-        cr[q] = cn;
+      for (int e = 0; e < NP; ++e) {
+        const float2 st = step_lds[e * bd + tid];
+        const float cn = __builtin_fmaf(cr[e], st.x, -(sr[e] * st.y));
+        sr[e] = __builtin_fmaf(sr[e], st.x, cr[e] * st.y);
+        cr[e] = cn;
       }
     }
   };
@@ -1381,14 +1419,22 @@ __global__ __launch_bounds__(vg_plan::kRingBlock, 4) void bwd_rope_ring_kernel(c
   float* prow = a.partial + (int64_t)blockIdx.x * a.dim;
   if (groups == 1) {
 #pragma unroll
-    for (int q = 0; q < V / 4; ++q)
-      store16<VELOGRAD_DTYPE_F32>(prow, col + 4 * q, Codec<VELOGRAD_DTYPE_F32>::pack(&acc[4 * q]));
+    for (int k = 0; k < NV; ++k) {
+#pragma unroll
+      for (int q = 0; q < V / 4; ++q)
+        store16<VELOGRAD_DTYPE_F32>(prow, col_of(k) + 4 * q,
+                                    Codec<VELOGRAD_DTYPE_F32>::pack(&acc[k][4 * q]));
+    }
     return;
   }
   for (int gi = 0; gi < groups; ++gi) {
     if (grp == gi) {
 #pragma unroll
-      for (int i = 0; i < V; ++i) comb[col + i] = (gi == 0) ? acc[i] : comb[col + i] + acc[i];
+      for (int k = 0; k < NV; ++k) {
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          comb[col_of(k) + i] = (gi == 0) ? acc[k][i] : comb[col_of(k) + i] + acc[k][i];
+      }
     }
     __syncthreads();
   }
@@ -1638,7 +1684,10 @@ void launch_bwd_flags(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
   }
   if constexpr ((F & kRopeG) != 0) {
     if (b.ring) {
-      hipLaunchKernelGGL((bwd_rope_ring_kernel<DT, WDT>), grid, block, lds, st, a);
+      if (p.nv == 2)
+        hipLaunchKernelGGL((bwd_rope_ring_kernel<DT, WDT, 2>), grid, block, lds, st, a);
+      else
+        hipLaunchKernelGGL((bwd_rope_ring_kernel<DT, WDT, 1>), grid, block, lds, st, a);
       return;
     }
     // NV 4 is never planned with the RoPE gradient (max_block_for_nv_rope); it is not compiled
