@@ -227,6 +227,15 @@ int main() {
     CHECK(fwd_late_h(p) == (dim <= 4096), "fwd_late_h dim=%lld tpr=%d", (long long)dim, p.tpr);
   }
   CHECK(!fwd_late_h(plan_rows(4096, 2, false, 0, kFwdOrder)), "fwd_late_h on the generic plan");
+  // the norm + RoPE forward's walk length: 32 rows for row groups of more than 256 threads over
+  // at least 16384 rows, else 16; the walk's inv_rms stores need a thread per row of the walk
+  for (int tpr = 64; tpr <= 1024; tpr += 64) {
+    for (int64_t rows : {1, 15, 16, 4096, 16383, 16384, 16385, 262147}) {
+      const int w = fwd_rope_walk_rows(rows, tpr);
+      CHECK(w == ((tpr > 256 && rows >= 16384) ? 32 : 16) && w <= tpr,
+            "fwd_rope_walk_rows rows=%lld tpr=%d -> %d", (long long)rows, tpr, w);
+    }
+  }
   if (failures) {
     fprintf(stderr, "%d failures over %ld plans\n", failures, plans);
     return 1;

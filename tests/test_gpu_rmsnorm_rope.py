@@ -3,8 +3,10 @@
 pinned oracles: rmsnorm_module_forward (nn.py:338-355, float64, 1e-12 floor) then apply_rotary_emb
 (functional.py:287-315, float64).  Tolerance per rotated element: 16 float32 ulps of the normalised
 pair (the fused kernels form the angles in double, so the bound does not grow with the
-position), a float32 term for the norm, and half an output ulp for bf16/fp16 (half the subnormal
-spacing for fp16 outputs below 2^-14); inv_rms |a-b|/(|b|+1e-6) <= 1e-5; h bit-exact.  The one-pass backward
+position), a float32 term for the norm, and for bf16/fp16 outputs 2^-17 of the pair for the
+forward walk's float32 rotation recurrence (at most 31 steps of about 3 float32 ulps from an
+exact value; fp32 outputs keep it in double) plus half an output ulp (half the subnormal spacing
+for fp16 outputs below 2^-14); inv_rms |a-b|/(|b|+1e-6) <= 1e-5; h bit-exact.  The one-pass backward
 (velograd_rmsnorm_rope_bwd) is checked against the composition of the inverse rotation and the
 module backward, with the bound stated above its test.  The autograd module is checked against
 torch float64 autograd of rms_norm and the complex-number rotation."""
@@ -21,17 +23,21 @@ from velograd_amd import nn as vnn
 pytestmark = pytest.mark.gpu
 
 ROUNDING = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8 * 1.01, torch.float16: 2.0 ** -11 * 1.01}
+# The forward walk's float32 rotation recurrence (16-bit outputs): at most 31 steps of about
+# 3 float32 ulps of the pair each from an exact value (2^-17.5); fp32 outputs keep it in double.
+RECURRENCE = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -17, torch.float16: 2.0 ** -17}
 # Half the spacing of the output dtype's subnormals: below 2^-14 an fp16 output rounds to a
 # multiple of 2^-24, so its rounding error is up to 2^-25 whatever its relative size.
 SUBNORMAL_HALF = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -134, torch.float16: 2.0 ** -25}
 
 
-def _bound(n: np.ndarray, base: float) -> np.ndarray:
+def _bound(n: np.ndarray, base: float, recurrence: float = 0.0) -> np.ndarray:
     """RoPE tolerance for pairs (n_2i, n_2i+1), plus a float32 term for the norm.  The fused
     kernels form every angle pos * freq in double and reduce it exactly before a float32
-    sincospi, so the bound does not grow with the position: 16 float32 ulps of the pair."""
+    sincospi, so the bound does not grow with the position: 16 float32 ulps of the pair, plus
+    `recurrence` of the pair for a float32 rotation recurrence."""
     mag = np.abs(n[..., 0::2]) + np.abs(n[..., 1::2])
-    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -21 + 2.0 ** -20) * mag
+    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -21 + 2.0 ** -20 + recurrence) * mag
     out = np.empty_like(n)
     out[..., 0::2] = b
     out[..., 1::2] = b
@@ -41,12 +47,15 @@ def _bound(n: np.ndarray, base: float) -> np.ndarray:
 CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 8192), False),
          (torch.float32, (3, 33, 1000), True), (torch.float16, (2, 50, 256), False),
          (torch.bfloat16, (3, 5, 6), True), (torch.float32, (4, 2, 3, 40), False),
-         # the 16-bit kernel's walks over rows b, b + G, ... (G = rows / 16 workgroups): no
-         # sequence end (G = 1024, seq 16384), returning to the walk's first position every 2 rows
-         # (seq 2048 a multiple of G) and on every row (G = 128 a multiple of seq 64), and angles
-         # evaluated afresh where a walk crosses a sequence end (G = 938, seq 3000)
+         # the 16-bit kernel's walks over rows b, b + G, ... (G = rows / W workgroups, W = 32
+         # rows for row groups over 256 threads and at least 16384 rows, else 16): no sequence
+         # end (W = 32, G = 512, seq 16384), returning to the walk's first position every 4 rows
+         # (seq 2048 a multiple of G = 512) and on every row (W = 16, G = 128 a multiple of seq
+         # 64), angles evaluated afresh where a walk crosses a sequence end (W = 16, G = 938, seq
+         # 3000; W = 32, G = 563), and 640-thread rows returning every 16 rows (W = 32, G = 512)
          (torch.bfloat16, (1, 16384, 4096), False), (torch.float16, (8, 2048, 4096), True),
-         (torch.bfloat16, (32, 64, 1024), True), (torch.bfloat16, (5, 3000, 4096), False)]
+         (torch.bfloat16, (32, 64, 1024), True), (torch.bfloat16, (5, 3000, 4096), False),
+         (torch.bfloat16, (6, 3000, 4096), False), (torch.bfloat16, (2, 8192, 5120), True)]
 
 
 @pytest.mark.parametrize("dtype,shape,with_res", CASES,
@@ -75,7 +84,8 @@ def test_fused_norm_rope_matches_the_oracle_composition(dtype, shape, with_res, 
                                          1e-6)
     want = ora.apply_rotary_emb(n, base)
     assert P.rel_err(P.upcast(inv), rinv) <= P.FP32_REL_TOL
-    tol = _bound(n, base) + ROUNDING[dtype] * np.abs(want) + SUBNORMAL_HALF[dtype]
+    tol = (_bound(n, base, RECURRENCE[dtype]) + ROUNDING[dtype] * np.abs(want)
+           + SUBNORMAL_HALF[dtype])
     err = np.abs(P.upcast(y).astype(np.float64) - want)
     assert np.all(err <= tol), float((err - tol).max())
 

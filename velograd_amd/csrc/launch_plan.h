@@ -297,6 +297,22 @@ inline BwdPlan plan_bwd_rope(int64_t rows, int64_t dim, int elem_bytes, bool ali
                   kBwdOrderRope);
 }
 
+// Rows per walk of the norm + RoPE forward (fwd_rope_kernel: workgroup b walks rows b, b + G, ...
+// with G = ceil(rows / W)).  32-row walks halve the workgroups and the per-walk set-up (the
+// step and first rotations, a few hundred vector instructions a thread); they pay where a row
+// group fills a CU's waves with fewer workgroups (more than 256 threads) and the tensor keeps
+// at least two 32-row walks per CU on 256 CUs.  Measured on MI355X (bf16, module form, A/B in one
+// process, 3 rounds; 16-row against 32-row walks): 16384 x 4096 51.2 / 50.0 us (one sequence
+// 50.3 / 49.8), 16384 x 5120 73.4 / 61.4, 16384 x 7168 98.2 / 89.5, 16384 x 8192 103.8 / 94.1,
+// 16384 x 3072 42.1 / 40.3; against: 32768 x 2048 51.6 / 52.2 (256-thread rows), 8192 x 4096
+// 27.2 / 31.2 (256 workgroups); 64-row walks lost everywhere (99.6 us at 16384 x 4096).
+constexpr int kNormRopeRows = 16;
+constexpr int kNormRopeLongRows = 32;
+constexpr int64_t kNormRopeLongMinRows = 16384;
+inline int fwd_rope_walk_rows(int64_t rows, int tpr) {
+  return tpr > 256 && rows >= kNormRopeLongMinRows ? kNormRopeLongRows : kNormRopeRows;
+}
+
 // Workspace of the backward's dweight partial rows.  The plan depends on the element size, on
 // pointer alignment and on whether the RoPE gradient is fused, which a size query does not know,
 // so this is the largest need over every plan the backward can pick for (rows, dim).

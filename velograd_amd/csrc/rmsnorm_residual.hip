@@ -465,7 +465,8 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 
 // ------------------------------------------------------------------------------------------
 // Forward with the model's RoPE on y (kOutRopeI), one 16-byte chunk per thread.  Workgroup b of
-// G walks up to kNormRopeRows rows b, b + G, b + 2G, ...: at each step the resident workgroups
+// G walks up to W rows b, b + G, b + 2G, ... (W = 16, or 32 for long tensors of wide rows:
+// launch_plan.h fwd_rope_walk_rows): at each step the resident workgroups
 // touch adjacent rows, one compact address front that HBM serves better than runs of
 // consecutive rows per workgroup (those spread the front over 16 rows per workgroup).  The next
 // rows' chunks are in flight while the current one reduces.  Each thread keeps the rotation
@@ -475,7 +476,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 // VALU-bound, no faster than two passes.  The walk's first angle is the double pos * freq_j
 // reduced exactly before a float sincospi (a few float32 ulps), and so is the step's; the
 // recurrence adds ~1e-16 per step in double, about 3 float32 ulps of the pair in float32, over
-// at most kNormRopeRows - 1 steps from an exact value.  Where a step crosses
+// at most W - 1 steps from an exact value.  Where a step crosses
 // the end of a sequence (row position = row % rope_seq) and G is a multiple or a divisor of
 // rope_seq, the position returns to the walk's first one and so does the rotation (kept); any
 // other crossing re-evaluates the angle at the new position.
@@ -490,13 +491,14 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
 // each row waits for its own loads only instead of draining every load and store at each row.
 // Shorter walks and walks that re-evaluate angles take the guarded loop.
 // ------------------------------------------------------------------------------------------
-constexpr int kNormRopeRows = 16;
 constexpr int kRopeRes = 1;     // RF: a residual is added
 constexpr int kRopeWriteH = 2;  // RF: h is stored
 constexpr int kRopeDimPow2 = 4; // RF: dim is a power of two
 
-template <int DT, int WDT, int RF>
+template <int DT, int WDT, int RF, int W>
 __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const FwdArgs a) {
+  static_assert(W == vg_plan::kNormRopeRows || W == vg_plan::kNormRopeLongRows,
+                "walks of 16 or 32 rows");
   using C = Codec<DT>;
   constexpr int V = C::kVec;
   constexpr int PP = V / 2;  // pairs per chunk
@@ -511,7 +513,7 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
   const int64_t G = gridDim.x;   // row step of the walk
   const int64_t row0 = blockIdx.x;
   const int64_t left = (a.rows - row0 + G - 1) / G;
-  const int nrows = (int)(left < kNormRopeRows ? left : kNormRopeRows);
+  const int nrows = (int)(left < W ? left : W);
   const int64_t col = (int64_t)lt * V;
   const int64_t seq = a.rope_seq;
   const int64_t pos0 = row0 % seq;
@@ -531,9 +533,11 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
     wc.load((has_w && lane_ok) ? a.w : nullptr, col);
     wc.unpack(has_w, wf);
   }
-  // The rotation state: double for fp32 outputs; float32 for bf16/fp16 ones, whose walks of at
-  // most kNormRopeRows rows from an exact start stay within ~45 float32 ulps of the pair, far
-  // below their output's rounding.
+  // The rotation state: double for fp32 outputs; float32 for bf16/fp16 ones, within about 3
+  // float32 ulps of the pair per step over at most W - 1 = 31 steps (~2^-17.5 of the pair), far
+  // below their output's rounding (2^-9 for bf16, 2^-12 for fp16).  Re-evaluating it at the 16th
+  // row of a 32-row walk cost 2-5 us at 16384 rows (trigonometry set aside for it before the
+  // walk; placed in the unrolled loop it stopped the unrolling).
   using RotT = std::conditional_t<DT == VELOGRAD_DTYPE_F32, double, float>;
   auto rot_fma = [](RotT x, RotT y, RotT z) {
     if constexpr (DT == VELOGRAD_DTYPE_F32) return __builtin_fma(x, y, z);
@@ -626,9 +630,9 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
     }
   };
 
-  const bool walk_ok = back_to_start || pos0 + (int64_t)(kNormRopeRows - 1) * G < seq;
-  if (nrows == kNormRopeRows && nchunk == tpr && walk_ok) {
-    __shared__ float inv_lds[kNormRopeRows];
+  const bool walk_ok = back_to_start || pos0 + (int64_t)(W - 1) * G < seq;
+  if (nrows == W && nchunk == tpr && walk_ok) {
+    __shared__ float inv_lds[W];
     constexpr int RB = 3;
     u32x4 xb[RB], rb[RB];
     xb[0] = xv;
@@ -637,10 +641,10 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
     if constexpr (has_res) rb[1] = load16_stream<DT>(a.res, (row0 + G) * a.ld_res + col);
     int64_t pos = pos0;
 #pragma unroll
-    for (int it = 0; it < kNormRopeRows; ++it) {
+    for (int it = 0; it < W; ++it) {
       const int b = it % RB;
       const int64_t row = row0 + it * G;
-      if (it + 2 < kNormRopeRows) {
+      if (it + 2 < W) {
         const int nb = (it + 2) % RB;
         xb[nb] = load16_stream<DT>(a.x, (row + 2 * G) * a.ld_x + col);
         if constexpr (has_res) rb[nb] = load16_stream<DT>(a.res, (row + 2 * G) * a.ld_res + col);
@@ -653,10 +657,10 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
       float yf[V];
       make_y(hf, r, yf);
       store16_stream<DT>(a.y, row * a.ld_y + col, C::pack(yf));
-      if (it + 1 < kNormRopeRows) advance(pos, std::false_type{});
+      if (it + 1 < W) advance(pos, std::false_type{});
     }
-    // thread 0 wrote inv_lds; threads 1..15 of its wave read it in program order
-    if (lt < kNormRopeRows && a.inv_rms != nullptr) a.inv_rms[row0 + lt * G] = inv_lds[lt];
+    // thread 0 wrote inv_lds; threads 1..W-1 of its wave read it in program order
+    if (lt < W && a.inv_rms != nullptr) a.inv_rms[row0 + lt * G] = inv_lds[lt];
     return;
   }
 
@@ -1612,19 +1616,28 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
                          dim3(kGenericBlock), 0, st, a);
       return;
     }
-    const dim3 grid((uint32_t)((a.rows + kNormRopeRows - 1) / kNormRopeRows)), block(p.tpr);
+    const int w = vg_plan::fwd_rope_walk_rows(a.rows, p.tpr);
+    const dim3 grid((uint32_t)((a.rows + w - 1) / w)), block(p.tpr);
     const int rf = (a.res == nullptr ? 0 : a.h == nullptr ? kRopeRes : kRopeRes | kRopeWriteH) |
                    ((a.dim & (a.dim - 1)) == 0 ? kRopeDimPow2 : 0);
-    switch (rf) {
-#define VG_ROPE_FWD(F) \
-  case F: hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, F>), grid, block, 0, st, a); break;
+    switch (rf * 2 + (w == vg_plan::kNormRopeLongRows ? 1 : 0)) {
+#define VG_ROPE_FWD(F)                                                                      \
+  case 2 * (F):                                                                             \
+    hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, F, vg_plan::kNormRopeRows>), grid, block, 0, \
+                       st, a);                                                              \
+    break;                                                                                  \
+  case 2 * (F) + 1:                                                                         \
+    hipLaunchKernelGGL((fwd_rope_kernel<DT, WDT, F, vg_plan::kNormRopeLongRows>), grid,       \
+                       block, 0, st, a);                                                    \
+    break;
       VG_ROPE_FWD(0)
       VG_ROPE_FWD(kRopeRes)
       VG_ROPE_FWD(kRopeRes | kRopeWriteH)
       VG_ROPE_FWD(kRopeDimPow2)
       VG_ROPE_FWD(kRopeDimPow2 | kRopeRes)
-      default: VG_ROPE_FWD(kRopeDimPow2 | kRopeRes | kRopeWriteH)
+      VG_ROPE_FWD(kRopeDimPow2 | kRopeRes | kRopeWriteH)
 #undef VG_ROPE_FWD
+      default: break;
     }
   } else {
     const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups));
