@@ -208,11 +208,13 @@ BWD_CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 81
              (torch.float32, (4, 4096, 1024), True), (torch.float16, (3, 1000, 512), False),
              (torch.bfloat16, (257, 64, 1024), True), (torch.bfloat16, (8, 1024, 2048), True),
              (torch.bfloat16, (2, 1024, 3072), True),
-             # two chunks per thread (rows of 513 to 1024 chunks): 320-, 448- and 512-thread
-             # row groups, fp32 and bf16; then the same widths where walks cross sequence ends
+             # two chunks per thread (rows of 513 to 1024 chunks): 320-, 384-, 448- and
+             # 512-thread row groups, fp32, fp16 and bf16; then the same widths where walks cross
+             # sequence ends
              # elsewhere (bwd_vec_kernel)
              (torch.bfloat16, (2, 1024, 5120), True), (torch.bfloat16, (4, 512, 7168), False),
              (torch.float32, (2, 1024, 2560), True), (torch.float32, (1, 4096, 4096), True),
+             (torch.float16, (2, 512, 6144), True),
              (torch.bfloat16, (6, 1000, 4096), True), (torch.bfloat16, (3, 1000, 8192), True)]
 
 
