@@ -85,6 +85,9 @@ def parse_args(argv=None):
     p.add_argument("--no-norm-rope", action="store_true",
                    help="skip the fused versus two-pass RMSNorm + RoPE timing and the "
                         "module-form norm on its buffers")
+    p.add_argument("--norm-rope-dim", type=int, default=4096,
+                   help="hidden size of the interleaved RoPE and norm + RoPE legs (their rows "
+                        "are the config's)")
     p.add_argument("--no-torch-baseline", action="store_true",
                    help="skip the PyTorch eager comparison and the reference benchmark's shapes")
     p.add_argument("--no-copy-ceiling", action="store_true",
@@ -389,10 +392,12 @@ def decode_latency(lib, stream, calls: int = 1000) -> list:
     return out
 
 
-def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True) -> dict:
+def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True,
+                hid: int = 4096) -> dict:
     """Fused RoPE (velograd_rope) on a Llama-3-8B-like attention input of the same token
     count: q [tokens, 32, 128] and k [tokens, 8, 128] bf16, theta 500000, one launch each per
-    step, rotating over `sets` buffer sets.  Bytes: q and k read once and written once."""
+    step, rotating over `sets` buffer sets.  Bytes: q and k read once and written once.  Then
+    the interleaved RoPE and the norm + RoPE legs over [tokens, hid]."""
     import torch
 
     from velograd_amd import _lib
@@ -433,8 +438,7 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True)
     del bufs
 
     # The reference model's RoPE (functional.py:287-315): interleaved pairs over the whole
-    # hidden vector of the normalised attention input, [tokens, 4096] bf16, base 10000.
-    hid = 4096
+    # hidden vector of the normalised attention input, [tokens, hid] bf16, base 10000.
     ibufs = [(torch.randn(tokens, hid, device=dev).to(torch.bfloat16),
               torch.empty(tokens, hid, device=dev, dtype=torch.bfloat16)) for _ in range(sets)]
 
@@ -902,7 +906,8 @@ def main(argv=None) -> int:
         if d % 32 == 0:
             extra.update(mx_forward_timing(lib, sets, rows, d, s, code, eps, stream))
     if not args.no_rope:
-        extra.update(rope_timing(lib, rows, stream, norm_rope=not args.no_norm_rope))
+        extra.update(rope_timing(lib, rows, stream, norm_rope=not args.no_norm_rope,
+                                 hid=args.norm_rope_dim))
     if not args.no_torch_baseline:
         extra.update(torch_eager_timing(sets, rows, d, s, eps, with_bwd, stream))
         extra["speedup_vs_torch_eager"] = round(
