@@ -246,13 +246,28 @@ __device__ __forceinline__ void rope_cos_sin(int64_t pos, int i, float c_hi, flo
   sincospif(2.0f * (float)(rev - rint(rev)), &s, &c);
 }
 
-__device__ __forceinline__ void rope_pair(float& y0, float& y1, int64_t pos, int i, float c_hi,
-                                          float c_lo) {
-  float s, c;
-  rope_cos_sin(pos, i, c_hi, c_lo, c, s);
-  const float x0 = y0, x1 = y1;
-  y0 = x0 * c - x1 * s;                                                   // functional.py:313
-  y1 = x0 * s + x1 * c;                                                   // functional.py:314
+// The frequencies of a thread's pairs in a strided loop (pairs i0, i0 + stride, ...): the first
+// from exp2, each next one the previous times base^(-2 stride / dim), in double (a few double
+// ulps over a row, far below the float32 rotation's rounding), so the generic kernels pay one
+// double exp2 per row and thread instead of one per pair.
+struct RopeFreqWalk {
+  double f, ratio;
+  __device__ RopeFreqWalk(int i0, int stride, float c_hi, float c_lo) {
+    const double c = (double)c_hi + (double)c_lo;
+    f = exp2(-(double)i0 * c);
+    ratio = exp2(-(double)stride * c);
+  }
+  __device__ double next() {
+    const double v = f;
+    f *= ratio;
+    return v;
+  }
+};
+
+// cos and sin at position pos of the pair whose frequency is fr (as rope_cos_sin)
+__device__ __forceinline__ void rope_cos_sin_f(int64_t pos, double fr, float& c, float& s) {
+  const double rev = (double)pos * fr * kInv2PiD;
+  sincospif(2.0f * (float)(rev - rint(rev)), &s, &c);
 }
 
 // Largest value over aligned groups of L lanes (L = 4 or 8), on every lane of the group.
@@ -722,11 +737,13 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
     for (int j = threadIdx.x; j < a.dim; j += blockDim.x) C::store1(a.y, row * a.ld_y + j, y_at(j));
   } else if constexpr (OUT == kOutRopeI) {
     const int64_t pos = row % a.rope_seq;
+    RopeFreqWalk fw(threadIdx.x, blockDim.x, a.rope_c_hi, a.rope_c_lo);
     for (int i = threadIdx.x; i < a.rope_half; i += blockDim.x) {
-      float y0 = y_at(2 * i), y1 = y_at(2 * i + 1);
-      rope_pair(y0, y1, pos, i, a.rope_c_hi, a.rope_c_lo);
-      C::store1(a.y, row * a.ld_y + 2 * i, y0);
-      C::store1(a.y, row * a.ld_y + 2 * i + 1, y1);
+      const float x0 = y_at(2 * i), x1 = y_at(2 * i + 1);
+      float c, sn;
+      rope_cos_sin_f(pos, fw.next(), c, sn);
+      C::store1(a.y, row * a.ld_y + 2 * i, x0 * c - x1 * sn);       // functional.py:313
+      C::store1(a.y, row * a.ld_y + 2 * i + 1, x0 * sn + x1 * c);   // functional.py:314
     }
   } else if constexpr (OUT == kOutMxE4M3 || OUT == kOutMxE2M1) {
     // MX epilogue (see fwd_vec_kernel): a third pass, one 32-element block per thread.
@@ -1464,32 +1481,19 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
     const int64_t row = slot + (int64_t)it * nslots;
     if (row >= a.rows) break;  // uniform across the workgroup
     const float rr = a.inv_rms[row];
-    // element j of grad_y rotated back: its pair (y0, y1) -> (y0 c + y1 s, y1 c - y0 s)
-    auto grad_at = [&](int j) {
-      const float gj = C::load1(a.g, row * a.ld_g + j);
-      if constexpr (ROPE) {
-        const float gp = C::load1(a.g, row * a.ld_g + (j ^ 1));
-        float c, sn;
-        rope_cos_sin(row % a.rope_seq, j >> 1, a.rope_c_hi, a.rope_c_lo, c, sn);
-        return (j & 1) ? gj * c - gp * sn : gj * c + gp * sn;
-      } else {
-        return gj;
-      }
+    // element j's contributions given its (rotated-back) gradient gf: to the row sum, then to
+    // dx, dres and the partial row
+    auto xh_at = [&](int j) {
+      float xh = C::load1(a.saved, row * a.ld_s + j);
+      if constexpr (SAVED_IS_H) xh = xh * rr;
+      return xh;
     };
-    float s = 0.0f;
-    for (int j = threadIdx.x; j < a.dim; j += blockDim.x) {
-      const float gf = grad_at(j);
-      float xh = C::load1(a.saved, row * a.ld_s + j);
-      if constexpr (SAVED_IS_H) xh = xh * rr;
+    auto sum_term = [&](int j, float gf) {
       const float gw = has_w ? gf * CW::load1(a.w, j) : gf;
-      s += gw * xh;
-    }
-    s = row_sum(s, blockDim.x, 0, red[it & 1]);
-    const float m = s / (float)a.dim;
-    for (int j = threadIdx.x; j < a.dim; j += blockDim.x) {
-      const float gf = grad_at(j);
-      float xh = C::load1(a.saved, row * a.ld_s + j);
-      if constexpr (SAVED_IS_H) xh = xh * rr;
+      return gw * xh_at(j);
+    };
+    auto finish = [&](int j, float gf, float m) {
+      const float xh = xh_at(j);
       const float gw = has_w ? gf * CW::load1(a.w, j) : gf;
       float d = rr * (gw - xh * m);
       if constexpr (HAS_GH) d = d + C::load1(a.gh, row * a.ld_gh + j);
@@ -1499,6 +1503,43 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
         const float p = gf * xh;
         prow[j] = (it == 0) ? p : prow[j] + p;
       }
+    };
+    float s = 0.0f;
+    if constexpr (ROPE) {
+      // one rotation per pair (y0, y1) -> (y0 c + y1 s, y1 c - y0 s) and pass
+      const int64_t pos = row % a.rope_seq;
+      const int half = a.dim / 2;
+      auto grad_pair = [&](int i, double fr, float& g0, float& g1) {
+        float c, sn;
+        rope_cos_sin_f(pos, fr, c, sn);
+        const float y0 = C::load1(a.g, row * a.ld_g + 2 * i);
+        const float y1 = C::load1(a.g, row * a.ld_g + 2 * i + 1);
+        g0 = y0 * c + y1 * sn;
+        g1 = y1 * c - y0 * sn;
+      };
+      RopeFreqWalk fw(threadIdx.x, blockDim.x, a.rope_c_hi, a.rope_c_lo);
+      for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        float g0, g1;
+        grad_pair(i, fw.next(), g0, g1);
+        s += sum_term(2 * i, g0);
+        s += sum_term(2 * i + 1, g1);
+      }
+      s = row_sum(s, blockDim.x, 0, red[it & 1]);
+      const float m = s / (float)a.dim;
+      RopeFreqWalk fw2(threadIdx.x, blockDim.x, a.rope_c_hi, a.rope_c_lo);
+      for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        float g0, g1;
+        grad_pair(i, fw2.next(), g0, g1);
+        finish(2 * i, g0, m);
+        finish(2 * i + 1, g1, m);
+      }
+    } else {
+      for (int j = threadIdx.x; j < a.dim; j += blockDim.x)
+        s += sum_term(j, C::load1(a.g, row * a.ld_g + j));
+      s = row_sum(s, blockDim.x, 0, red[it & 1]);
+      const float m = s / (float)a.dim;
+      for (int j = threadIdx.x; j < a.dim; j += blockDim.x)
+        finish(j, C::load1(a.g, row * a.ld_g + j), m);
     }
   }
 }
