@@ -55,7 +55,11 @@ CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 8192),
          # 3000; W = 32, G = 563), and 640-thread rows returning every 16 rows (W = 32, G = 512)
          (torch.bfloat16, (1, 16384, 4096), False), (torch.float16, (8, 2048, 4096), True),
          (torch.bfloat16, (32, 64, 1024), True), (torch.bfloat16, (5, 3000, 4096), False),
-         (torch.bfloat16, (6, 3000, 4096), False), (torch.bfloat16, (2, 8192, 5120), True)]
+         (torch.bfloat16, (6, 3000, 4096), False), (torch.bfloat16, (2, 8192, 5120), True),
+         # rows of more than 1024 chunks: the one-shot rows with each pair's rotation evaluated
+         # directly (two to four chunks per thread)
+         (torch.bfloat16, (2, 64, 16384), True), (torch.float32, (3, 16, 6144), False),
+         (torch.float16, (1, 40, 12288), True)]
 
 
 @pytest.mark.parametrize("dtype,shape,with_res", CASES,

@@ -225,6 +225,9 @@ constexpr int kOutMxE4M3 = 2;  // MXFP8: e4m3 codes, one E8M0 scale per 32 eleme
 constexpr int kOutMxE2M1 = 3;  // MXFP4: e2m1 nibbles (two per byte), one E8M0 scale per 32
 constexpr int kOutRopeI = 4;   // y rotated by the reference model's interleaved RoPE
 constexpr int kOutDtypeLateH = 5;  // as kOutDtype, with h stored after the row reduction
+// y rotated by the interleaved RoPE with each pair's (cos, sin) evaluated directly: rows too wide
+// for fwd_rope_kernel's walk (more than one 16-byte chunk per thread)
+constexpr int kOutRopeDirect = 6;
 
 // The reference model's RoPE applied to y in registers (python/velograd/functional.py:287-315;
 // models/llama.py:48-49 rotates the normalised attention input): the pair (y_2i, y_2i+1) of a
@@ -370,7 +373,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
   };
 
   static_assert(OUT != kOutRopeI, "the RoPE output runs in fwd_rope_kernel");
-  if constexpr (OUT == kOutDtype || OUT == kOutDtypeLateH) {
+  if constexpr (OUT == kOutDtype || OUT == kOutDtypeLateH || OUT == kOutRopeDirect) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = lt + k * tpr;
@@ -382,6 +385,20 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
         }
         float yf[V];
         make_y(k, yf);
+        if constexpr (OUT == kOutRopeDirect) {
+          // pairs c * V/2 + q at position row % rope_seq (functional.py:302-314): double
+          // frequency and angle, exact reduction, float sincospi, as rope_cos_sin
+          const int64_t pos = row % a.rope_seq;
+          RopeFreqWalk fw(c * (V / 2), 1, a.rope_c_hi, a.rope_c_lo);
+#pragma unroll
+          for (int q = 0; q < V / 2; ++q) {
+            float cs, sn;
+            rope_cos_sin_f(pos, fw.next(), cs, sn);
+            const float y0 = yf[2 * q], y1 = yf[2 * q + 1];
+            yf[2 * q] = y0 * cs - y1 * sn;                                 // functional.py:313
+            yf[2 * q + 1] = y0 * sn + y1 * cs;                             // functional.py:314
+          }
+        }
         store16_stream<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
       }
     }
@@ -1649,8 +1666,20 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
     // chunks would hold 16 more doubles per chunk and spill, so longer rows take the generic
     // kernel.
     if (p.nv != 1) {
-      hipLaunchKernelGGL((fwd_generic_kernel<DT, WDT, OUT>), dim3((uint32_t)a.rows),
-                         dim3(kGenericBlock), 0, st, a);
+      // wider rows: the register-resident one-shot rows with each pair's rotation evaluated
+      // directly (1024-thread row groups, two to four chunks per thread)
+      const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups)), block(p.block);
+      switch (p.nv) {
+        case 2:
+          hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 2, kOutRopeDirect>), grid, block, 0, st, a);
+          break;
+        case 3:
+          hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 3, kOutRopeDirect>), grid, block, 0, st, a);
+          break;
+        default:
+          hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, 4, kOutRopeDirect>), grid, block, 0, st, a);
+          break;
+      }
       return;
     }
     const int w = vg_plan::fwd_rope_walk_rows(a.rows, p.tpr);
