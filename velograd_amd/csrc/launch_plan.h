@@ -285,12 +285,23 @@ inline bool rope_ring_eligible(const RowPlan& p, int64_t dim, int elem_bytes) {
 // generic plan where a row group does not fit that bound.
 inline BwdPlan plan_bwd_rope(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
                              int prefer_nv, int max_block, int waves_per_cu) {
-  const RowPlan rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrderRope);
+  RowPlan rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrderRope);
+  if (rp.vec && max_block_for_nv_rope(rp.nv) < rp.tpr) {
+    // the first chunk count whose row group fits the RoPE walk's bound (rows of 1536 chunks:
+    // three chunks per thread in 512 threads, not two in 768)
+    rp.vec = false;
+    for (int nv = 1; nv <= kMaxNV && !rp.vec; ++nv) {
+      const RowPlan q = plan_rows(dim, elem_bytes, aligned, nv, kBwdOrderRope);
+      if (q.vec && q.nv == nv && q.tpr <= max_block_for_nv_rope(nv)) rp = q;
+    }
+    if (!rp.vec)
+      return plan_bwd(rows, dim, elem_bytes, false, cus, prefer_nv, max_block,
+                      waves_per_cu);  // generic
+    prefer_nv = rp.nv;
+  }
   int mb = max_block;
   if (rp.vec) {
     const int bound = max_block_for_nv_rope(rp.nv);
-    if (bound < rp.tpr) return plan_bwd(rows, dim, elem_bytes, false, cus, prefer_nv, max_block,
-                                        waves_per_cu);  // generic
     if (bound < mb) mb = bound;
   }
   return plan_bwd(rows, dim, elem_bytes, aligned, cus, prefer_nv, mb, waves_per_cu,
