@@ -447,26 +447,30 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True,
         return fn(x.data_ptr(), out.data_ptr(), 1, tokens, 1, hid, hid, 10000.0, 0,
                   _lib.ROPE_INTERLEAVED, _lib.DTYPE_BF16, sp)
 
-    for i in range(sets * 2):
-        _lib.check(istep(i), "interleaved rope warm-up")
-    torch.cuda.synchronize()
-    e0.record(stream)
-    rc = 0
-    for i in range(reps):
-        rc |= istep(i)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    _lib.check(rc, "interleaved rope timed")
-    ius = e0.elapsed_time(e1) * 1e3 / reps
-    ibytes = 2 * tokens * hid * 2
-
     out = {"rope_qk_us_mean": round(us, 2), "rope_qk_bytes": nbytes,
            "rope_qk_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-           "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5",
-           "rope_interleaved_us_mean": round(ius, 2), "rope_interleaved_bytes": ibytes,
-           "rope_interleaved_gbs": round(ibytes / (ius * 1e-6) / 1e9, 1),
-           "rope_interleaved_workload": f"x [{tokens},{hid}] bf16, pairs (2i, 2i+1) over the "
-                                        f"hidden vector, base 1e4 (functional.apply_rotary_emb)"}
+           "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5"}
+    # velograd_rope rotates at most 8192 elements per token: wider rows have no standalone
+    # interleaved leg and no two-pass comparison
+    standalone = hid <= 8192
+    if standalone:
+        for i in range(sets * 2):
+            _lib.check(istep(i), "interleaved rope warm-up")
+        torch.cuda.synchronize()
+        e0.record(stream)
+        rc = 0
+        for i in range(reps):
+            rc |= istep(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        _lib.check(rc, "interleaved rope timed")
+        ius = e0.elapsed_time(e1) * 1e3 / reps
+        ibytes = 2 * tokens * hid * 2
+        out.update({
+            "rope_interleaved_us_mean": round(ius, 2), "rope_interleaved_bytes": ibytes,
+            "rope_interleaved_gbs": round(ibytes / (ius * 1e-6) / 1e9, 1),
+            "rope_interleaved_workload": f"x [{tokens},{hid}] bf16, pairs (2i, 2i+1) over the "
+                                         f"hidden vector, base 1e4 (functional.apply_rotary_emb)"})
     if not norm_rope:
         del ibufs
         return out
@@ -500,7 +504,8 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True,
                        1e-12, sp)
 
     times = {}
-    for name, st in (("fused", fstep), ("two_pass", tstep), ("norm_only", nstep)):
+    legs = (("fused", fstep), ("two_pass", tstep), ("norm_only", nstep))
+    for name, st in (legs if standalone else (legs[0], legs[2])):
         for i in range(sets * 2):
             _lib.check(st(i), f"norm+rope {name} warm-up")
         torch.cuda.synchronize()
@@ -538,7 +543,8 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True,
                            dxb.data_ptr(), None, dwb.data_ptr(), ws.data_ptr(), ws_bytes, tokens,
                            hid, hid, hid, hid, hid, hid, _lib.DTYPE_BF16, _lib.DTYPE_BF16, sp)
 
-    for name, st in (("bwd_fused", bstep), ("bwd_two_pass", b2step)):
+    for name, st in ((("bwd_fused", bstep), ("bwd_two_pass", b2step)) if standalone
+                     else (("bwd_fused", bstep),)):
         for i in range(sets * 2):
             _lib.check(st(i), f"norm+rope {name} warm-up")
         torch.cuda.synchronize()
@@ -555,10 +561,11 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True,
     out.update({
         "norm_rope_bwd_fused_us_mean": round(times["bwd_fused"], 2),
         "norm_rope_bwd_fused_gbs": round(nbytes_bwd / (times["bwd_fused"] * 1e-6) / 1e9, 1),
-        "norm_rope_bwd_two_pass_us_mean": round(times["bwd_two_pass"], 2),
+        "norm_rope_bwd_two_pass_us_mean": (round(times["bwd_two_pass"], 2) if standalone
+                                           else None),
         "norm_rope_fused_us_mean": round(times["fused"], 2),
         "norm_rope_fused_gbs": round(nbytes_fused / (times["fused"] * 1e-6) / 1e9, 1),
-        "norm_rope_two_pass_us_mean": round(times["two_pass"], 2),
+        "norm_rope_two_pass_us_mean": round(times["two_pass"], 2) if standalone else None,
         # the module-form RMSNorm alone (nn.py:338-355: x read, y written, no residual)
         "norm_module_us_mean": round(times["norm_only"], 2),
         "norm_module_gbs": round(nbytes_fused / (times["norm_only"] * 1e-6) / 1e9, 1),
