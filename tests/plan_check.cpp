@@ -107,14 +107,22 @@ int main() {
                   CHECK(b.lds_bytes == 0 || (b.rp.vec && b.rp.groups > 1),
                         "lds without a group combine");
                   // the fused-RoPE plan: same facts, its own block bound, and its step table
-                  // (dim floats of LDS) within 64 KiB
+                  // (dim floats of LDS) within 64 KiB; or, for rows no walk plan fits, the plain
+                  // plan with the rotation evaluated directly (no step table)
                   const BwdPlan br =
                       plan_bwd_rope(rows, dim, eb, aligned != 0, cus, prefer, max_block, waves);
                   check_row_plan(br.rp, dim, eb, aligned != 0);
-                  CHECK(!br.rp.vec || br.rp.block <= max_block_for_nv_rope(br.rp.nv),
-                        "rope block %d over its bound for nv %d", br.rp.block, br.rp.nv);
-                  CHECK(!br.rp.vec || dim * 4 <= 64 * 1024, "rope step table %lld floats",
-                        (long long)dim);
+                  if (br.rope_direct) {
+                    CHECK(br.rp.vec && br.rp.block <= max_block_for_nv(br.rp.nv) &&
+                              br.lds_bytes <= 64 * 1024,
+                          "rope direct block %d nv %d lds %zu", br.rp.block, br.rp.nv,
+                          br.lds_bytes);
+                  } else {
+                    CHECK(!br.rp.vec || br.rp.block <= max_block_for_nv_rope(br.rp.nv),
+                          "rope block %d over its bound for nv %d", br.rp.block, br.rp.nv);
+                    CHECK(!br.rp.vec || dim * 4 <= 64 * 1024, "rope step table %lld floats",
+                          (long long)dim);
+                  }
                   CHECK((size_t)br.wgs * (size_t)dim * sizeof(float) <= ws,
                         "rope partials %lld x %lld exceed workspace %zu", (long long)br.wgs,
                         (long long)dim, ws);

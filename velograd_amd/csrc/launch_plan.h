@@ -145,6 +145,9 @@ struct BwdPlan {
   int64_t wgs;       // workgroups = dweight partial rows
   size_t lds_bytes;  // dynamic LDS of the group combine
   bool ring = false; // the ring-pipelined kernel (plan_bwd_ring) instead of bwd_vec_kernel
+  // with the RoPE gradient: bwd_vec_kernel's plain plan, each pair's rotation evaluated directly
+  // where g is decoded (rows too wide for the RoPE walk's bound)
+  bool rope_direct = false;
 };
 
 // The ring-pipelined backward (bwd_ring_kernel): a ring of kRingPrefetch + 1 row buffers per
@@ -294,9 +297,18 @@ inline BwdPlan plan_bwd_rope(int64_t rows, int64_t dim, int elem_bytes, bool ali
       const RowPlan q = plan_rows(dim, elem_bytes, aligned, nv, kBwdOrderRope);
       if (q.vec && q.nv == nv && q.tpr <= max_block_for_nv_rope(nv)) rp = q;
     }
-    if (!rp.vec)
+    if (!rp.vec) {
+      // no chunk count fits the walk (rows of more than 1536 chunks): the plain plan with each
+      // pair's rotation evaluated where g is decoded, preferring four chunks per thread (248
+      // VGPRs in 512-thread rows; two chunks in 1024-thread rows spill), else the generic kernel
+      BwdPlan d = plan_bwd(rows, dim, elem_bytes, aligned, cus, 4, max_block, waves_per_cu);
+      if (d.rp.vec) {
+        d.rope_direct = true;
+        return d;
+      }
       return plan_bwd(rows, dim, elem_bytes, false, cus, prefer_nv, max_block,
                       waves_per_cu);  // generic
+    }
     prefer_nv = rp.nv;
   }
   int mb = max_block;

@@ -811,6 +811,9 @@ constexpr int kGradH = 2;
 // F.apply_rotary_emb(attention_norm(x)), models/llama.py:48-49), rotated back in registers
 // before use: the backward of the rotation (functional.py:316-345) fused into the norm's.
 constexpr int kRopeG = 4;
+// kRopeDirect: as kRopeG with each pair's rotation evaluated directly where g is decoded (both
+// passes), no walk state and no LDS table: rows too wide for the walk's launch bound.
+constexpr int kRopeDirect = 16;
 // Rows of the RoPE-gradient walk between direct evaluations of the rotation state.
 constexpr int kRopeAnchor = 16;
 
@@ -822,6 +825,8 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
   constexpr bool SAVED_IS_H = (FLAGS & kSavedIsH) != 0;
   constexpr bool HAS_GH = (FLAGS & kGradH) != 0;
   constexpr bool ROPE = (FLAGS & kRopeG) != 0;
+  constexpr bool RD = (FLAGS & kRopeDirect) != 0;
+  static_assert(!(ROPE && RD), "one RoPE mode");
   constexpr int NH = HAS_GH ? NV : 1;  // grad_h chunks (a dummy slot when absent)
   constexpr int P = V / 2;             // RoPE pairs per chunk
   constexpr int NR = ROPE ? NV : 1;    // rotation state slots (a dummy slot without RoPE)
@@ -914,10 +919,33 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
       }
     }
   };
+  // kRopeDirect: the current row's position, each chunk's first pair frequency (double) and
+  // the ratio between consecutive pairs' frequencies, base^(-2/dim)
+  int64_t rd_pos = 0;
+  double rd_f0[RD ? NV : 1], rd_ratio = 0.0;
+  if constexpr (RD) {
+    const double cc = (double)a.rope_c_hi + (double)a.rope_c_lo;
+    rd_ratio = exp2(-cc);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) rd_f0[k] = exp2(-(double)((lt + k * tpr) * P) * cc);
+  }
   // Decoded chunk k of the current row: g, xhat (h * inv_rms when h was saved), weight.
   auto decode = [&](const u32x4* gv, const u32x4* sv, float rr, int k, float* gf, float* xh,
                     float* wf) {
     C::unpack(gv[k], gf);
+    if constexpr (RD) {
+      // inverse rotation, each pair's (cos, sin) from its double angle (as rope_cos_sin)
+      double f = rd_f0[k];
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        float cs, sn;
+        rope_cos_sin_f(rd_pos, f, cs, sn);
+        f *= rd_ratio;
+        const float g0 = gf[2 * p], g1 = gf[2 * p + 1];
+        gf[2 * p] = g0 * cs + g1 * sn;
+        gf[2 * p + 1] = g1 * cs - g0 * sn;
+      }
+    }
     if constexpr (ROPE) {
       // inverse rotation of each pair (y0, y1) -> (y0 c + y1 s, y1 c - y0 s)
 #pragma unroll
@@ -944,6 +972,7 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
 
   for (int it = 0; it < a.iters; ++it) {
     const bool ok = row < a.rows;
+    if constexpr (RD) rd_pos = row % a.rope_seq;
     const int64_t nrow = row + nslots;
     u32x4 gn[NV], sn[NV], hn[NH];
     float rn = 0.0f;
@@ -1769,6 +1798,16 @@ void launch_bwd_flags(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
         hipLaunchKernelGGL((bwd_rope_ring_kernel<DT, WDT, 1>), grid, block, lds, st, a);
       return;
     }
+    if (b.rope_direct) {
+      constexpr int FD = (F & ~kRopeG) | kRopeDirect;
+      switch (p.nv) {
+        case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, FD>), grid, block, lds, st, a); break;
+        case 2: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 2, FD>), grid, block, lds, st, a); break;
+        case 3: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 3, FD>), grid, block, lds, st, a); break;
+        default: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 4, FD>), grid, block, lds, st, a); break;
+      }
+      return;
+    }
     // NV 4 is never planned with the RoPE gradient (max_block_for_nv_rope); it is not compiled
     switch (p.nv) {
       case 1: hipLaunchKernelGGL((bwd_vec_kernel<DT, WDT, 1, F>), grid, block, lds, st, a); break;
@@ -2039,15 +2078,17 @@ int32_t run_bwd(const void* grad_y, const void* saved, int32_t saved_is_h, const
   BwdPlan plan = plan_bwd(rows, dim, eb, aligned, cus, rope, rope_seq);
   // bwd_vec_kernel's RoPE walk keeps its step rotations (two floats per pair: dim floats) in the
   // same dynamic LDS as the group combine, one after the other.
-  if (rope && plan.rp.vec && !plan.ring) plan.lds_bytes = (size_t)dim * sizeof(float);
+  if (rope && plan.rp.vec && !plan.ring && !plan.rope_direct)
+    plan.lds_bytes = (size_t)dim * sizeof(float);
   if (!vg_plan::row_plan_valid(plan.rp, dim, eb) || plan.wgs < 1 || plan.wgs > INT32_MAX ||
       plan.lds_bytes > 64 * 1024 ||
       (plan.ring && !rope && (!vg_plan::ring_eligible(plan.rp, dim, eb) ||
                               plan.rp.block > vg_plan::kRingBlock)) ||
       (plan.ring && rope && (!vg_plan::rope_ring_eligible(plan.rp, dim, eb) ||
                              !vg_plan::rope_walk_ok(rows, plan.wgs * plan.rp.groups, rope_seq))) ||
-      (rope && plan.rp.vec && !plan.ring &&
-       plan.rp.block > vg_plan::max_block_for_nv_rope(plan.rp.nv)))
+      (rope && plan.rp.vec && !plan.ring && !plan.rope_direct &&
+       plan.rp.block > vg_plan::max_block_for_nv_rope(plan.rp.nv)) ||
+      (plan.rope_direct && (!rope || plan.rp.block > vg_plan::max_block_for_nv(plan.rp.nv))))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "bwd: internal launch plan rejected (dim=%lld)",
                 (long long)dim);
   const int64_t slots = plan.wgs * plan.rp.groups;  // row slots walking the rows
