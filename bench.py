@@ -450,9 +450,9 @@ def rope_timing(lib, tokens: int, stream, sets: int = 2, norm_rope: bool = True,
     out = {"rope_qk_us_mean": round(us, 2), "rope_qk_bytes": nbytes,
            "rope_qk_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
            "rope_workload": f"q [{tokens},32,128] + k [{tokens},8,128] bf16, theta 5e5"}
-    # velograd_rope rotates at most 8192 elements per token: wider rows have no standalone
-    # interleaved leg and no two-pass comparison
-    standalone = hid <= 8192
+    # velograd_rope rotates more than 8192 elements per token on 16-byte rows only (bf16 rows of
+    # a multiple of 8 elements): other wide rows have no standalone leg and no two-pass comparison
+    standalone = hid <= 8192 or hid % 8 == 0
     if standalone:
         for i in range(sets * 2):
             _lib.check(istep(i), "interleaved rope warm-up")

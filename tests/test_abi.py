@@ -252,7 +252,9 @@ def _rope(lib, **kw):
     (dict(rot_dim=63), _lib.ERR_INVALID_ARGUMENT, "must be even"),
     (dict(rot_dim=0), _lib.ERR_INVALID_ARGUMENT, "must be even"),
     (dict(rot_dim=66), _lib.ERR_INVALID_ARGUMENT, "<= dim"),
-    (dict(dim=16384, rot_dim=16384), _lib.ERR_INVALID_ARGUMENT, "<= 8192"),
+    (dict(dim=16384, rot_dim=16384), _lib.ERR_INVALID_ARGUMENT, "needs the interleaved"),
+    (dict(dim=16384, rot_dim=16384, pairing=1, x=8), _lib.ERR_INVALID_ARGUMENT,
+     "needs the interleaved"),
     (dict(x=None), _lib.ERR_INVALID_ARGUMENT, "must not be NULL"),
     (dict(theta=0.0), _lib.ERR_INVALID_ARGUMENT, "theta"),
     (dict(pairing=2), _lib.ERR_INVALID_ARGUMENT, "pairing"),

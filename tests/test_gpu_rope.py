@@ -154,6 +154,7 @@ def _interleaved_bound(x: np.ndarray, base: float) -> np.ndarray:
 
 INTERLEAVED_CASES = [(torch.float32, (37, 64)), (torch.bfloat16, (2, 128, 4096)),
                      (torch.float16, (3, 50, 256)), (torch.bfloat16, (1, 64, 8192)),
+                     (torch.bfloat16, (1, 64, 16384)),
                      (torch.float32, (3, 5, 6)), (torch.bfloat16, (2, 9, 12)),
                      (torch.float32, (2, 9, 12)), (torch.float32, (4, 2, 3, 40)),
                      # the scalar path at long positions (10 and 12 elements do not split into
@@ -206,7 +207,5 @@ def test_interleaved_rope_errors():
         vk.fused_rope_interleaved(torch.zeros(4, 7, device="cuda"))      # odd dim
     with pytest.raises(ValueError):
         vk.fused_rope_interleaved(torch.zeros(8, device="cuda"))         # no seq axis
-    with pytest.raises(ValueError):
-        vk.fused_rope_interleaved(torch.zeros(2, 16384, device="cuda"))  # wider than 8192
     with pytest.raises(TypeError):
         vk.fused_rope_interleaved(np.zeros((4, 8), np.float32))

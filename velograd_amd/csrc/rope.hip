@@ -372,10 +372,21 @@ VELOGRAD_API int32_t velograd_rope(const void* x, void* out, int64_t outer, int6
     clear_error();
     return 0;
   }
-  if (rot_dim < 2 || rot_dim % 2 != 0 || rot_dim > dim || rot_dim / 2 > kRopeMaxHalf)
+  if (rot_dim < 2 || rot_dim % 2 != 0 || rot_dim > dim)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
-                "rope: rot_dim=%lld must be even, >= 2, <= dim=%lld and <= %d",
-                (long long)rot_dim, (long long)dim, 2 * kRopeMaxHalf);
+                "rope: rot_dim=%lld must be even, >= 2 and <= dim=%lld", (long long)rot_dim,
+                (long long)dim);
+  // The table kernels hold one token's frequencies and (cos, sin) in LDS: rot_dim <= 8192.  The
+  // interleaved pairing on 16-byte chunks walks positions without tables (rope_run_kernel), so it
+  // takes any rot_dim (a whole hidden vector of 16384, say).
+  const int vec_chunk = 16 / eb;
+  const bool run_path = pairing == VELOGRAD_ROPE_INTERLEAVED && aligned16(x) && aligned16(out) &&
+                        dim % vec_chunk == 0 && rot_dim % vec_chunk == 0;
+  if (rot_dim / 2 > kRopeMaxHalf && !run_path)
+    return fail(VELOGRAD_ERR_INVALID_ARGUMENT,
+                "rope: rot_dim=%lld above %d needs the interleaved pairing on 16-byte aligned, "
+                "16-byte multiple rows",
+                (long long)rot_dim, 2 * kRopeMaxHalf);
   if (x == nullptr || out == nullptr)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "rope: x and out must not be NULL");
   if (!(theta > 0.0f))
@@ -401,7 +412,7 @@ VELOGRAD_API int32_t velograd_rope(const void* x, void* out, int64_t outer, int6
   // Tokens per workgroup: about kRopeTargetElems elements, bounded by the LDS tables
   // (freq[half] + cos/sin[tpb][half]) and by the items a workgroup indexes in int32.
   int64_t tpb = (kRopeTargetElems + tok_elems - 1) / tok_elems;
-  const int64_t lds_cap = (kRopeLdsFloats - a.half) / (2 * a.half);
+  const int64_t lds_cap = a.half <= kRopeMaxHalf ? (kRopeLdsFloats - a.half) / (2 * a.half) : 1;
   if (tpb > lds_cap) tpb = lds_cap;
   if (tpb > 64) tpb = 64;
   if (tpb < 1) tpb = 1;

@@ -602,7 +602,8 @@ def fused_rope_interleaved(x: torch.Tensor, base: float = 10000.0,
     input with it) and src/ops.rs:465-499.  x is [..., seq, dim]: positions run along axis -2,
     the pairs (x_2i, x_2i+1) of the whole last axis rotate by pos * base^(-2i / dim).
     `inverse=True` rotates back: the backward (functional.py:316-345, ops.rs:501-530).  Returns
-    a new tensor in x's dtype; device tensors only, dim even and at most 8192."""
+    a new tensor in x's dtype; device tensors only, dim even (above 8192 the rows must be
+    16-byte aligned, as contiguous torch allocations are)."""
     if not _is_device_tensor(x):
         raise TypeError("fused_rope_interleaved takes torch tensors on a ROCm device")
     if x.dim() < 2:
