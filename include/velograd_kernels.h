@@ -280,8 +280,9 @@ VELOGRAD_API size_t velograd_rmsnorm_residual_bwd_workspace_bytes(int64_t rows, 
  *
  *   x, out   : [outer, seq, heads, dim] contiguous in `dtype`; out may be x itself (in place)
  *              but must not otherwise overlap it.
- *   rot_dim  : the rotated width (the reference's head_dim): even, 2 <= rot_dim <= dim,
- *              rot_dim <= 8192.
+ *   rot_dim  : the rotated width (the reference's head_dim): even, 2 <= rot_dim <= dim;
+ *              rot_dim <= 8192 unless the pairing is interleaved on 16-byte aligned rows of a
+ *              16-byte multiple (any rot_dim there).
  *   theta    : the frequency base (> 0).
  *   inverse  : nonzero rotates by -angle: the backward (grad_x from grad_out), the rotary
  *              backward of src/ops.rs:501-530 and functional.py:316-345.
