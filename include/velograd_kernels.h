@@ -212,9 +212,11 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
  *   Arguments and results as velograd_rmsnorm_residual_bwd (same kernels, so bitwise the same
  *   outputs), minus `workspace` and `ws_bytes`.
  *   Limit: returns VELOGRAD_ERR_WORKSPACE_TOO_SMALL, launching nothing, when dweight would
- *   need more than the 16 MiB, i.e. one fp32 row of dim per partial: 256 partials on a 256-CU
- *   MI355X for 16-byte-aligned bf16/fp16 rows up to dim 16384 (fp32 up to 4096), and up to
- *   min(rows, 4 per CU) partials on the generic path (unaligned or odd-sized rows).
+ *   need more than the 16 MiB, i.e. one fp32 row of dim per partial.  With the default launch
+ *   plans on a 256-CU MI355X that is 256 partials for 16-byte-aligned rows up to dim 16384
+ *   bf16/fp16 or 8192 fp32, and up to min(rows, 4 per CU) partials on the generic path
+ *   (unaligned or odd-sized rows: dim up to 4096 at 1024 or more rows).  The VELOGRAD_BWD_*
+ *   tuning variables change the plans, and with them which shapes are refused.
  *   Calls that overlap on one GPU (several streams or host threads at once) share the scratch
  *   and race: serialise them.  The scratch keeps the last call's contents; nothing in it has
  *   to start at zero.

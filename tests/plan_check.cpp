@@ -244,6 +244,59 @@ int main() {
             "fwd_rope_walk_rows rows=%lld tpr=%d -> %d", (long long)rows, tpr, w);
     }
   }
+  // Wide norm + RoPE rows (tests/test_gpu_rmsnorm_rope.py): the backward's walk takes three
+  // chunks per thread up to 1536 chunks; past that the plain plan with each pair's rotation
+  // evaluated directly, two chunks per thread in 832-thread rows at 1540 chunks and four in
+  // 512-thread rows at 2048; the forward's direct rows take three or four chunks per thread in
+  // 512-thread rows when VELOGRAD_FWD_NV asks for them.
+  {
+    const BwdPlan a = plan_bwd_rope(64, 12288, 2, true, 256, 0, 1024, 16);
+    CHECK(a.rp.vec && !a.rope_direct && a.rp.nv == 3 && a.rp.tpr == 512, "rope bwd 12288");
+    const BwdPlan b = plan_bwd_rope(64, 12320, 2, true, 256, 0, 1024, 16);
+    CHECK(b.rp.vec && b.rope_direct && b.rp.nv == 2 && b.rp.tpr == 832 &&
+              b.rp.block <= max_block_for_nv(2),
+          "rope bwd 12320: direct %d nv %d tpr %d", (int)b.rope_direct, b.rp.nv, b.rp.tpr);
+    const BwdPlan c = plan_bwd_rope(64, 16384, 2, true, 256, 0, 1024, 16);
+    CHECK(c.rp.vec && c.rope_direct && c.rp.nv == 4 && c.rp.tpr == 512, "rope bwd 16384");
+    const RowPlan f3 = plan_rows(12288, 2, true, 3, kFwdOrder);
+    CHECK(f3.vec && f3.nv == 3 && f3.tpr == 512 && f3.block <= max_block_for_nv(3),
+          "fwd nv 3 at 12288: nv %d tpr %d", f3.nv, f3.tpr);
+    const RowPlan f4 = plan_rows(16384, 2, true, 4, kFwdOrder);
+    CHECK(f4.vec && f4.nv == 4 && f4.tpr == 512 && f4.block <= max_block_for_nv(4),
+          "fwd nv 4 at 16384: nv %d tpr %d", f4.nv, f4.tpr);
+    const RowPlan f4s = plan_rows(8192, 4, true, 4, kFwdOrder);
+    CHECK(f4s.vec && f4s.nv == 4 && f4s.tpr == 512, "fwd nv 4 at fp32 8192");
+  }
+  // The allocation-free backward refuses fp32 2048 x 16384 (tests/test_zz_no_alloc.py): on 256
+  // CUs with the default tuning, every plan the backward can pick for that shape (aligned or
+  // not, with or without the ring) needs more partial rows than its 16 MiB scratch holds, while
+  // fp32 8192 (its documented bound) fits.
+  {
+    const int64_t rows = 2048, dim = 16384;
+    const size_t scratch = (size_t)16 << 20;
+    for (int aligned = 0; aligned < 2; ++aligned) {
+      const BwdPlan b = plan_bwd(rows, dim, 4, aligned != 0, 256, 0, 1024, 16);
+      CHECK((size_t)b.wgs * dim * sizeof(float) > scratch,
+            "no-alloc refusal shape plans %lld partial rows, within the scratch",
+            (long long)b.wgs);
+      const BwdPlan rg = plan_bwd_ring(rows, dim, 4, aligned != 0, 256, 0);
+      CHECK(!rg.ring, "no-alloc refusal shape got a ring plan");
+    }
+    // the bounds the header states, on the plans the backward picks (no RoPE): 16-byte aligned
+    // rows up to 8192 fp32 or 16384 bf16/fp16 elements, other rows up to 4096
+    for (int64_t r : {1, 64, 2048, 16384, 262144}) {
+      for (int eb = 2; eb <= 4; eb += 2) {
+        for (int aligned = 0; aligned < 2; ++aligned) {
+          const int64_t dim = aligned ? (eb == 4 ? 8192 : 16384) : 4096;
+          const BwdPlan rg = plan_bwd_ring(r, dim, eb, aligned != 0, 256, 0);
+          const BwdPlan b = rg.ring ? rg : plan_bwd(r, dim, eb, aligned != 0, 256, 0, 1024, 16);
+          CHECK((size_t)b.wgs * dim * sizeof(float) <= scratch,
+                "no-alloc bound: eb %d aligned %d dim %lld rows %lld plans %lld partial rows",
+                eb, aligned, (long long)dim, (long long)r, (long long)b.wgs);
+        }
+      }
+    }
+  }
   if (failures) {
     fprintf(stderr, "%d failures over %ld plans\n", failures, plans);
     return 1;

@@ -221,9 +221,11 @@ BWD_CASES = [(torch.bfloat16, (2, 64, 4096), True), (torch.bfloat16, (1, 128, 81
              (torch.float16, (2, 512, 6144), True),
              (torch.bfloat16, (6, 1000, 4096), True), (torch.bfloat16, (3, 1000, 8192), True),
              # wider rows: bwd_vec_kernel's walk with three chunks per thread (1280 and 1536
-             # chunks), then the generic kernel (2048 chunks)
+             # chunks); then rows no walk plan fits, bwd_vec_kernel with each pair's rotation
+             # evaluated where g is decoded: 1540 chunks as two per thread in 832-thread rows,
+             # 2048 chunks as four per thread in 512-thread rows
              (torch.bfloat16, (1, 300, 10240), False), (torch.bfloat16, (2, 256, 12288), True),
-             (torch.bfloat16, (1, 64, 16384), True)]
+             (torch.bfloat16, (1, 64, 12320), True), (torch.bfloat16, (1, 64, 16384), True)]
 
 
 @pytest.mark.parametrize("dtype,shape,with_w", BWD_CASES,
@@ -398,3 +400,36 @@ def test_backward_errors():
         vk.rmsnorm_rope_backward(g, g, None, inv, base=-1.0)                       # base
     with pytest.raises(TypeError):
         vk.rmsnorm_rope_backward(np.zeros((2, 4, 8), np.float32), g, None, inv)
+
+
+_FORWARD_NV_CHILD = r'''
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from tests.test_gpu_rmsnorm_rope import test_fused_norm_rope_matches_the_oracle_composition as t
+dt = {"bf16": torch.bfloat16, "fp32": torch.float32}[sys.argv[2]]
+shape = tuple(int(v) for v in sys.argv[3].split("x"))
+for with_res in (False, True):
+    for base in (10000.0, 500000.0):
+        t(dt, shape, with_res, base)
+print("forward-nv ok", flush=True)
+'''
+
+
+@pytest.mark.parametrize("nv,dtype,shape", [(3, "bf16", "1x64x12288"), (4, "bf16", "1x64x16384"),
+                                            (4, "fp32", "2x16x8192")])
+def test_fused_forward_three_and_four_chunks_per_thread(nv, dtype, shape):
+    """The one-shot rows with each pair's rotation evaluated directly at three and four chunks
+    per thread (512-thread rows).  The default plans take two chunks per thread up to 2048
+    chunks, so these layouts run only under VELOGRAD_FWD_NV, read once per process: a child
+    process with it set runs the oracle comparison above on rows of 1536 and 2048 chunks."""
+    import os
+    import subprocess
+    import sys
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print(f"child: VELOGRAD_FWD_NV={nv} rmsnorm_rope forward {dtype} {shape}", flush=True)
+    env = dict(os.environ, VELOGRAD_FWD_NV=str(nv))
+    out = subprocess.run([sys.executable, "-c", _FORWARD_NV_CHILD, repo, dtype, shape], env=env,
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, (out.stdout[-2000:], out.stderr[-4000:])
+    assert "forward-nv ok" in out.stdout

@@ -105,13 +105,23 @@ def test_noalloc_without_dweight_matches():
 
 def test_noalloc_refuses_sizes_beyond_the_scratch():
     lib = _lib.load()
-    # fp32 rows of 16384 take the generic kernel: 1024 partial rows of 64 KiB = 64 MiB
+    # fp32 rows of 16384: every plan the backward can pick needs more than 16 MiB of partial
+    # rows (checked on the CPU in tests/plan_check.cpp).  The buffers are real device tensors of
+    # the stated shape, so a refusal that regressed would compute on valid memory and fail the
+    # return-code assertion instead of touching invalid addresses.
     rows, dim = 2048, 16384
     assert vk.bwd_workspace_bytes(rows, dim, DEV) > SCRATCH_BYTES
+    g = torch.zeros(rows, dim, device=DEV, dtype=torch.float32)
+    h = torch.zeros_like(g)
+    dx = torch.empty_like(g)
+    w = torch.ones(dim, device=DEV, dtype=torch.float32)
+    inv = torch.ones(rows, device=DEV, dtype=torch.float32)
+    dw = torch.empty(dim, device=DEV, dtype=torch.float32)
     stream = torch.cuda.current_stream().cuda_stream
     rc = lib.velograd_rmsnorm_residual_bwd_noalloc(
-        16, 48, 1, 64, 80, None, 96, None, 112, rows, dim, dim, dim, dim, dim, dim,
-        _lib.DTYPE_F32, _lib.DTYPE_F32, stream)
+        _p(g), _p(h), 1, _p(w), _p(inv), None, _p(dx), None, _p(dw), rows, dim, dim, dim, dim,
+        dim, dim, _lib.DTYPE_F32, _lib.DTYPE_F32, stream)
+    torch.cuda.synchronize()
     assert rc == _lib.ERR_WORKSPACE_TOO_SMALL
     msg = _lib.last_error()
     assert "fixed maximum" in msg and str(SCRATCH_BYTES) in msg, msg
@@ -150,3 +160,60 @@ def test_noalloc_graph_replays_equal_eager():
         torch.cuda.synchronize()
         assert torch.equal(dx, want[0]), f"replay {rep}: dx differs"
         assert torch.equal(dw, want[2]), f"replay {rep}: dweight differs"
+
+
+_FIRST_CALL_UNDER_CAPTURE = r'''
+import ctypes, sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+from velograd_amd import _lib
+from velograd_amd import kernels as vk
+lib = _lib.load()
+dev = torch.device("cuda", 0)
+rows, dim = 1024, 4096
+gen = torch.Generator(device=dev).manual_seed(7)
+g = torch.randn(rows, dim, device=dev, generator=gen).to(torch.bfloat16)
+h = torch.randn(rows, dim, device=dev, generator=gen).to(torch.bfloat16)
+w = (1 + 0.1 * torch.randn(dim, device=dev, generator=gen)).to(torch.bfloat16)
+inv = torch.rand(rows, device=dev, generator=gen) + 0.5
+dx = torch.empty_like(g)
+dw = torch.empty(dim, device=dev, dtype=torch.float32)
+code = _lib.DTYPE_BF16
+torch.cuda.synchronize()
+side = torch.cuda.Stream()
+graph = torch.cuda.CUDAGraph()
+# the library's first call of the process (and so its first look-up of the scratch address)
+# is made while the stream is being captured
+with torch.cuda.stream(side):
+    with torch.cuda.graph(graph, stream=side):
+        rc = lib.velograd_rmsnorm_residual_bwd_noalloc(
+            g.data_ptr(), h.data_ptr(), 1, w.data_ptr(), inv.data_ptr(), None, dx.data_ptr(),
+            None, dw.data_ptr(), rows, dim, dim, dim, dim, dim, dim, code, code,
+            ctypes.c_void_p(side.cuda_stream))
+_lib.check(rc, "first call under capture")
+want_dx, want_dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv.view(rows, 1), saved_is_h=True)
+for rep in range(3):
+    dx.fill_(float("nan"))
+    dw.fill_(float("nan"))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(dx, want_dx), f"replay {rep}: dx differs"
+    assert torch.equal(dw, want_dw), f"replay {rep}: dweight differs"
+print("first-call-under-capture ok", flush=True)
+'''
+
+
+def test_noalloc_first_call_of_the_process_under_capture():
+    """A fresh process whose first library call is a no-alloc backward inside HIP graph capture
+    (the scratch address is looked up there): the replays equal the workspace entry point."""
+    import os
+    import subprocess
+    import sys
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("child: first no-alloc call under graph capture, bf16 1024 x 4096", flush=True)
+    out = subprocess.run([sys.executable, "-c", _FIRST_CALL_UNDER_CAPTURE, repo],
+                         capture_output=True, text=True, timeout=240)
+    assert out.returncode == 0, (out.stdout[-2000:], out.stderr[-4000:])
+    assert "first-call-under-capture ok" in out.stdout
