@@ -60,6 +60,12 @@ def bwd_bytes(rows: int, d: int, s: int) -> int:
     return 3 * rows * d * s + d * s + 4 * rows + 4 * d
 
 
+def bwd_grad_h_bytes(rows: int, d: int, s: int) -> int:
+    """Backward with the residual-stream gradient (the training path): read grad_y, h and
+    grad_h, write dx; plus weight, inv_rms and fp32 dweight."""
+    return 4 * rows * d * s + d * s + 4 * rows + 4 * d
+
+
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -92,6 +98,10 @@ def parse_args(argv=None):
                    help="skip the PyTorch eager comparison and the reference benchmark's shapes")
     p.add_argument("--no-copy-ceiling", action="store_true",
                    help="skip the same-run stream-probe ceilings")
+    p.add_argument("--probe-sweep", action="store_true",
+                   help="instead of the benchmark: sweep the stream probe's shapes over the "
+                        "config's tensors and print a markdown table of the byte patterns' "
+                        "ceilings")
     return p.parse_args(argv)
 
 
@@ -185,14 +195,32 @@ def cpu_baseline(rows: int, d: int, s: int, eps: float, budget_s: float, with_bw
     }
 
 
+def traffic_file(config: str) -> str:
+    return os.path.join(REPO, "profiles", f"pmc_traffic_config_{config}.json")
+
+
 def load_traffic(config: str, which: str = "fwd"):
-    """HBM bytes per launch of the forward (`which` = "fwd") or of the backward's two stages
-    ("bwd") from the committed rocprofv3 PMC summary of `config`, or None."""
-    path = os.path.join(REPO, "profiles", f"pmc_traffic_config_{config}.json")
+    """HBM bytes per launch of the forward (`which` = "fwd"), of the backward's two stages
+    ("bwd") or of the backward with grad_h ("bwd_grad_h") from the committed rocprofv3 PMC
+    summary of `config`, or None."""
+    path = traffic_file(config)
     if not os.path.exists(path):
         return None
     with open(path) as f:
         return json.load(f).get(f"{which}_traffic_bytes_per_launch")
+
+
+def traffic_source(config: str):
+    """The file `roofline.traffic` is read from and the sha256 of its bytes (the commit that
+    last changed it holds the same bytes), or None."""
+    import hashlib
+
+    path = traffic_file(config)
+    if not os.path.exists(path):
+        return None
+    with open(path, "rb") as f:
+        digest = hashlib.sha256(f.read()).hexdigest()[:16]
+    return {"file": os.path.relpath(path, REPO), "sha256_16": digest}
 
 
 def stream_ceilings(sets, stream_bytes: int, stream) -> dict:
@@ -219,7 +247,8 @@ def stream_ceilings(sets, stream_bytes: int, stream) -> dict:
                                           ("fwd_pattern", 1, 4, ("x", "res", "y", "h")),
                                           ("bwd_pattern", 2, 3, ("x", "res", "y", None)),
                                           ("read_only", 3, 2, ("x", "res", "y", None)),
-                                          ("write_only", 4, 2, ("x", None, "y", "h"))):
+                                          ("write_only", 4, 2, ("x", None, "y", "h")),
+                                          ("grad_h_pattern", 5, 4, ("x", "res", "y", "h"))):
         def run(i):
             b = sets[i % len(sets)]
             ptrs = [b[k].data_ptr() if k else None for k in keys]
@@ -688,6 +717,15 @@ def measure(lib, config: str, steps: int, warmup: int, nsets: int, kernel_events
 
     fwd_batch_ms, nbatched = batch_mean_ms(fwd_fn, fwd_args)
     bwd_batch_ms = batch_mean_ms(bwd_fn, bwd_args)[0] if with_bwd else None
+    gh_batch_ms = None
+    if with_bwd:
+        # the training path's backward: the residual-stream gradient grad_h (here the set's x)
+        # read too and summed into dx in the same pass
+        gh_args = [(b["g"].data_ptr(), b["h"].data_ptr(), 1, b["w"].data_ptr(),
+                    b["inv"].data_ptr(), b["x"].data_ptr(), b["dx"].data_ptr(), None,
+                    b["dw"].data_ptr(), b["ws"].data_ptr(), ws_bytes, rows, d, d, d, d, d, d,
+                    code, code, sp) for b in sets]
+        gh_batch_ms = batch_mean_ms(bwd_fn, gh_args)[0]
 
     for k in range(warmup):
         _lib.check(step(k), "warm-up step")
@@ -733,6 +771,8 @@ def measure(lib, config: str, steps: int, warmup: int, nsets: int, kernel_events
             "bwd_gbs": round(bb / (mean_bwd_ms * 1e-3) / 1e9, 1),
             "bwd_bytes": bb,
             "bwd_workspace_bytes": ws_bytes,
+            "bwd_grad_h_us_mean": round(gh_batch_ms * 1e3, 2),
+            "bwd_grad_h_bytes": bwd_grad_h_bytes(rows, d, s),
         })
     out["rows_per_s"] = round(rows / (ms_per_step * 1e-3), 1)
     out["pct_hbm_peak"] = round(100.0 * value / HBM_PEAK_GBS, 2)
@@ -843,12 +883,140 @@ def other_configs(lib, main_config: str, stream) -> dict:
     return out
 
 
+PROBE_PATTERNS = (("2R2W", 2, 2), ("2R1W", 2, 1), ("3R1W", 3, 1), ("1R1W", 1, 1),
+                  ("2R0W", 2, 0), ("0R2W", 0, 2))
+
+
+def probe_sweep(config: str, nsets: int = 4, reps: int = 12, rounds: int = 3) -> str:
+    """The stream probe's shapes (velograd_stream_probe_shape) over the config's tensors, four
+    per set (the forward's x, residual, h, y), rotating over `nsets` sets: each byte pattern with
+    the bench's shape, every workgroup size x vectors per thread x bytes per lane one-pass, the
+    bench's and the best one-pass shape on persistent grids, each load/store cache policy, and
+    the second write stream unrotated, each in guarded and flat code (the probe's two code
+    styles: a branch around each access, or none in whole tiles).  Per shape the best of
+    `rounds` batches of `reps`
+    back-to-back launches, HIP events around each batch.  Returns a markdown table."""
+    import ctypes
+
+    import torch
+
+    from velograd_amd.build import PROBE_LIB_PATH
+
+    lib = ctypes.CDLL(PROBE_LIB_PATH)
+    fn = lib.velograd_stream_probe_shape
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+                   ctypes.c_int64] + [ctypes.c_int32] * 5 + [ctypes.c_void_p]
+    fixed = lib.velograd_stream_probe
+    fixed.restype = ctypes.c_int32
+    fixed.argtypes = [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p]
+    fixed_pattern = {"2R2W": 1, "2R1W": 2, "3R1W": 5, "1R1W": 0, "2R0W": 3, "0R2W": 4}
+    rows, d, _, _ = CONFIGS[config]
+    s = 2 if config != "A" else 4
+    nbytes = rows * d * s
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    sets = [[torch.empty(nbytes, device=dev, dtype=torch.uint8).random_(0, 256)
+             for _ in range(4)] for _ in range(nsets)]
+    ptr_arrays = []
+    for bufs in sets:
+        rd = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in bufs[:3]])
+        wr = (ctypes.c_void_p * 2)(bufs[3].data_ptr(), bufs[2].data_ptr())
+        ptr_arrays.append((rd, wr))
+    n16 = nbytes // 16
+    base = dict(block=256, vpt=2, lane=16, wpc=0, flags=7)
+
+    def time_shape(nr, nw, block, vpt, lane, wpc, flags, pattern=None):
+        def launch(i):
+            rd, wr = ptr_arrays[i % nsets]
+            if pattern is not None:  # the bench's own ceiling kernel
+                bufs = sets[i % nsets]
+                rc = fixed(pattern, bufs[0].data_ptr(), bufs[1].data_ptr(), bufs[3].data_ptr(),
+                           bufs[2].data_ptr(), n16, stream.cuda_stream)
+            else:
+                rc = fn(nr, nw, ctypes.cast(rd, ctypes.c_void_p),
+                        ctypes.cast(wr, ctypes.c_void_p), n16, block, vpt, lane, wpc, flags,
+                        stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"probe shape failed: rc {rc}")
+        for i in range(nsets):
+            launch(i)
+        best = float("inf")
+        for _ in range(rounds):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(reps):
+                launch(i)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / reps)
+        return best
+
+    lines = [f"Stream-probe sweep over config {config}'s tensors ({nbytes} B per stream, "
+             f"{nsets} rotating sets of 4 streams), best of {rounds} batches of {reps} "
+             "launches. µs per launch and TB/s of the streams' bytes; 'bench shape' = the "
+             "bench's own ceiling kernel (velograd_stream_probe: 256 threads, 2 vectors, 16 B "
+             "per lane, one pass, nt loads and stores, second write stream rotated); the other "
+             "rows are velograd_stream_probe_shape.", "",
+             "| pattern | block | vectors/thread | B/lane | grid | loads | stores | rotate | "
+             "code | µs | TB/s |", "|---|---:|---:|---:|---|---|---|---|---|---:|---:|"]
+    summary = []
+    for name, nr, nw in PROBE_PATTERNS:
+        nstreams = nr + nw
+        results = []
+
+        def run(block, vpt, lane, wpc, flags):
+            us = time_shape(nr, nw, block, vpt, lane, wpc, flags)
+            tbs = nstreams * nbytes / (us * 1e-6) / 1e12
+            results.append((us, block, vpt, lane, wpc, flags))
+            lines.append(f"| {name} | {block} | {vpt} | {lane} | "
+                         f"{'one pass' if wpc == 0 else f'{wpc}/CU persistent'} | "
+                         f"{'nt' if flags & 1 else 'plain'} | {'nt' if flags & 2 else 'plain'} | "
+                         f"{'yes' if (flags & 4 and nw == 2 and vpt >= 2) else '-'} | "
+                         f"{'flat' if flags & 8 else 'guarded'} | {us:.2f} | {tbs:.3f} |")
+            print(lines[-1], flush=True)
+
+        bench_us = time_shape(nr, nw, **base, pattern=fixed_pattern[name])
+        results.append((bench_us, 256, 2, 16, 0, 7))
+        lines.append(f"| {name} | 256 | 2 | 16 | one pass | nt | nt | "
+                     f"{'yes' if nw == 2 else '-'} | the bench's ceiling kernel | "
+                     f"{bench_us:.2f} | {nstreams * nbytes / (bench_us * 1e-6) / 1e12:.3f} |")
+        print(lines[-1], flush=True)
+        for style in (0, 8):
+            for block in (256, 512, 1024):
+                for vpt in (1, 2, 4):
+                    for lane in (16, 32):
+                        run(block, vpt, lane, 0, 7 | style)
+        one_pass_best = min(results, key=lambda r: r[0])
+        for shape in {(256, 2, 16, 7), (one_pass_best[1], one_pass_best[2], one_pass_best[3],
+                                         one_pass_best[5])}:
+            for wpc in (1, 2, 4, 8):
+                if shape[0] * wpc <= 2048:
+                    run(shape[0], shape[1], shape[2], wpc, shape[3])
+        for flags in (6, 5, 4):
+            run(256, 2, 16, 0, flags)
+        if nw == 2:
+            run(256, 2, 16, 0, 3)
+        best = min(results, key=lambda r: r[0])
+        summary.append(f"| {name} | {bench_us:.2f} | {nstreams * nbytes / (bench_us * 1e-6) / 1e12:.3f} | "
+                       f"{best[0]:.2f} | {nstreams * nbytes / (best[0] * 1e-6) / 1e12:.3f} | "
+                       f"{best[1]} thr, {best[2]} vec, {best[3]} B/lane, "
+                       f"{'one pass' if best[4] == 0 else f'{best[4]}/CU'}, "
+                       f"{'flat' if best[5] & 8 else 'guarded'}, flags {best[5] & 7} |")
+    out = lines + ["", "| pattern | bench shape µs | TB/s | best µs | TB/s | best shape |",
+                   "|---|---:|---:|---:|---:|---|"] + summary
+    return "\n".join(out)
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus "
               f"{args.gpus}", file=sys.stderr)
         return 2
+    if args.probe_sweep:
+        print(probe_sweep(args.config), flush=True)
+        return 0
 
     import torch
 
@@ -878,6 +1046,13 @@ def main(argv=None) -> int:
             "achieved": round(bw_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(bw_gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(args.config, "bwd"),
             "us_mean": m["bwd_us_mean"], "us_event_median": m["bwd_us_event_median"]}
+        gh_gbs = m["bwd_grad_h_bytes"] / (m["bwd_grad_h_us_mean"] * 1e-6) / 1e9
+        extra["roofline_bwd_grad_h"] = {
+            "bound": "hbm", "kernel": "bwd_ring_kernel (grad_h) + dweight_reduce_kernel",
+            "achieved": round(gh_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gh_gbs / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic(args.config, "bwd_grad_h"),
+            "us_mean": m["bwd_grad_h_us_mean"]}
     cpu_inputs = None
     if args.cpu_seconds > 0:
         b0 = sets[0]
@@ -894,6 +1069,10 @@ def main(argv=None) -> int:
                 t_ideal += bb / (ceil["ceiling_bwd_pattern_gbs"] * 1e9)
             extra["ceiling_step_gbs"] = round((fb + bb) / t_ideal / 1e9, 1)
             extra["frac_of_ceiling"] = round(value / extra["ceiling_step_gbs"], 4)
+            if with_bwd and "roofline_bwd_grad_h" in extra:
+                extra["roofline_bwd_grad_h"]["frac_of_3r1w_probe"] = round(
+                    extra["roofline_bwd_grad_h"]["achieved"] / ceil["ceiling_grad_h_pattern_gbs"],
+                    4)
 
     # Warm-MALL figure (informational): the same step repeated on one buffer set, whose
     # 768 MiB exceed the 256 MiB MALL only partly.
@@ -964,6 +1143,7 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(fb / (mean_fwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": load_traffic(args.config),
+            "traffic_source": traffic_source(args.config),
             "us_mean": m["fwd_us_mean"],
             "launches": m["batched_launches"],
         },
