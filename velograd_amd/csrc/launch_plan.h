@@ -194,19 +194,27 @@ inline bool ring_eligible(const RowPlan& p, int64_t dim, int elem_bytes) {
 // Plan of the ring-pipelined backward: row groups packed into workgroups of up to kRingBlock
 // threads, one workgroup per CU.  `ring` is false (and the plan unusable) when the row layout
 // does not suit it; the caller then plans bwd_vec_kernel.
+// `max_block` (at most kRingBlock) bounds the workgroup and `wgs_per_cu` (1 or 2) sets the
+// resident workgroups per CU: two 256-thread workgroups per CU hold the same waves as one of 512
+// (the ring's registers allow eight waves per CU) without sharing a barrier.
 inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
-                             int prefer_nv) {
+                             int prefer_nv, int max_block = kRingBlock, int wgs_per_cu = 1) {
   BwdPlan b;
   b.rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrder);
   b.wgs = 0;
   b.lds_bytes = 0;
-  b.ring = ring_eligible(b.rp, dim, elem_bytes);
+  if (max_block > kRingBlock) max_block = kRingBlock;
+  if (wgs_per_cu < 1) wgs_per_cu = 1;
+  if (wgs_per_cu > 2) wgs_per_cu = 2;
+  b.ring = ring_eligible(b.rp, dim, elem_bytes) && b.rp.tpr <= max_block;
   if (!b.ring) return b;
+  if (b.rp.tpr * wgs_per_cu > kRingBlock) wgs_per_cu = 1;  // a row group fills the CU's waves
   RowPlan& p = b.rp;
-  p.groups = kRingBlock / p.tpr;
+  p.groups = max_block / p.tpr;
+  if (p.groups * wgs_per_cu * p.tpr > kRingBlock) p.groups = kRingBlock / (wgs_per_cu * p.tpr);
   p.block = p.tpr * p.groups;
   const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
-  int64_t wgs = cus > 0 ? cus : 1;
+  int64_t wgs = cus > 0 ? (int64_t)cus * wgs_per_cu : 1;
   if (wgs > wgs_needed) wgs = wgs_needed;
   b.wgs = wgs;
   b.lds_bytes = p.groups > 1 ? (size_t)dim * sizeof(float) : 0;
@@ -340,7 +348,8 @@ inline int fwd_rope_walk_rows(int64_t rows, int tpr) {
 // pointer alignment and on whether the RoPE gradient is fused, which a size query does not know,
 // so this is the largest need over every plan the backward can pick for (rows, dim).
 inline size_t bwd_workspace_bytes(int64_t rows, int64_t dim, int cus, int prefer_nv,
-                                  int max_block, int waves_per_cu) {
+                                  int max_block, int waves_per_cu, int ring_block = kRingBlock,
+                                  int ring_wgs_per_cu = 1) {
   if (rows <= 0 || dim <= 0 || cus <= 0) return 0;
   int64_t most = 0;
   const int sizes[2] = {2, 4};
@@ -352,7 +361,8 @@ inline size_t bwd_workspace_bytes(int64_t rows, int64_t dim, int cus, int prefer
       const int64_t nr = plan_bwd_rope(rows, dim, sizes[si], al != 0, cus, prefer_nv, max_block,
                                        waves_per_cu).wgs;
       if (nr > most) most = nr;
-      const BwdPlan rg = plan_bwd_ring(rows, dim, sizes[si], al != 0, cus, prefer_nv);
+      const BwdPlan rg = plan_bwd_ring(rows, dim, sizes[si], al != 0, cus, prefer_nv,
+                                       ring_block, ring_wgs_per_cu);
       if (rg.ring && rg.wgs > most) most = rg.wgs;
       const BwdPlan rr = plan_bwd_rope_ring(rows, dim, sizes[si], al != 0, cus);
       if (rr.ring && rr.wgs > most) most = rr.wgs;

@@ -1638,6 +1638,8 @@ struct Tuning {
   int bwd_waves_per_cu;   // resident waves per CU targeted by the persistent backward grid
   int bwd_block;          // upper bound on backward workgroup size (row groups per workgroup)
   int bwd_ring;           // 1: the ring-pipelined backward where the rows suit it
+  int ring_block;         // upper bound on the ring backward's workgroup size
+  int ring_wgs_per_cu;    // ring backward workgroups per CU (1 or 2)
 };
 
 const Tuning& tuning() {
@@ -1647,6 +1649,8 @@ const Tuning& tuning() {
       env_int("VELOGRAD_BWD_WAVES_PER_CU", 16, 1, 64),
       env_int("VELOGRAD_BWD_BLOCK", 1024, 64, 1024),
       env_int("VELOGRAD_BWD_RING", 1, 0, 1),
+      env_int("VELOGRAD_BWD_RING_BLOCK", vg_plan::kRingBlock, 64, vg_plan::kRingBlock),
+      env_int("VELOGRAD_BWD_RING_WGS_PER_CU", 1, 1, 2),
   };
   return t;
 }
@@ -1664,7 +1668,8 @@ BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cu
                  int64_t rope_seq) {
   const Tuning& t = tuning();
   if (!rope && t.bwd_ring) {
-    const BwdPlan r = vg_plan::plan_bwd_ring(rows, dim, elem_bytes, aligned, cus, t.bwd_nv);
+    const BwdPlan r = vg_plan::plan_bwd_ring(rows, dim, elem_bytes, aligned, cus, t.bwd_nv,
+                                             t.ring_block, t.ring_wgs_per_cu);
     if (r.ring) return r;
   }
   if (rope && t.bwd_ring) {
@@ -1867,7 +1872,8 @@ bool types_ok(int32_t dt, int32_t wdt) {
 
 size_t workspace_bytes_for(int64_t rows, int64_t dim, int cus) {
   const Tuning& t = tuning();
-  return vg_plan::bwd_workspace_bytes(rows, dim, cus, t.bwd_nv, t.bwd_block, t.bwd_waves_per_cu);
+  return vg_plan::bwd_workspace_bytes(rows, dim, cus, t.bwd_nv, t.bwd_block, t.bwd_waves_per_cu,
+                                      t.ring_block, t.ring_wgs_per_cu);
 }
 
 // ------------------------------------------------------------------------------------------
