@@ -172,9 +172,12 @@ hipError_t launch_policy(int flags, const ProbeLaunch& p) {
   if (ntl && nts && rot) return launch_one<NR, NW, VPT, L, BLOCK, true, true, true>(p);
   if constexpr (VPT == 2 && L == 1 && BLOCK == 256) {
     if (ntl && nts) return launch_one<NR, NW, 2, 1, 256, true, true, false>(p);
-    if (ntl) return launch_one<NR, NW, 2, 1, 256, true, false, true>(p);
-    if (nts) return launch_one<NR, NW, 2, 1, 256, false, true, true>(p);
-    return launch_one<NR, NW, 2, 1, 256, false, false, true>(p);
+    if (ntl && rot) return launch_one<NR, NW, 2, 1, 256, true, false, true>(p);
+    if (ntl) return launch_one<NR, NW, 2, 1, 256, true, false, false>(p);
+    if (nts && rot) return launch_one<NR, NW, 2, 1, 256, false, true, true>(p);
+    if (nts) return launch_one<NR, NW, 2, 1, 256, false, true, false>(p);
+    if (rot) return launch_one<NR, NW, 2, 1, 256, false, false, true>(p);
+    return launch_one<NR, NW, 2, 1, 256, false, false, false>(p);
   }
   return hipErrorInvalidValue;
 }
