@@ -149,6 +149,37 @@ int main() {
                   } else {
                     CHECK(!ring_eligible(rg.rp, dim, eb), "eligible ring plan refused");
                   }
+                  // the ring plan under its tuning knobs (workgroup bound, workgroups per CU):
+                  // the same facts, at most two workgroups of at most kRingBlock / 2 threads per
+                  // CU (so a CU's resident waves stay eight), and a workspace query made with
+                  // the same knobs covering its partial rows
+                  for (int rb = 64; rb <= kRingBlock; rb *= 2) {
+                    for (int wpc = 1; wpc <= 2; ++wpc) {
+                      const BwdPlan rk = plan_bwd_ring(rows, dim, eb, aligned != 0, cus, prefer,
+                                                       rb, wpc);
+                      if (!rk.ring) {
+                        CHECK(!ring_eligible(rk.rp, dim, eb) || rk.rp.tpr > rb,
+                              "ring refused under knobs rb=%d wpc=%d dim=%lld", rb, wpc,
+                              (long long)dim);
+                        continue;
+                      }
+                      check_row_plan(rk.rp, dim, eb, aligned != 0);
+                      const int64_t per_cu = rk.wgs > cus ? 2 : 1;
+                      CHECK(rk.rp.block <= rb && rk.rp.block <= kRingBlock &&
+                                rk.rp.block * per_cu <= kRingBlock &&
+                                rk.wgs >= 1 && rk.wgs <= (int64_t)cus * wpc &&
+                                rk.wgs <= (rows + rk.rp.groups - 1) / rk.rp.groups,
+                            "ring under knobs rb=%d wpc=%d: block %d wgs %lld", rb, wpc,
+                            rk.rp.block, (long long)rk.wgs);
+                      CHECK(rk.lds_bytes <= 64 * 1024 &&
+                                (rk.lds_bytes == 0) == (rk.rp.groups == 1),
+                            "ring lds under knobs %zu", rk.lds_bytes);
+                      const size_t wsk = bwd_workspace_bytes(rows, dim, cus, prefer, max_block,
+                                                             waves, rb, wpc);
+                      CHECK((size_t)rk.wgs * (size_t)dim * sizeof(float) <= wsk,
+                            "ring partials under knobs exceed workspace %zu", wsk);
+                    }
+                  }
                   // the ring-pipelined plan with the fused RoPE gradient: whole rows of one
                   // chunk per thread (two for rows of 513 to 1024 chunks), one workgroup per
                   // CU, two for one chunk per thread in workgroups under 512 threads (or as
