@@ -243,6 +243,10 @@ def stream_ceilings(sets, stream_bytes: int, stream) -> dict:
     n16 = stream_bytes // 16
     sp = stream.cuda_stream
     out = {}
+    shape = lib.velograd_stream_probe_shape
+    shape.restype = ctypes.c_int32
+    shape.argtypes = ([ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+                       ctypes.c_int64] + [ctypes.c_int32] * 5 + [ctypes.c_void_p])
     for name, pattern, nstreams, keys in (("copy", 0, 2, ("x", None, "y", None)),
                                           ("fwd_pattern", 1, 4, ("x", "res", "y", "h")),
                                           ("bwd_pattern", 2, 3, ("x", "res", "y", None)),
@@ -266,6 +270,29 @@ def stream_ceilings(sets, stream_bytes: int, stream) -> dict:
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / reps
         out[f"ceiling_{name}_gbs"] = round(nstreams * n16 * 16 / (us * 1e-6) / 1e9, 1)
+    # The backward pattern in the fastest shape the probe sweep found for it (256 threads, four
+    # 16-byte vectors per thread and stream, one pass, no per-access guards;
+    # profiles/stream_probe_sweep_config_C.md): no shape beat the forward pattern's bench shape.
+    ptrs = [((ctypes.c_void_p * 3)(b["x"].data_ptr(), b["res"].data_ptr(), 0),
+             (ctypes.c_void_p * 2)(b["y"].data_ptr(), b["h"].data_ptr())) for b in sets]
+
+    def run_best(i):
+        rd, wr = ptrs[i % len(sets)]
+        rc = shape(2, 1, ctypes.cast(rd, ctypes.c_void_p), ctypes.cast(wr, ctypes.c_void_p), n16,
+                   256, 4, 16, 0, 7 | 8, sp)
+        if rc != 0:
+            raise RuntimeError(f"stream probe best 2R1W shape failed: {rc}")
+    for i in range(len(sets)):
+        run_best(i)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 20
+    e0.record(stream)
+    for i in range(reps):
+        run_best(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    out["ceiling_bwd_pattern_best_shape_gbs"] = round(3 * n16 * 16 / (us * 1e-6) / 1e9, 1)
     return out
 
 
@@ -1069,6 +1096,14 @@ def main(argv=None) -> int:
                 t_ideal += bb / (ceil["ceiling_bwd_pattern_gbs"] * 1e9)
             extra["ceiling_step_gbs"] = round((fb + bb) / t_ideal / 1e9, 1)
             extra["frac_of_ceiling"] = round(value / extra["ceiling_step_gbs"], 4)
+            if with_bwd:
+                # the same step with the backward's bytes moved at the best 2R1W shape's speed
+                # and no dweight reduction: what any kernel of this byte mix could reach
+                t_best = (fb / (ceil["ceiling_fwd_pattern_gbs"] * 1e9)
+                          + bb / (ceil["ceiling_bwd_pattern_best_shape_gbs"] * 1e9))
+                extra["ceiling_step_best_shapes_gbs"] = round((fb + bb) / t_best / 1e9, 1)
+                extra["ceiling_step_best_shapes_pct_peak"] = round(
+                    100.0 * (fb + bb) / t_best / 1e9 / HBM_PEAK_GBS, 2)
             if with_bwd and "roofline_bwd_grad_h" in extra:
                 extra["roofline_bwd_grad_h"]["frac_of_3r1w_probe"] = round(
                     extra["roofline_bwd_grad_h"]["achieved"] / ceil["ceiling_grad_h_pattern_gbs"],
