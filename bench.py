@@ -1001,14 +1001,14 @@ def probe_sweep(config: str, nsets: int = 4, reps: int = 12, rounds: int = 3) ->
                          f"{'nt' if flags & 1 else 'plain'} | {'nt' if flags & 2 else 'plain'} | "
                          f"{'yes' if (flags & 4 and nw == 2 and vpt >= 2) else '-'} | "
                          f"{'flat' if flags & 8 else 'guarded'} | {us:.2f} | {tbs:.3f} |")
-            print(lines[-1], flush=True)
+            print(lines[-1], file=sys.stderr, flush=True)  # progress; the table goes to stdout
 
         bench_us = time_shape(nr, nw, **base, pattern=fixed_pattern[name])
         results.append((bench_us, 256, 2, 16, 0, 7))
         lines.append(f"| {name} | 256 | 2 | 16 | one pass | nt | nt | "
                      f"{'yes' if nw == 2 else '-'} | the bench's ceiling kernel | "
                      f"{bench_us:.2f} | {nstreams * nbytes / (bench_us * 1e-6) / 1e12:.3f} |")
-        print(lines[-1], flush=True)
+        print(lines[-1], file=sys.stderr, flush=True)
         for style in (0, 8):
             for block in (256, 512, 1024):
                 for vpt in (1, 2, 4):
