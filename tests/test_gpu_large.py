@@ -213,3 +213,23 @@ def test_rope_beyond_2_pow_31_elements():
     assert np.all(np.abs(got - want) <= tol)
     del q, out
     torch.cuda.synchronize()
+
+
+def test_interleaved_rope_beyond_2_pow_31_elements():
+    """The interleaved pairing's 16-byte tiles with element offsets past 2^31 (position 262144
+    of a [262145, 8192] sequence starts at element 2^31; 262145 leaves a two-position last tile)."""
+    seq, d = 262145, 8192
+    _say(f"large interleaved rope [{seq}, {d}]")
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(seq, d, device="cuda", dtype=torch.bfloat16, generator=gen)
+    out = vk.fused_rope_interleaved(x, 500000.0)
+    pos = [0, 1, 2, 3, 262141, 262142, 262143, 262144]
+    got = out[pos].double().cpu().numpy()
+    xs = x[pos].double().cpu().numpy()
+    want = ora.apply_rotary_emb(xs, 500000.0, positions=pos)
+    mag = np.abs(xs[:, 0::2]) + np.abs(xs[:, 1::2])
+    b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -21) * np.repeat(mag, 2, axis=1)
+    tol = b + 2.0 ** -8 * 1.01 * np.abs(want)
+    assert np.all(np.abs(got - want) <= tol)
+    del x, out
+    torch.cuda.synchronize()

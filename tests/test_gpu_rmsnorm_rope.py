@@ -96,7 +96,7 @@ def test_fused_norm_rope_matches_the_oracle_composition(dtype, shape, with_res, 
 
 def test_fused_equals_the_two_pass_path_up_to_the_intermediate_rounding():
     """fp32: the fused pass and rmsnorm_forward + fused_rope_interleaved agree closely (the
-    two-pass path rounds the normalised rows once more and uses the double-precision walk).
+    two-pass path rounds the normalised rows once more and evaluates every angle afresh).
     The row statistic is the same fp32 sum of squares taken in another order (the module-form
     norm without a residual reads two 16-byte chunks per thread, the fused pass one), so the
     two inv_rms agree to a couple of ulps rather than bit for bit."""

@@ -142,7 +142,9 @@ def _interleaved_bound(x: np.ndarray, base: float) -> np.ndarray:
     """Tolerance for pairs (x_2i, x_2i+1): ROPE_ANGLE_ULPS float32 ulps of the pair for cos and
     sin plus 2^-21 for the rotation's products.  It does not grow with the position: both paths
     form the angles in double (as the reference's Python floats do) and reduce them exactly
-    before a float32 sincospi (the scalar path) or walk them in double (the 16-byte path)."""
+    before a float32 sincospi; the 16-byte path does so for every position of fp32 outputs and
+    for the first of each 3-position tile of bf16/fp16 ones, whose next two positions advance the
+    float32 rotation by a step rotation (a few float32 ulps each)."""
     x = np.abs(np.asarray(x, np.float64))
     mag = x[..., 0::2] + x[..., 1::2]
     b = (P.ROPE_ANGLE_ULPS * 2.0 ** -24 + 2.0 ** -21) * mag
@@ -200,6 +202,61 @@ def test_interleaved_rope_round_trip_and_autograd():
     assert float((x.grad.double().cpu() - t.grad).abs().max()) < 2e-4
     back = vk.fused_rope_interleaved(y.detach(), 10000.0, inverse=True)
     assert float((back - x.detach()).abs().max()) < 1e-4
+
+
+# The 16-byte interleaved path (rope_tile_kernel) through the C ABI: several heads, a rotated
+# prefix of each head with the rest copied, in place, token vectors of fewer than 256 chunks and
+# of a number of chunks that is not a multiple of 256, every remainder of the sequence length by
+# the kernel's 3-position tiles, and bases under 1 (whose step rotations exceed one radian and are
+# reduced as the tiles' first rotations are).
+TILE_CASES = [
+    # (dtype, outer, seq, heads, dim, rot_dim, base)
+    (torch.bfloat16, 2, 49, 4, 128, 64, 10000.0),
+    (torch.float16, 1, 50, 1, 4104, 4104, 10000.0),
+    (torch.float32, 3, 31, 2, 48, 32, 500000.0),
+    (torch.bfloat16, 1, 64, 8, 256, 256, 0.5),
+    (torch.float32, 2, 65, 1, 512, 512, 0.25),
+    (torch.float16, 1, 7, 3, 2048, 1024, 10000.0),
+    (torch.bfloat16, 1, 3, 1, 8, 8, 10000.0),
+]
+_CODES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16,
+          torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def _heads_want(x64: np.ndarray, rot: int, base: float, inverse: bool) -> np.ndarray:
+    """x64 [outer, seq, heads, dim]: each head's first `rot` elements rotated by the oracle
+    (positions moved to axis -2 for it), the rest copied."""
+    want = x64.copy()
+    part = np.ascontiguousarray(x64[..., :rot].transpose(0, 2, 1, 3))
+    want[..., :rot] = ora.apply_rotary_emb(part, base, inverse=inverse).transpose(0, 2, 1, 3)
+    return want
+
+
+@pytest.mark.parametrize("dtype,outer,seq,heads,dim,rot,base", TILE_CASES,
+                         ids=[f"{str(c[0]).split('.')[-1]}-{c[1]}x{c[2]}x{c[3]}x{c[4]}-r{c[5]}"
+                              f"-b{c[6]}" for c in TILE_CASES])
+def test_interleaved_tiles_through_the_c_abi(dtype, outer, seq, heads, dim, rot, base):
+    _say(f"rope interleaved tiles {dtype} [{outer}, {seq}, {heads}, {dim}] rot {rot} base {base}")
+    rng = np.random.default_rng(seq * 7 + dim)
+    x = P.to_device(P.gaussian(rng, (outer, seq, heads, dim)), dtype)
+    x64 = P.upcast(x).astype(np.float64)
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    for inverse in (0, 1):
+        out = torch.full_like(x, float("nan"))
+        _lib.check(lib.velograd_rope(x.data_ptr(), out.data_ptr(), outer, seq, heads, dim, rot,
+                                     base, inverse, _lib.ROPE_INTERLEAVED, _CODES[dtype], st),
+                   "velograd_rope interleaved")
+        want = _heads_want(x64, rot, base, bool(inverse))
+        tol = _interleaved_bound(x64, base) + ROUNDING[dtype] * np.abs(want)
+        tol[..., rot:] = 0.0                                    # copied exactly
+        err = np.abs(P.upcast(out).astype(np.float64) - want)
+        assert np.all(err <= tol), (inverse, float((err - tol).max()))
+        buf = x.clone()
+        _lib.check(lib.velograd_rope(buf.data_ptr(), buf.data_ptr(), outer, seq, heads, dim, rot,
+                                     base, inverse, _lib.ROPE_INTERLEAVED, _CODES[dtype], st),
+                   "velograd_rope interleaved in place")
+        assert torch.equal(buf, out)
 
 
 def test_interleaved_rope_errors():

@@ -58,7 +58,7 @@ constexpr double kInv2Pi = 0.159154943091895335768883763372514362;  // 1 / (2 pi
 // them in float32 as its reference does (fused.py:98-103); the interleaved pairing forms freq_j
 // and the angle in double, as its reference's Python floats do (functional.py:302-305), and
 // reduces the angle exactly to [-1/2, 1/2] revolutions before a float32 sincospi, so cos and
-// sin are within a few float32 ulps at any position (the 16-byte path, rope_run_kernel, walks
+// sin are within a few float32 ulps at any position (the 16-byte path, rope_tile_kernel, forms
 // the same double-precision angles).
 __device__ inline void rope_tables(const RopeArgs& a, int64_t tok0, int ntok, float* freq,
                                    float* cs, float* sn) {
@@ -134,8 +134,8 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(const RopeArgs a) {
   if constexpr (INTERLEAVED) {
     // Scalar interleaved path (rows that do not split into whole 16-byte pairs of chunks): one
     // item = one pair of the rotated region [0, 2 * half), then the pass-through elements.  The
-    // 16-byte path is rope_run_kernel.
-    static_assert(!VEC, "interleaved 16-byte chunks go through rope_run_kernel");
+    // 16-byte path is rope_tile_kernel.
+    static_assert(!VEC, "interleaved 16-byte chunks go through rope_tile_kernel");
     const int rot_items = a.half;
     const int tail_items = a.copy_tail ? a.dim - 2 * a.half : 0;
     const int per_head = rot_items + tail_items;
@@ -239,93 +239,186 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(const RopeArgs a) {
   }
 }
 
-// Interleaved pairs, 16-byte path: a thread owns one chunk column (V / 2 pairs) of the token
-// vector (heads * dim elements) of one outer index and walks the positions w, w + G, w + 2G, ...
-// (G = ceil(seq / kRopeRun) position groups, about kRopeRun positions per thread), so that at any
-// moment the whole grid works on a compact band of rows.  Its rotation (cos, sin) starts from a
-// double-precision sincos of angle w * freq_j and advances by the rotation through G * freq_j,
-// also in double (about 1e-16 drift per step): no per-(position, pair) sincos is evaluated.
-// With the whole hidden vector rotated (the reference model's RoPE) there is no sharing across
-// heads to amortise rope_kernel's tables, whose sincosf per (position, pair) bound that kernel
-// by VALU at a quarter of the copy speed.  The angles come out closer to the reference's
-// double-precision ones (functional.py:302-305) than a float32 angle does.  kRopeDepth loads
-// stay in flight per thread; they are issued before the double-precision set-up.  The kernel is
-// latency-bound on its loads, so the launch bounds ask for 4 waves per SIMD (128 VGPRs, no
-// spills; 138 VGPRs and 3 waves ran 10% slower).
-constexpr int kRopeRun = 32;
-constexpr int kRopeDepth = 4;
+// Interleaved pairs, 16-byte path: a one-pass grid of short tiles.  A thread owns one chunk
+// column (P = V / 2 pairs) of kRopeTileRows consecutive positions of one sequence: it issues the
+// tile's loads back to back (a position past the sequence's end re-reads the last one and stores
+// nothing), forms its pairs' frequencies and rotations while they are in flight, then rotates
+// and stores each position.  A 256-thread workgroup takes 256 chunk columns of one tile (or, for
+// token vectors of fewer than 256 chunks, whole token vectors of several tiles), so consecutive
+// workgroups sweep the tensor front to back as the copy kernels do.  Short-lived threads whose
+// loads are all in flight at once keep HBM busier than long walks down the positions (each thread
+// walking ~32 positions with 4 loads in flight ran 49.5-49.8 us at [16384, 4096] bf16 against
+// 44.2-44.4 us here; the 1R1W copy takes 43.4-44.0).
+//
+// Angles, as the reference's Python floats form them (functional.py:302-305): the pair frequency
+// in revolutions per position, g_j = theta^(-j / half) / (2 pi), in double (one exp2 per chunk,
+// then the chunk's next pairs by the double ratio theta^(-1 / half)); the angle of position s is
+// s * g_j in double, reduced exactly to [-1/2, 1/2] revolutions (rev - rint(rev) is exact) before
+// a float32 sincospi, so cos and sin are within a few float32 ulps at any position.
+//   fp32 outputs: every position evaluates its own angle that way.
+//   bf16/fp16 outputs: the tile's first position does; the next ones advance the float32
+//   rotation by the step rotation (cos g_j 2pi, sin g_j 2pi), at most kRopeTileRows - 1 steps of
+//   a few float32 ulps each, far below those formats' rounding.  The step's angle g_j 2pi is at
+//   most 1 radian when theta >= 1 and takes the Taylor series of cos and sin (below); a base under
+//   1 reduces it as the anchors are reduced.
+constexpr int kRopeTileRows = 3;
+constexpr double kTwoPi = 6.283185307179586476925286766559005768;
+
+// cos and sin of |x| <= 1 by their Taylor series through x^12 and x^11 (truncation below 2e-10,
+// then float32 rounding of the Horner steps).
+__device__ inline void cos_sin_small(float x, float& c, float& s) {
+  const float z = x * x;
+  float ps = -1.0f / 39916800.0f;
+  ps = fmaf(ps, z, 1.0f / 362880.0f);
+  ps = fmaf(ps, z, -1.0f / 5040.0f);
+  ps = fmaf(ps, z, 1.0f / 120.0f);
+  ps = fmaf(ps, z, -1.0f / 6.0f);
+  s = fmaf(x * z, ps, x);
+  float pc = 1.0f / 479001600.0f;
+  pc = fmaf(pc, z, -1.0f / 3628800.0f);
+  pc = fmaf(pc, z, 1.0f / 40320.0f);
+  pc = fmaf(pc, z, -1.0f / 720.0f);
+  pc = fmaf(pc, z, 1.0f / 24.0f);
+  pc = fmaf(pc, z, -0.5f);
+  c = fmaf(z, pc, 1.0f);
+}
+
+// cos and sin of 2 pi rev for any double rev: exact reduction to [-1/2, 1/2], then sincospi.
+__device__ inline void cos_sin_rev(double rev, float& c, float& s) {
+  sincospif(2.0f * (float)(rev - rint(rev)), &s, &c);
+}
+
+struct RopeTileGrid {
+  int32_t tok_chunks;   // 16-byte chunks per token vector (heads * dim / V)
+  int32_t col_blocks;   // workgroups per tile when tok_chunks >= kRopeBlock, else 0
+  int32_t tiles_per_block;  // tiles per workgroup when tok_chunks < kRopeBlock, else 1
+  int64_t row_tiles;    // tiles per sequence: ceil(seq / kRopeTileRows)
+  int64_t tiles;        // outer * row_tiles
+  double g_log2_step;   // -log2(theta) / half: g_j = 2^(j * g_log2_step) / (2 pi)
+  double g_ratio;       // theta^(-1 / half): g_{j+1} = g_j * g_ratio
+};
 
 template <int DT>
-__global__ __launch_bounds__(kRopeBlock, 4) void rope_run_kernel(const RopeArgs a,
-                                                                 int64_t col_blocks,
-                                                                 int64_t groups) {
+__global__ __launch_bounds__(kRopeBlock) void rope_tile_kernel(const RopeArgs a,
+                                                               const RopeTileGrid gd) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
   constexpr int P = V / 2;
-  const int64_t tok_elems = (int64_t)a.heads * a.dim;
-  const int64_t tok_chunks = tok_elems / V;
-  const int64_t blk = blockIdx.x;
-  const int64_t run = blk / col_blocks;
-  const int64_t col = (blk - run * col_blocks) * blockDim.x + threadIdx.x;
-  if (col >= tok_chunks) return;
-  const int64_t o = run / groups;
-  const int64_t w = run - o * groups;                // first position; the walk strides by groups
-  const int ns = (int)((a.seq - w + groups - 1) / groups);
-  const int chunks_per_head = a.dim / V;
-  const int h = (int)(col / chunks_per_head);
-  const int c = (int)(col - (int64_t)h * chunks_per_head);
-  const int64_t base0 = ((o * a.seq + w) * a.heads + h) * (int64_t)a.dim + (int64_t)c * V;
-  const int64_t stride = groups * tok_elems;
-
+  constexpr int R = kRopeTileRows;
+  int64_t tile;
+  int32_t col;
+  if (gd.col_blocks > 0) {
+    const int64_t blk = blockIdx.x;
+    tile = blk / gd.col_blocks;
+    col = (int32_t)(blk - tile * gd.col_blocks) * kRopeBlock + (int32_t)threadIdx.x;
+    if (col >= gd.tok_chunks) return;
+  } else {
+    const int32_t t = (int32_t)threadIdx.x / gd.tok_chunks;
+    if (t >= gd.tiles_per_block) return;
+    col = (int32_t)threadIdx.x - t * gd.tok_chunks;
+    tile = (int64_t)blockIdx.x * gd.tiles_per_block + t;
+    if (tile >= gd.tiles) return;
+  }
+  const int64_t o = tile / gd.row_tiles;
+  const int64_t s0 = (tile - o * gd.row_tiles) * R;
+  const int ns = (int)((a.seq - s0) < R ? (a.seq - s0) : R);   // >= 1
+  const int64_t tok_elems = (int64_t)gd.tok_chunks * V;
+  const int64_t base = (o * a.seq + s0) * tok_elems + (int64_t)col * V;
+  const int32_t c = col % (a.dim / V);
   if (c * V >= 2 * a.half) {  // pass-through chunk past rot_dim
     if (!a.copy_tail) return;
-    for (int t = 0; t < ns; ++t) {
-      const int64_t e = base0 + (int64_t)t * stride;
-      store16_stream<DT>(a.out, e, load16_stream<DT>(a.x, e));
-    }
+    u32x4 buf[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u)
+      buf[u] = load16_stream<DT>(a.x, base + (int64_t)(u < ns ? u : ns - 1) * tok_elems);
+#pragma unroll
+    for (int u = 0; u < R; ++u)
+      if (u < ns) store16_stream<DT>(a.out, base + (int64_t)u * tok_elems, buf[u]);
     return;
   }
-  u32x4 buf[kRopeDepth];
+  // Every load is issued before any arithmetic (no branch between them, so no wait either).
+  u32x4 buf[R];
 #pragma unroll
-  for (int u = 0; u < kRopeDepth; ++u)
-    buf[u] = u < ns ? load16_stream<DT>(a.x, base0 + (int64_t)u * stride) : u32x4{0u, 0u, 0u, 0u};
-  double cr[P], sr[P], cstep[P], sstep[P];
-  const double log2_theta = log2((double)a.theta);
+  for (int u = 0; u < R; ++u)
+    buf[u] = load16_stream<DT>(a.x, base + (int64_t)(u < ns ? u : ns - 1) * tok_elems);
+  double g = exp2((double)(c * P) * gd.g_log2_step) * kInv2Pi;
+  if constexpr (DT == VELOGRAD_DTYPE_F32) {
+    double gp[P];
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int j = c * P + p;
-    const double fr = exp2(-(double)j / (double)a.half * log2_theta);  // 1/theta^(2j/rot_dim)
-    double sv, cv;
-    sincos((double)w * fr, &sv, &cv);
-    cr[p] = cv;
-    sr[p] = (double)a.sin_sign * sv;
-    sincos((double)groups * fr, &sv, &cv);
-    cstep[p] = cv;
-    sstep[p] = (double)a.sin_sign * sv;
-  }
-  for (int t = 0; t < ns; t += kRopeDepth) {
+    for (int p = 0; p < P; ++p) {
+      gp[p] = g;
+      g *= gd.g_ratio;
+    }
 #pragma unroll
-    for (int u = 0; u < kRopeDepth; ++u) {
-      const int tt = t + u;
-      if (tt < ns) {
+    for (int u = 0; u < R; ++u) {
+      if (u < ns) {
         float f[V];
         C::unpack(buf[u], f);
-        if (tt + kRopeDepth < ns)
-          buf[u] = load16_stream<DT>(a.x, base0 + (int64_t)(tt + kRopeDepth) * stride);
 #pragma unroll
         for (int p = 0; p < P; ++p) {
-          const float cv = (float)cr[p], sv = (float)sr[p];
+          float cv, sv;
+          cos_sin_rev((double)(s0 + u) * gp[p], cv, sv);
+          sv *= a.sin_sign;
           const float x1 = f[2 * p], x2 = f[2 * p + 1];
           f[2 * p] = x1 * cv - x2 * sv;                                  // functional.py:313
           f[2 * p + 1] = x1 * sv + x2 * cv;                              // functional.py:314
-          const double cn = cr[p] * cstep[p] - sr[p] * sstep[p];
-          sr[p] = sr[p] * cstep[p] + cr[p] * sstep[p];
-          cr[p] = cn;
         }
-        store16_stream<DT>(a.out, base0 + (int64_t)tt * stride, C::pack(f));
+        store16_stream<DT>(a.out, base + (int64_t)u * tok_elems, C::pack(f));
+      }
+    }
+  } else {
+    float cr[P], sr[P], cs[P], ss[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      float cv, sv;
+      cos_sin_rev((double)s0 * g, cv, sv);
+      cr[p] = cv;
+      sr[p] = a.sin_sign * sv;
+      if (a.theta >= 1.0f)
+        cos_sin_small((float)(g * kTwoPi), cv, sv);
+      else
+        cos_sin_rev(g, cv, sv);
+      cs[p] = cv;
+      ss[p] = a.sin_sign * sv;
+      g *= gd.g_ratio;
+    }
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      if (u < ns) {
+        float f[V];
+        C::unpack(buf[u], f);
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          const float x1 = f[2 * p], x2 = f[2 * p + 1];
+          f[2 * p] = x1 * cr[p] - x2 * sr[p];                            // functional.py:313
+          f[2 * p + 1] = x1 * sr[p] + x2 * cr[p];                        // functional.py:314
+          if (u + 1 < R) {
+            const float cn = fmaf(cr[p], cs[p], -(sr[p] * ss[p]));
+            sr[p] = fmaf(sr[p], cs[p], cr[p] * ss[p]);
+            cr[p] = cn;
+          }
+        }
+        store16_stream<DT>(a.out, base + (int64_t)u * tok_elems, C::pack(f));
       }
     }
   }
+}
+
+RopeTileGrid rope_tile_grid(const RopeArgs& a, int vec) {
+  RopeTileGrid g;
+  g.tok_chunks = (int32_t)((int64_t)a.heads * a.dim / vec);
+  g.col_blocks = g.tok_chunks >= kRopeBlock ? (g.tok_chunks + kRopeBlock - 1) / kRopeBlock : 0;
+  g.tiles_per_block = g.tok_chunks >= kRopeBlock ? 1 : kRopeBlock / g.tok_chunks;
+  g.row_tiles = (a.seq + kRopeTileRows - 1) / kRopeTileRows;
+  g.tiles = (a.tokens / a.seq) * g.row_tiles;
+  g.g_log2_step = -log2((double)a.theta) / (double)a.half;
+  g.g_ratio = exp2(g.g_log2_step);
+  return g;
+}
+
+int64_t rope_tile_blocks(const RopeTileGrid& g) {
+  return g.col_blocks > 0 ? g.tiles * g.col_blocks
+                          : (g.tiles + g.tiles_per_block - 1) / g.tiles_per_block;
 }
 
 template <int DT>
@@ -334,12 +427,9 @@ void launch_rope(const RopeArgs& a, bool vec, hipStream_t st) {
   const size_t lds = (size_t)(a.half + 2 * a.tpb * a.half) * sizeof(float);
   if (a.interleaved) {
     if (vec) {
-      const int64_t col_blocks =
-          ((int64_t)a.heads * a.dim / Codec<DT>::kVec + kRopeBlock - 1) / kRopeBlock;
-      const int64_t groups = (a.seq + kRopeRun - 1) / kRopeRun;
-      const int64_t outer = a.tokens / a.seq;
-      hipLaunchKernelGGL((rope_run_kernel<DT>), dim3((uint32_t)(col_blocks * groups * outer)),
-                         dim3(kRopeBlock), 0, st, a, col_blocks, groups);
+      const RopeTileGrid gd = rope_tile_grid(a, Codec<DT>::kVec);
+      hipLaunchKernelGGL((rope_tile_kernel<DT>), dim3((uint32_t)rope_tile_blocks(gd)),
+                         dim3(kRopeBlock), 0, st, a, gd);
     } else {
       hipLaunchKernelGGL((rope_kernel<DT, false, true>), grid, dim3(kRopeBlock), lds, st, a);
     }
@@ -377,8 +467,8 @@ VELOGRAD_API int32_t velograd_rope(const void* x, void* out, int64_t outer, int6
                 "rope: rot_dim=%lld must be even, >= 2 and <= dim=%lld", (long long)rot_dim,
                 (long long)dim);
   // The table kernels hold one token's frequencies and (cos, sin) in LDS: rot_dim <= 8192.  The
-  // interleaved pairing on 16-byte chunks walks positions without tables (rope_run_kernel), so it
-  // takes any rot_dim (a whole hidden vector of 16384, say).
+  // interleaved pairing on 16-byte chunks forms its angles without tables (rope_tile_kernel), so
+  // it takes any rot_dim (a whole hidden vector of 16384, say).
   const int vec_chunk = 16 / eb;
   const bool run_path = pairing == VELOGRAD_ROPE_INTERLEAVED && aligned16(x) && aligned16(out) &&
                         dim % vec_chunk == 0 && rot_dim % vec_chunk == 0;
@@ -417,18 +507,13 @@ VELOGRAD_API int32_t velograd_rope(const void* x, void* out, int64_t outer, int6
   if (tpb > 64) tpb = 64;
   if (tpb < 1) tpb = 1;
   a.tpb = (int32_t)tpb;
-  const int64_t grid = (a.tokens + tpb - 1) / tpb;
+  const int vec_elems = 16 / eb;
+  const int64_t grid = run_path ? rope_tile_blocks(rope_tile_grid(a, vec_elems))
+                                : (a.tokens + tpb - 1) / tpb;
   if (grid > INT32_MAX)
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "rope: %lld tokens exceed the grid limit",
                 (long long)a.tokens);
 
-  const int vec_elems = 16 / eb;
-  if (pairing == VELOGRAD_ROPE_INTERLEAVED) {
-    const int64_t run_blocks = ((tok_elems / vec_elems + kRopeBlock - 1) / kRopeBlock) *
-                               ((seq + kRopeRun - 1) / kRopeRun) * outer;
-    if (run_blocks > INT32_MAX)
-      return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "rope: tensor too large for the grid");
-  }
   // 16-byte chunks must not straddle the rotated region's boundaries: rotate-half needs each
   // half chunk-aligned, interleaved the whole region (a chunk then holds whole pairs).
   const bool vec = aligned16(x) && aligned16(out) && a.dim % vec_elems == 0 &&
