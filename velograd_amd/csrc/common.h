@@ -178,6 +178,25 @@ __device__ inline float dpp_move(float v) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// cos and sin of |x| <= 1 by their Taylor series through x^12 and x^11 (truncation below 2e-10,
+// then float32 rounding of the Horner steps).
+__device__ inline void cos_sin_small(float x, float& c, float& s) {
+  const float z = x * x;
+  float ps = -1.0f / 39916800.0f;
+  ps = fmaf(ps, z, 1.0f / 362880.0f);
+  ps = fmaf(ps, z, -1.0f / 5040.0f);
+  ps = fmaf(ps, z, 1.0f / 120.0f);
+  ps = fmaf(ps, z, -1.0f / 6.0f);
+  s = fmaf(x * z, ps, x);
+  float pc = 1.0f / 479001600.0f;
+  pc = fmaf(pc, z, -1.0f / 3628800.0f);
+  pc = fmaf(pc, z, 1.0f / 40320.0f);
+  pc = fmaf(pc, z, -1.0f / 720.0f);
+  pc = fmaf(pc, z, 1.0f / 24.0f);
+  pc = fmaf(pc, z, -0.5f);
+  c = fmaf(z, pc, 1.0f);
+}
+
 // Empty register barrier: the compiler must assume `v` changed here, so values it decoded from
 // `v` before this point are decoded again afterwards instead of being held in extra VGPRs
 // across the row reduction.  Emits no instruction.

@@ -264,25 +264,6 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(const RopeArgs a) {
 constexpr int kRopeTileRows = 3;
 constexpr double kTwoPi = 6.283185307179586476925286766559005768;
 
-// cos and sin of |x| <= 1 by their Taylor series through x^12 and x^11 (truncation below 2e-10,
-// then float32 rounding of the Horner steps).
-__device__ inline void cos_sin_small(float x, float& c, float& s) {
-  const float z = x * x;
-  float ps = -1.0f / 39916800.0f;
-  ps = fmaf(ps, z, 1.0f / 362880.0f);
-  ps = fmaf(ps, z, -1.0f / 5040.0f);
-  ps = fmaf(ps, z, 1.0f / 120.0f);
-  ps = fmaf(ps, z, -1.0f / 6.0f);
-  s = fmaf(x * z, ps, x);
-  float pc = 1.0f / 479001600.0f;
-  pc = fmaf(pc, z, -1.0f / 3628800.0f);
-  pc = fmaf(pc, z, 1.0f / 40320.0f);
-  pc = fmaf(pc, z, -1.0f / 720.0f);
-  pc = fmaf(pc, z, 1.0f / 24.0f);
-  pc = fmaf(pc, z, -0.5f);
-  c = fmaf(z, pc, 1.0f);
-}
-
 // cos and sin of 2 pi rev for any double rev: exact reduction to [-1/2, 1/2], then sincospi.
 __device__ inline void cos_sin_rev(double rev, float& c, float& s) {
   sincospif(2.0f * (float)(rev - rint(rev)), &s, &c);
