@@ -1129,6 +1129,13 @@ def main(argv=None) -> int:
     if not args.no_rope:
         extra.update(rope_timing(lib, rows, stream, norm_rope=not args.no_norm_rope,
                                  hid=args.norm_rope_dim))
+        # the interleaved RoPE and the fused norm + RoPE move one read and one write stream of
+        # [rows, hid] bf16: against the same run's copy probe when that moved tensors of this size
+        if "ceiling_copy_gbs" in extra and rows * args.norm_rope_dim * 2 == rows * d * s:
+            for key in ("rope_interleaved", "norm_rope_fused"):
+                if f"{key}_gbs" in extra:
+                    extra[f"{key}_frac_of_copy_probe"] = round(
+                        extra[f"{key}_gbs"] / extra["ceiling_copy_gbs"], 4)
     if not args.no_torch_baseline:
         extra.update(torch_eager_timing(sets, rows, d, s, eps, with_bwd, stream))
         extra["speedup_vs_torch_eager"] = round(
