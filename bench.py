@@ -98,6 +98,10 @@ def parse_args(argv=None):
                    help="skip the PyTorch eager comparison and the reference benchmark's shapes")
     p.add_argument("--no-copy-ceiling", action="store_true",
                    help="skip the same-run stream-probe ceilings")
+    p.add_argument("--row-scaling", action="store_true",
+                   help="instead of the bench line: the forward, the backward with and without "
+                        "dweight and their streaming probes over 4096..65536 rows at dim 4096 "
+                        "bf16, with each kernel's fixed cost and cost per row (a markdown table)")
     p.add_argument("--probe-sweep", action="store_true",
                    help="instead of the benchmark: sweep the stream probe's shapes over the "
                         "config's tensors and print a markdown table of the byte patterns' "
@@ -753,6 +757,10 @@ def measure(lib, config: str, steps: int, warmup: int, nsets: int, kernel_events
                     b["dw"].data_ptr(), b["ws"].data_ptr(), ws_bytes, rows, d, d, d, d, d, d,
                     code, code, sp) for b in sets]
         gh_batch_ms = batch_mean_ms(bwd_fn, gh_args)[0]
+        # the same backward with no dweight requested (dweight = NULL): stage 1 alone, without
+        # its partial rows, so the line shows what the deterministic dweight reduction costs
+        nodw_args = [a[:8] + (None,) + a[9:] for a in bwd_args]
+        nodw_batch_ms = batch_mean_ms(bwd_fn, nodw_args)[0]
 
     for k in range(warmup):
         _lib.check(step(k), "warm-up step")
@@ -800,6 +808,8 @@ def measure(lib, config: str, steps: int, warmup: int, nsets: int, kernel_events
             "bwd_workspace_bytes": ws_bytes,
             "bwd_grad_h_us_mean": round(gh_batch_ms * 1e3, 2),
             "bwd_grad_h_bytes": bwd_grad_h_bytes(rows, d, s),
+            "bwd_no_dweight_us_mean": round(nodw_batch_ms * 1e3, 2),
+            "dweight_cost_us": round((mean_bwd_ms - nodw_batch_ms) * 1e3, 2),
         })
     out["rows_per_s"] = round(rows / (ms_per_step * 1e-3), 1)
     out["pct_hbm_peak"] = round(100.0 * value / HBM_PEAK_GBS, 2)
@@ -1035,6 +1045,121 @@ def probe_sweep(config: str, nsets: int = 4, reps: int = 12, rounds: int = 3) ->
     return "\n".join(out)
 
 
+ROW_SCALING_ROWS = (4096, 8192, 16384, 32768, 65536)
+
+
+def row_scaling(d: int = 4096, rows_list=ROW_SCALING_ROWS, rounds: int = 3) -> str:
+    """The forward, the backward (with and without dweight) and the streaming probes of their
+    byte patterns over a range of row counts at one width (bf16): per kernel the best of
+    `rounds` batches of 10 back-to-back launches over rotating buffer sets of at least 1.5 GiB,
+    then per row count what the deterministic dweight reduction adds to the backward and each
+    kernel's time against its pattern's probe.  Returns a markdown table."""
+    import ctypes
+
+    import torch
+
+    from velograd_amd import _lib
+    from velograd_amd import kernels as vk
+    from velograd_amd.build import PROBE_LIB_PATH
+
+    lib = _lib.load()
+    plib = ctypes.CDLL(PROBE_LIB_PATH)
+    probe = plib.velograd_stream_probe
+    probe.restype = ctypes.c_int32
+    probe.argtypes = [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p]
+    shape = plib.velograd_stream_probe_shape
+    shape.restype = ctypes.c_int32
+    shape.argtypes = ([ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+                       ctypes.c_int64] + [ctypes.c_int32] * 5 + [ctypes.c_void_p])
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    code = _lib.DTYPE_BF16
+    fwd_fn, bwd_fn = lib.velograd_rmsnorm_residual_fwd, lib.velograd_rmsnorm_residual_bwd
+    names = ("forward", "2R2W probe", "backward", "backward, no dweight", "2R1W probe",
+             "2R1W best shape")
+    table = {}
+    for rows in rows_list:
+        tb = rows * d * 2
+        nsets = max(4, -(-(3 << 29) // (4 * tb)))
+        ws_bytes = vk.bwd_workspace_bytes(rows, d, dev)
+        sets = []
+        for _ in range(nsets):
+            b = {k: torch.randn(rows, d, device=dev).to(torch.bfloat16) for k in ("x", "r", "g")}
+            for k in ("y", "h", "dx"):
+                b[k] = torch.empty(rows, d, device=dev, dtype=torch.bfloat16)
+            b["w"] = (1 + 0.1 * torch.randn(d, device=dev)).to(torch.bfloat16)
+            b["inv"] = torch.empty(rows, device=dev)
+            b["dw"] = torch.empty(d, device=dev)
+            b["ws"] = torch.empty(max(ws_bytes, 16), device=dev, dtype=torch.uint8)
+            sets.append(b)
+        p = {k: [b[k].data_ptr() for b in sets] for k in sets[0]}
+        n16 = tb // 16
+        ptrs = [((ctypes.c_void_p * 3)(p["g"][i], p["h"][i], 0),
+                 (ctypes.c_void_p * 2)(p["dx"][i], 0)) for i in range(nsets)]
+
+        def fwd(i):
+            return fwd_fn(p["x"][i], p["r"][i], p["w"][i], p["y"][i], p["h"][i], p["inv"][i],
+                          rows, d, d, d, d, d, code, code, 1e-5, sp)
+
+        def bwd(i, dw=True):
+            return bwd_fn(p["g"][i], p["h"][i], 1, p["w"][i], p["inv"][i], None, p["dx"][i], None,
+                          p["dw"][i] if dw else None, p["ws"][i], ws_bytes, rows, d, d, d, d, d,
+                          d, code, code, sp)
+
+        def best2r1w(i):
+            rd, wr = ptrs[i]
+            return shape(2, 1, ctypes.cast(rd, ctypes.c_void_p), ctypes.cast(wr, ctypes.c_void_p),
+                         n16, 256, 4, 16, 0, 7 | 8, sp)
+
+        fns = (fwd,
+               lambda i: probe(1, p["x"][i], p["r"][i], p["y"][i], p["h"][i], n16, sp),
+               bwd, lambda i: bwd(i, False),
+               lambda i: probe(2, p["g"][i], p["h"][i], p["dx"][i], None, n16, sp),
+               best2r1w)
+        for i in range(nsets):
+            _lib.check(fwd(i), "row scaling forward")
+        for name, fn in zip(names, fns):
+            best = float("inf")
+            for _ in range(rounds):
+                evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                       for _ in range(9)]
+                torch.cuda.synchronize()
+                rc = 0
+                for bi, (e0, e1) in enumerate(evs):
+                    e0.record(stream)
+                    for j in range(10):
+                        rc |= fn((bi * 10 + j) % nsets)
+                    e1.record(stream)
+                torch.cuda.synchronize()
+                if rc != 0:
+                    raise RuntimeError(f"row scaling {name} at {rows} rows failed: rc {rc}")
+                best = min(best, statistics.fmean(e0.elapsed_time(e1) * 100.0
+                                                  for e0, e1 in evs[1:]))
+            table[(name, rows)] = best
+            print(f"rows {rows} {name}: {best:.2f} us", file=sys.stderr, flush=True)
+        del sets
+        torch.cuda.empty_cache()
+
+    lines = [f"Row scaling at dim {d} bf16: µs per launch (best of {rounds} batches of 10 "
+             "back-to-back launches, rotating buffer sets of at least 1.5 GiB).", "",
+             "| kernel | " + " | ".join(f"{r} rows" for r in rows_list) + " |",
+             "|---|" + "---:|" * len(rows_list)]
+    for name in names:
+        lines.append(f"| {name} | " + " | ".join(f"{table[(name, r)]:.2f}" for r in rows_list)
+                     + " |")
+    if rows_list:
+        lines.append("")
+        lines.append("| rows | backward − backward without dweight (µs) | backward without "
+                     "dweight / 2R1W probe | forward / 2R2W probe |")
+        lines.append("|---:|---:|---:|---:|")
+        for r in rows_list:
+            lines.append(f"| {r} | {table[('backward', r)] - table[('backward, no dweight', r)]:.2f}"
+                         f" | {table[('backward, no dweight', r)] / table[('2R1W probe', r)]:.3f}"
+                         f" | {table[('forward', r)] / table[('2R2W probe', r)]:.3f} |")
+    return "\n".join(lines)
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -1043,6 +1168,9 @@ def main(argv=None) -> int:
         return 2
     if args.probe_sweep:
         print(probe_sweep(args.config), flush=True)
+        return 0
+    if args.row_scaling:
+        print(row_scaling(), flush=True)
         return 0
 
     import torch
