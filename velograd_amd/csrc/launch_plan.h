@@ -26,6 +26,13 @@ constexpr int kMaxWavesPerRow = 16;  // 1024 threads per row at most
 // understood, NV 5..8 are neither planned nor compiled.
 constexpr int kMaxNV = 4;
 constexpr int kGenericBlock = 256;
+// The generic backward sums a slot's dweight columns in dynamic LDS (dim floats) for rows of up
+// to kGenericLdsCols elements (64 KiB of LDS a workgroup, less its static row-sum buffers), else
+// in its partial row in global memory.  Returns the launch's dynamic LDS bytes.
+constexpr int kGenericLdsCols = 16000;
+VG_HOST_DEVICE constexpr size_t generic_bwd_lds_bytes(int64_t dim, bool dweight) {
+  return dweight && dim > 0 && dim <= kGenericLdsCols ? (size_t)dim * sizeof(float) : 0;
+}
 
 // Workgroup size bound of the register-resident kernels, so that a thread's packed chunks fit
 // its VGPR budget (512 VGPRs per SIMD lane shared by the block's waves on that SIMD):
