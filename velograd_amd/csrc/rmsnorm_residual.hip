@@ -93,6 +93,39 @@ __device__ inline uintptr_t row_offset16(const void* base, int64_t elem, int ele
   return (reinterpret_cast<uintptr_t>(base) + (uintptr_t)(elem * elem_bytes)) & 15u;
 }
 
+// The 16 bytes at p whatever its 2-byte alignment (`align` = p's offset in its 16-byte line, the
+// same on every lane), in the widest loads that alignment allows: the generic kernels' weight
+// values for a body chunk, which sits elsewhere in its line than the row's chunk.
+__device__ inline u32x4 load16_unaligned(const char* p, uintptr_t align) {
+  if (align == 0) return *reinterpret_cast<const u32x4*>(p);
+  if ((align & 7) == 0) {
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(p);
+    const u32x2 hi = *reinterpret_cast<const u32x2*>(p + 8);
+    return u32x4{lo.x, lo.y, hi.x, hi.y};
+  }
+  if ((align & 3) == 0) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    return u32x4{q[0], q[1], q[2], q[3]};
+  }
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = (uint32_t)h[2 * i] | ((uint32_t)h[2 * i + 1] << 16);
+  return v;
+}
+
+// The weight values of the body chunk at element j (Codec<DT>::kVec of them) into f, for the
+// generic kernels: one to four loads of 16 bytes' worth instead of one per element.  `align` is
+// the weight's offset inside its 16-byte line at the row's first body element (uniform).
+template <int DT, int WDT>
+__device__ inline void weight_run(const void* w, int64_t j, uintptr_t align, float* f) {
+  constexpr int kParts = (Codec<DT>::kVec * Codec<WDT>::kBytes) / 16;
+  const char* p = static_cast<const char*>(w) + j * Codec<WDT>::kBytes;
+#pragma unroll
+  for (int q = 0; q < kParts; ++q)
+    Codec<WDT>::unpack(load16_unaligned(p + 16 * q, align), f + q * Codec<WDT>::kVec);
+}
+
 // Largest |value| over the `tpr` threads of row group `grp`, on the bit patterns of |value|
 // (sign cleared): for non-negative IEEE floats the unsigned order is the numeric order, and
 // every NaN pattern lies above +inf, so a NaN anywhere in the row wins (NaN propagates).
@@ -756,12 +789,61 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
   const int tail = head + nbody * C::kVec;  // first element after the body
   auto scalar_j = [&](int t) { return t < head ? t : tail + (t - head); };
   const int nscalar = a.dim - nbody * C::kVec;
+  // the weight at the body's chunks: where it sits in its 16-byte lines (2-byte aligned at least)
+  const uintptr_t w_align = has_w ? row_offset16(a.w, head, CW::kBytes) : 0;
 
-  // The first pass reads the body with the normal cache policy so that the second finds it in
-  // L2, and the second reads it non-temporally (its last use): 147.6 against 174.9 us the other
-  // way round at 16384 x 4100 bf16.
+  // A thread's first KR body chunks stay in registers from the first pass to the second (rows
+  // of up to KR * 256 chunks: 8192 bf16/fp16 or 4096 fp32 elements read once); chunks past
+  // them are read again in the second pass.  That re-read finds them in L2 when the first pass
+  // reads with the normal cache policy and the second non-temporally (its last use): 147.6
+  // against 174.9 us the other way round at 16384 x 4100 bf16, before the registers.
+  constexpr int KR = OUT == kOutDtype ? 4 : 0;
+  u32x4 xk[KR > 0 ? KR : 1], rk[KR > 0 ? KR : 1];
+#pragma unroll
+  for (int k = 0; k < KR; ++k) {
+    const int c = threadIdx.x + k * blockDim.x;
+    xk[k] = u32x4{0u, 0u, 0u, 0u};
+    rk[k] = u32x4{0u, 0u, 0u, 0u};
+    if (c < nbody) {
+      const int64_t j = head + (int64_t)c * C::kVec;
+      xk[k] = load16_stream<DT>(a.x, row * a.ld_x + j);
+      if (has_res) rk[k] = load16_stream<DT>(a.res, row * a.ld_res + j);
+    }
+  }
+  // With a body, the head and tail are fewer than two chunks' worth of elements: one per thread
+  // at most, loaded with the body, so a row waits for memory once per pass.
+  const bool few_scalar = KR > 0 && nbody > 0;
+  int j_s = 0;
+  float h_s = 0.0f, w_s = 1.0f;
+  if (few_scalar && (int)threadIdx.x < nscalar) {
+    j_s = scalar_j(threadIdx.x);
+    h_s = C::load1(a.x, row * a.ld_x + j_s);
+    if (has_res) h_s = h_s + C::load1(a.res, row * a.ld_res + j_s);
+    if (has_w) w_s = CW::load1(a.w, j_s);
+  }
+  // h of register chunk k (the same single fp32 add as every other path)
+  auto h_reg = [&](int k, float* hf) {
+    C::unpack(xk[k], hf);
+    if (has_res) {
+      float rf[C::kVec];
+      C::unpack(rk[k], rf);
+#pragma unroll
+      for (int i = 0; i < C::kVec; ++i) hf[i] = hf[i] + rf[i];
+    }
+  };
   float ss = 0.0f;
-  for (int c = threadIdx.x; c < nbody; c += blockDim.x) {
+#pragma unroll
+  for (int k = 0; k < KR; ++k) {
+    const int c = threadIdx.x + k * blockDim.x;
+    if (c < nbody) {
+      float hf[C::kVec];
+      h_reg(k, hf);
+      if (write_h) store16_stream<DT>(a.h, row * a.ld_h + head + (int64_t)c * C::kVec, C::pack(hf));
+#pragma unroll
+      for (int i = 0; i < C::kVec; ++i) ss += hf[i] * hf[i];
+    }
+  }
+  for (int c = threadIdx.x + KR * blockDim.x; c < nbody; c += blockDim.x) {
     const int64_t j = head + (int64_t)c * C::kVec;
     float hf[C::kVec];
     C::unpack(load16<DT>(a.x, row * a.ld_x + j), hf);
@@ -775,12 +857,19 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
 #pragma unroll
     for (int i = 0; i < C::kVec; ++i) ss += hf[i] * hf[i];
   }
-  for (int t = threadIdx.x; t < nscalar; t += blockDim.x) {
-    const int j = scalar_j(t);
-    float hx = C::load1(a.x, row * a.ld_x + j);
-    if (has_res) hx = hx + C::load1(a.res, row * a.ld_res + j);
-    if (write_h) C::store1(a.h, row * a.ld_h + j, hx);
-    ss += hx * hx;
+  if (few_scalar) {
+    if ((int)threadIdx.x < nscalar) {
+      if (write_h) C::store1(a.h, row * a.ld_h + j_s, h_s);
+      ss += h_s * h_s;
+    }
+  } else {
+    for (int t = threadIdx.x; t < nscalar; t += blockDim.x) {
+      const int j = scalar_j(t);
+      float hx = C::load1(a.x, row * a.ld_x + j);
+      if (has_res) hx = hx + C::load1(a.res, row * a.ld_res + j);
+      if (write_h) C::store1(a.h, row * a.ld_h + j, hx);
+      ss += hx * hx;
+    }
   }
   ss = row_sum(ss, blockDim.x, 0, red);
   const float mean_sq = floor_mean_sq(ss / (float)a.dim, a.ms_floor);
@@ -794,8 +883,24 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
     return has_w ? n * CW::load1(a.w, j) : n;
   };
   if constexpr (OUT == kOutDtype) {
-    // the second pass over the body reads x and the residual again (normally from L2)
-    for (int c = threadIdx.x; c < nbody; c += blockDim.x) {
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+      const int c = threadIdx.x + k * blockDim.x;
+      if (c < nbody) {
+        const int64_t j = head + (int64_t)c * C::kVec;
+        float hf[C::kVec], wf[C::kVec];
+        h_reg(k, hf);
+        if (has_w) weight_run<DT, WDT>(a.w, j, w_align, wf);
+#pragma unroll
+        for (int i = 0; i < C::kVec; ++i) {
+          const float n = hf[i] * r;
+          hf[i] = has_w ? n * wf[i] : n;
+        }
+        store16_stream<DT>(a.y, row * a.ld_y + j, C::pack(hf));
+      }
+    }
+    // the chunks past the registers: x and the residual read again (normally from L2)
+    for (int c = threadIdx.x + KR * blockDim.x; c < nbody; c += blockDim.x) {
       const int64_t j = head + (int64_t)c * C::kVec;
       float hf[C::kVec];
       C::unpack(load16_stream<DT>(a.x, row * a.ld_x + j), hf);
@@ -805,16 +910,25 @@ __global__ __launch_bounds__(kGenericBlock) void fwd_generic_kernel(const FwdArg
 #pragma unroll
         for (int i = 0; i < C::kVec; ++i) hf[i] = hf[i] + rf[i];
       }
+      float wf[C::kVec];
+      if (has_w) weight_run<DT, WDT>(a.w, j, w_align, wf);
 #pragma unroll
       for (int i = 0; i < C::kVec; ++i) {
         const float n = hf[i] * r;
-        hf[i] = has_w ? n * CW::load1(a.w, j + i) : n;
+        hf[i] = has_w ? n * wf[i] : n;
       }
       store16_stream<DT>(a.y, row * a.ld_y + j, C::pack(hf));
     }
-    for (int t = threadIdx.x; t < nscalar; t += blockDim.x) {
-      const int j = scalar_j(t);
-      C::store1(a.y, row * a.ld_y + j, y_at(j));
+    if (few_scalar) {
+      if ((int)threadIdx.x < nscalar) {
+        const float n = h_s * r;  // y_at's arithmetic on the register copies
+        C::store1(a.y, row * a.ld_y + j_s, has_w ? n * w_s : n);
+      }
+    } else {
+      for (int t = threadIdx.x; t < nscalar; t += blockDim.x) {
+        const int j = scalar_j(t);
+        C::store1(a.y, row * a.ld_y + j, y_at(j));
+      }
     }
   } else if constexpr (OUT == kOutRopeI) {
     const int64_t pos = row % a.rope_seq;
@@ -1584,7 +1698,7 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
   // The dweight columns of the slot's rows, summed in row order: in dynamic LDS (dim floats)
   // where the launch gave it (vg_plan::generic_bwd_lds_bytes), else in the slot's partial row
   // in global memory, each column then always touched by the same thread.
-  extern __shared__ float acc_lds[];
+  extern __shared__ __align__(16) float acc_lds[];
   const int64_t slot = blockIdx.x;
   const int64_t nslots = gridDim.x;
   const bool has_w = a.w != nullptr;
@@ -1668,34 +1782,81 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
       const int tail = head + nbody * C::kVec;
       const int nscalar = a.dim - nbody * C::kVec;
       auto scalar_j = [&](int t) { return t < head ? t : tail + (t - head); };
+      const uintptr_t w_align = has_w ? row_offset16(a.w, head, CW::kBytes) : 0;
+      // A thread's first KR body chunks of g and the saved tensor stay in registers from the
+      // first pass to the second (rows of up to KR * 256 chunks read once); chunks past them
+      // are read in the first pass with the normal cache policy and again, non-temporally,
+      // in the second (normally from L2).
+      constexpr int KR = 4;
+      u32x4 gk[KR], sk[KR];
+#pragma unroll
+      for (int k = 0; k < KR; ++k) {
+        const int c = threadIdx.x + k * blockDim.x;
+        gk[k] = u32x4{0u, 0u, 0u, 0u};
+        sk[k] = u32x4{0u, 0u, 0u, 0u};
+        if (c < nbody) {
+          const int64_t j = head + (int64_t)c * C::kVec;
+          gk[k] = load16_stream<DT>(a.g, row * a.ld_g + j);
+          sk[k] = load16_stream<DT>(a.saved, row * a.ld_s + j);
+        }
+      }
+      // With a body, the head and tail are fewer than two chunks' worth of elements (one per
+      // thread at most): loaded with the body chunks, so a row waits for memory once per pass
+      // instead of three times.
+      const bool few_scalar = nbody > 0;
+      int j_s = 0;
+      float g_s = 0.0f, x_s = 0.0f, w_s = 1.0f;
+      if (few_scalar && (int)threadIdx.x < nscalar) {
+        j_s = scalar_j(threadIdx.x);
+        g_s = C::load1(a.g, row * a.ld_g + j_s);
+        x_s = C::load1(a.saved, row * a.ld_s + j_s);
+        if (has_w) w_s = CW::load1(a.w, j_s);
+        if constexpr (SAVED_IS_H) x_s = x_s * rr;
+      }
       // the body chunk at element j: g and x-hat decoded, g * w formed as sum_term and finish do
-      auto body_chunk = [&](int64_t j, bool first, float* gf, float* gw, float* xh) {
-        C::unpack(first ? load16_stream<DT>(a.g, row * a.ld_g + j) : load16<DT>(a.g, row * a.ld_g + j), gf);
-        C::unpack(first ? load16_stream<DT>(a.saved, row * a.ld_s + j)
-                        : load16<DT>(a.saved, row * a.ld_s + j), xh);
+      auto body_chunk = [&](const u32x4& gq, const u32x4& sq, int64_t j, float* gf, float* gw,
+                            float* xh) {
+        C::unpack(gq, gf);
+        C::unpack(sq, xh);
+        float wf[C::kVec];
+        if (has_w) weight_run<DT, WDT>(a.w, j, w_align, wf);
 #pragma unroll
         for (int i = 0; i < C::kVec; ++i) {
           if constexpr (SAVED_IS_H) xh[i] = xh[i] * rr;
-          gw[i] = has_w ? gf[i] * CW::load1(a.w, j + i) : gf[i];
+          gw[i] = has_w ? gf[i] * wf[i] : gf[i];
         }
       };
-      for (int c = threadIdx.x; c < nbody; c += blockDim.x) {
+#pragma unroll
+      for (int k = 0; k < KR; ++k) {
+        const int c = threadIdx.x + k * blockDim.x;
+        if (c < nbody) {
+          float gf[C::kVec], gw[C::kVec], xh[C::kVec];
+          body_chunk(gk[k], sk[k], head + (int64_t)c * C::kVec, gf, gw, xh);
+#pragma unroll
+          for (int i = 0; i < C::kVec; ++i) s += gw[i] * xh[i];
+        }
+      }
+      for (int c = threadIdx.x + KR * blockDim.x; c < nbody; c += blockDim.x) {
+        const int64_t j = head + (int64_t)c * C::kVec;
         float gf[C::kVec], gw[C::kVec], xh[C::kVec];
-        body_chunk(head + (int64_t)c * C::kVec, true, gf, gw, xh);
+        body_chunk(load16<DT>(a.g, row * a.ld_g + j), load16<DT>(a.saved, row * a.ld_s + j), j,
+                   gf, gw, xh);
 #pragma unroll
         for (int i = 0; i < C::kVec; ++i) s += gw[i] * xh[i];
       }
-      for (int t = threadIdx.x; t < nscalar; t += blockDim.x) {
-        const int j = scalar_j(t);
-        s += sum_term(j, C::load1(a.g, row * a.ld_g + j));
+      if (few_scalar) {
+        if ((int)threadIdx.x < nscalar) s += (has_w ? g_s * w_s : g_s) * x_s;
+      } else {
+        for (int t = threadIdx.x; t < nscalar; t += blockDim.x) {
+          const int j = scalar_j(t);
+          s += sum_term(j, C::load1(a.g, row * a.ld_g + j));
+        }
       }
       s = row_sum(s, blockDim.x, 0, red[it & 1]);
       const float m = s / (float)a.dim;
-      // the second pass reads the body again (normally from L2)
-      for (int c = threadIdx.x; c < nbody; c += blockDim.x) {
-        const int64_t j = head + (int64_t)c * C::kVec;
-        float gf[C::kVec], gw[C::kVec], xh[C::kVec], d[C::kVec];
-        body_chunk(j, false, gf, gw, xh);
+      // dx of a body chunk, its stores and its dweight terms
+      auto finish_chunk = [&](int64_t j, const float* gf, const float* gw, const float* xh) {
+        float d[C::kVec];
 #pragma unroll
         for (int i = 0; i < C::kVec; ++i) d[i] = rr * (gw[i] - xh[i] * m);
         if constexpr (HAS_GH) {
@@ -1704,17 +1865,70 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
 #pragma unroll
           for (int i = 0; i < C::kVec; ++i) d[i] = d[i] + ghf[i];
         }
-        const u32x4 pv = C::pack(d);
-        store16_stream<DT>(a.dx, row * a.ld_dx + j, pv);
-        if (has_dres) store16_stream<DT>(a.dres, row * a.ld_dres + j, pv);
+        const u32x4 pk = C::pack(d);
+        store16_stream<DT>(a.dx, row * a.ld_dx + j, pk);
+        if (has_dres) store16_stream<DT>(a.dres, row * a.ld_dres + j, pk);
         if (prow != nullptr) {
+          float pv[C::kVec];
 #pragma unroll
-          for (int i = 0; i < C::kVec; ++i) accumulate((int)j + i, gf[i] * xh[i], it);
+          for (int i = 0; i < C::kVec; ++i) pv[i] = gf[i] * xh[i];
+          // the widest LDS accesses the chunk's first column allows: the dweight reduction costs
+          // 11.9 / 13.8 / 27.0 us at 16384 x 4100 / 4102 / 4099 bf16, whose chunks start 16-byte
+          // / 8-byte / any aligned in LDS; one word per element in a layout that spreads a
+          // chunk's columns across lanes (no bank conflicts, 8 accesses a chunk) cost ~25 us at
+          // all three
+          if (acc_in_lds && (j & 3) == 0) {
+            float4* a4 = reinterpret_cast<float4*>(acc_lds + j);
+#pragma unroll
+            for (int q = 0; q < C::kVec / 4; ++q) {
+              const float4 pq = {pv[4 * q], pv[4 * q + 1], pv[4 * q + 2], pv[4 * q + 3]};
+              a4[q] = (it == 0) ? pq : a4[q] + pq;
+            }
+          } else if (acc_in_lds && (j & 1) == 0) {
+            float2* a2 = reinterpret_cast<float2*>(acc_lds + j);
+#pragma unroll
+            for (int q = 0; q < C::kVec / 2; ++q) {
+              const float2 pq = {pv[2 * q], pv[2 * q + 1]};
+              a2[q] = (it == 0) ? pq : a2[q] + pq;
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < C::kVec; ++i) accumulate((int)j + i, pv[i], it);
+          }
+        }
+      };
+#pragma unroll
+      for (int k = 0; k < KR; ++k) {
+        const int c = threadIdx.x + k * blockDim.x;
+        if (c < nbody) {
+          const int64_t j = head + (int64_t)c * C::kVec;
+          float gf[C::kVec], gw[C::kVec], xh[C::kVec];
+          body_chunk(gk[k], sk[k], j, gf, gw, xh);
+          finish_chunk(j, gf, gw, xh);
         }
       }
-      for (int t = threadIdx.x; t < nscalar; t += blockDim.x) {
-        const int j = scalar_j(t);
-        finish(j, C::load1(a.g, row * a.ld_g + j), m);
+      for (int c = threadIdx.x + KR * blockDim.x; c < nbody; c += blockDim.x) {
+        const int64_t j = head + (int64_t)c * C::kVec;
+        float gf[C::kVec], gw[C::kVec], xh[C::kVec];
+        body_chunk(load16_stream<DT>(a.g, row * a.ld_g + j),
+                   load16_stream<DT>(a.saved, row * a.ld_s + j), j, gf, gw, xh);
+        finish_chunk(j, gf, gw, xh);
+      }
+      if (few_scalar) {
+        if ((int)threadIdx.x < nscalar) {
+          // finish's arithmetic on the register copies
+          const float gw = has_w ? g_s * w_s : g_s;
+          float d = rr * (gw - x_s * m);
+          if constexpr (HAS_GH) d = d + C::load1(a.gh, row * a.ld_gh + j_s);
+          C::store1(a.dx, row * a.ld_dx + j_s, d);
+          if (has_dres) C::store1(a.dres, row * a.ld_dres + j_s, d);
+          if (prow != nullptr) accumulate(j_s, g_s * x_s, it);
+        }
+      } else {
+        for (int t = threadIdx.x; t < nscalar; t += blockDim.x) {
+          const int j = scalar_j(t);
+          finish(j, C::load1(a.g, row * a.ld_g + j), m);
+        }
       }
     }
   }
