@@ -1788,16 +1788,20 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
       // are read in the first pass with the normal cache policy and again, non-temporally,
       // in the second (normally from L2).
       constexpr int KR = 4;
-      u32x4 gk[KR], sk[KR];
+      // (grad_h's register chunks too, loaded with them: its loads in the second pass, after
+      // the row reduction, cost a memory wait per row)
+      u32x4 gk[KR], sk[KR], hk[HAS_GH ? KR : 1];
 #pragma unroll
       for (int k = 0; k < KR; ++k) {
         const int c = threadIdx.x + k * blockDim.x;
         gk[k] = u32x4{0u, 0u, 0u, 0u};
         sk[k] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (HAS_GH) hk[k] = u32x4{0u, 0u, 0u, 0u};
         if (c < nbody) {
           const int64_t j = head + (int64_t)c * C::kVec;
           gk[k] = load16_stream<DT>(a.g, row * a.ld_g + j);
           sk[k] = load16_stream<DT>(a.saved, row * a.ld_s + j);
+          if constexpr (HAS_GH) hk[k] = load16_stream<DT>(a.gh, row * a.ld_gh + j);
         }
       }
       // With a body, the head and tail are fewer than two chunks' worth of elements (one per
@@ -1806,11 +1810,13 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
       const bool few_scalar = nbody > 0;
       int j_s = 0;
       float g_s = 0.0f, x_s = 0.0f, w_s = 1.0f;
+      float gh_s = 0.0f;
       if (few_scalar && (int)threadIdx.x < nscalar) {
         j_s = scalar_j(threadIdx.x);
         g_s = C::load1(a.g, row * a.ld_g + j_s);
         x_s = C::load1(a.saved, row * a.ld_s + j_s);
         if (has_w) w_s = CW::load1(a.w, j_s);
+        if constexpr (HAS_GH) gh_s = C::load1(a.gh, row * a.ld_gh + j_s);
         if constexpr (SAVED_IS_H) x_s = x_s * rr;
       }
       // the body chunk at element j: g and x-hat decoded, g * w formed as sum_term and finish do
@@ -1855,13 +1861,15 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
       s = row_sum(s, blockDim.x, 0, red[it & 1]);
       const float m = s / (float)a.dim;
       // dx of a body chunk, its stores and its dweight terms
-      auto finish_chunk = [&](int64_t j, const float* gf, const float* gw, const float* xh) {
+      // `ghq`: the chunk's grad_h when it is already in registers, else null (loaded here)
+      auto finish_chunk = [&](int64_t j, const float* gf, const float* gw, const float* xh,
+                              const u32x4* ghq) {
         float d[C::kVec];
 #pragma unroll
         for (int i = 0; i < C::kVec; ++i) d[i] = rr * (gw[i] - xh[i] * m);
         if constexpr (HAS_GH) {
           float ghf[C::kVec];
-          C::unpack(load16_stream<DT>(a.gh, row * a.ld_gh + j), ghf);
+          C::unpack(ghq != nullptr ? *ghq : load16_stream<DT>(a.gh, row * a.ld_gh + j), ghf);
 #pragma unroll
           for (int i = 0; i < C::kVec; ++i) d[i] = d[i] + ghf[i];
         }
@@ -1904,7 +1912,7 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
           const int64_t j = head + (int64_t)c * C::kVec;
           float gf[C::kVec], gw[C::kVec], xh[C::kVec];
           body_chunk(gk[k], sk[k], j, gf, gw, xh);
-          finish_chunk(j, gf, gw, xh);
+          finish_chunk(j, gf, gw, xh, HAS_GH ? &hk[k] : nullptr);
         }
       }
       for (int c = threadIdx.x + KR * blockDim.x; c < nbody; c += blockDim.x) {
@@ -1912,14 +1920,14 @@ __global__ __launch_bounds__(kGenericBlock) void bwd_generic_kernel(const BwdArg
         float gf[C::kVec], gw[C::kVec], xh[C::kVec];
         body_chunk(load16_stream<DT>(a.g, row * a.ld_g + j),
                    load16_stream<DT>(a.saved, row * a.ld_s + j), j, gf, gw, xh);
-        finish_chunk(j, gf, gw, xh);
+        finish_chunk(j, gf, gw, xh, nullptr);
       }
       if (few_scalar) {
         if ((int)threadIdx.x < nscalar) {
           // finish's arithmetic on the register copies
           const float gw = has_w ? g_s * w_s : g_s;
           float d = rr * (gw - x_s * m);
-          if constexpr (HAS_GH) d = d + C::load1(a.gh, row * a.ld_gh + j_s);
+          if constexpr (HAS_GH) d = d + gh_s;
           C::store1(a.dx, row * a.ld_dx + j_s, d);
           if (has_dres) C::store1(a.dres, row * a.ld_dres + j_s, d);
           if (prow != nullptr) accumulate(j_s, g_s * x_s, it);
