@@ -133,8 +133,16 @@ int main() {
                     check_row_plan(rg.rp, dim, eb, aligned != 0);
                     CHECK(ring_eligible(rg.rp, dim, eb), "ring plan not eligible dim=%lld",
                           (long long)dim);
-                    CHECK((int64_t)rg.rp.nv * rg.rp.tpr * (16 / eb) == dim,
-                          "ring plan over a partial row dim=%lld", (long long)dim);
+                    {
+                      // whole waves over the row's chunks, at most 1/8 of the slots idle, and
+                      // fewer idle slots than one chunk per lane
+                      const int64_t slots = (int64_t)rg.rp.nv * rg.rp.tpr;
+                      const int64_t chunks = dim / (16 / eb);
+                      CHECK(dim % (16 / eb) == 0 && slots >= chunks &&
+                                (slots - chunks) * 8 <= slots && slots - chunks < rg.rp.tpr,
+                            "ring plan idle lanes dim=%lld slots=%lld", (long long)dim,
+                            (long long)slots);
+                    }
                     CHECK(rg.rp.block <= kRingBlock && rg.rp.nv <= kRingMaxNV,
                           "ring block %d nv %d", rg.rp.block, rg.rp.nv);
                     CHECK(rg.wgs >= 1 && rg.wgs <= cus &&
@@ -147,7 +155,8 @@ int main() {
                               (rg.lds_bytes == 0) == (rg.rp.groups == 1),
                           "ring lds %zu", rg.lds_bytes);
                   } else {
-                    CHECK(!ring_eligible(rg.rp, dim, eb), "eligible ring plan refused");
+                    CHECK(!ring_eligible(rg.rp, dim, eb) || !ring_tail_pays(rg.rp, dim, eb),
+                          "eligible ring plan refused");
                   }
                   // the ring plan under its tuning knobs (workgroup bound, workgroups per CU):
                   // the same facts, at most two workgroups of at most kRingBlock / 2 threads per
@@ -158,7 +167,8 @@ int main() {
                       const BwdPlan rk = plan_bwd_ring(rows, dim, eb, aligned != 0, cus, prefer,
                                                        rb, wpc);
                       if (!rk.ring) {
-                        CHECK(!ring_eligible(rk.rp, dim, eb) || rk.rp.tpr > rb,
+                        CHECK(!ring_eligible(rk.rp, dim, eb) || rk.rp.tpr > rb ||
+                                  !ring_tail_pays(rk.rp, dim, eb),
                               "ring refused under knobs rb=%d wpc=%d dim=%lld", rb, wpc,
                               (long long)dim);
                         continue;
@@ -258,6 +268,22 @@ int main() {
             rope_walk_ok(16448, 2048, 64) && !rope_walk_ok(6000, 512, 1000),
         "rope_walk_ok on the test shapes");
   printf("rope walks checked: %ld\n", walks);
+  // The ring backward over rows with idle lanes: bf16 rows of 1000, 3000, 4000 and 5000 leave
+  // 3, 9, 12 and 15 of their chunk slots idle and take it; 768, 2056 and 4104 would leave more
+  // than 1/8 idle, 2240 has one chunk per thread in 320-thread rows and 7160 and 8184 two in
+  // 448- and 512-thread rows that are not whole 128-byte lines: those stay on bwd_vec_kernel,
+  // as do none of the whole rows (2560 in 320-thread rows, 8192).
+  for (int64_t dim : {1000, 3000, 4000, 5000, 768, 2056, 4104, 2240, 7160, 8184, 2560, 8192,
+                      6272, 3576}) {
+    const BwdPlan rg = plan_bwd_ring(16384, dim, 2, true, 256, 0);
+    const int64_t idle = (int64_t)rg.rp.nv * rg.rp.tpr - dim / 8;
+    const bool want = dim == 1000 || dim == 3000 || dim == 4000 || dim == 5000 || dim == 2560 ||
+                      dim == 8192 || dim == 6272 || dim == 3576;
+    CHECK(rg.ring == want, "ring plan over %lld bf16 columns: %d", (long long)dim, (int)rg.ring);
+    CHECK(!want || idle == (dim == 1000 ? 3 : dim == 3000 ? 9 : dim == 4000 ? 12 :
+                            dim == 5000 ? 15 : dim == 6272 ? 112 : dim == 3576 ? 1 : 0),
+          "idle chunk slots at %lld: %lld", (long long)dim, (long long)idle);
+  }
   // Where the forward stores h: after the reduction for the measured bf16 rows of 2048, 3072
   // and 4096 (whole rows of at most 512 threads), before it for 5120, 7168 and 8192, and never
   // on the generic path.

@@ -1,11 +1,12 @@
-"""The ring-pipelined backward (bwd_ring_kernel, the default for whole rows of up to 512 threads
-and two 16-byte chunks per thread) against the oracle, at row counts that put every pattern of
-its loop to work: rows fewer than the row slots (no steady iteration), whole rings of
-iterations, and one or two iterations past the last whole ring, with and without rows missing in
-the last one; the ring holds three rows (two with grad_h).  Its per-row arithmetic is that of
-bwd_vec_kernel, so dx must equal that kernel's bit for bit (the child process below runs it with
-VELOGRAD_BWD_RING=0); dweight groups its partial sums by other row slots, so it is held to the
-dweight tolerance."""
+"""The ring-pipelined backward (bwd_ring_kernel, the default for rows of whole 16-byte chunks
+over up to 512 threads and two chunks per thread, at most 1/8 of the lanes idle) against the
+oracle, at row counts that put every pattern of its loop to work: rows fewer than the row slots
+(no steady iteration), whole rings of iterations, and one or two iterations past the last whole
+ring, with and without rows missing in the last one; the ring holds three rows (two with
+grad_h).  Rows that leave lanes idle are checked over every dtype and both chunk counts.  Its
+per-row arithmetic is that of bwd_vec_kernel, so dx must equal that kernel's bit for bit (the
+child process below runs it with VELOGRAD_BWD_RING=0); dweight groups its partial sums by other
+row slots, so it is held to the dweight tolerance."""
 
 import json
 import os
@@ -95,9 +96,9 @@ np.savez(sys.argv[3], **out)
 """
 
 
-def test_ring_dx_equals_the_previous_kernel_bitwise(tmp_path):
+def _bitwise_against_previous_kernel(layouts, tmp_path):
     cases = [(r, d, str(dt).split(".")[-1], str(wdt).split(".")[-1], gh)
-             for r, d, dt, wdt, gh in LAYOUTS]
+             for r, d, dt, wdt, gh in layouts]
     path = str(tmp_path / "legacy.npz")
     env = dict(os.environ, VELOGRAD_BWD_RING="0")
     print("child process: the same backwards with VELOGRAD_BWD_RING=0", flush=True)
@@ -105,7 +106,7 @@ def test_ring_dx_equals_the_previous_kernel_bitwise(tmp_path):
                        capture_output=True, text=True, timeout=110)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
     legacy = np.load(path)
-    for i, (rows, d, dt, wdt, gh) in enumerate(LAYOUTS):
+    for i, (rows, d, dt, wdt, gh) in enumerate(layouts):
         print(f"ring vs previous kernel: {rows}x{d} {dt} w={wdt} grad_h={gh}", flush=True)
         rng = np.random.default_rng(rows * 7 + d)
         h = P.to_device(P.gaussian(rng, (rows, d)), dt)
@@ -117,6 +118,46 @@ def test_ring_dx_equals_the_previous_kernel_bitwise(tmp_path):
         bits = dx.view(torch.int16 if dx.element_size() == 2 else torch.int32).cpu().numpy()
         assert np.array_equal(bits, legacy[f"dx{i}"]), f"dx differs at {rows}x{d} {dt}"
         _check_oracle(dx, dw, h, g, w, inv, ghv, f"{rows}x{d} {dt}")
+
+
+def test_ring_dx_equals_the_previous_kernel_bitwise(tmp_path):
+    _bitwise_against_previous_kernel(LAYOUTS, tmp_path)
+
+
+# Rows of fewer 16-byte chunks than their row group's lanes hold (at most 1/8 of the slots idle):
+# the idle lanes reload the row's last chunk, add nothing to the row's sum and dweight and store
+# nothing.  (rows, dim, dtype, weight dtype, grad_h); the comments give idle / all chunk slots.
+IDLE = [(1537, 4000, torch.bfloat16, torch.bfloat16, False),  # 12/512, two row groups a workgroup
+        (2049, 5000, torch.bfloat16, torch.bfloat16, True),   # 15/640, one 320-thread row group
+        (1000, 3000, torch.float16, torch.float32, False),    # 9/384, two 192-thread row groups
+        (4097, 1000, torch.bfloat16, torch.bfloat16, True),   # 3/128, eight 64-thread row groups
+        (3001, 2000, torch.float32, torch.float32, False),    # 12/512
+        (777, 1000, torch.float32, torch.float32, True),      # 6/256, fewer rows than row slots
+        (999, 456, torch.bfloat16, torch.float32, True),      # 7/64, one chunk per thread
+        (2500, 3200, torch.float16, torch.float16, False),    # 48/448, one chunk per thread
+        (700, 6272, torch.bfloat16, torch.bfloat16, True)]    # 112/896, 448-thread row groups
+
+
+@pytest.mark.parametrize("rows,d,dt,wdt,gh", IDLE,
+                         ids=[f"{r}x{d}-{str(t).split('.')[-1]}" for r, d, t, _, _ in IDLE])
+def test_ring_idle_lanes_match_oracle(rows, d, dt, wdt, gh):
+    print(f"ring backward with idle lanes {rows}x{d} {dt} w={wdt} grad_h={gh}", flush=True)
+    h, g, w, inv, ghv = _inputs(rows, d, dt, wdt, rows + d, gh)
+    dres = torch.empty_like(g)
+    dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=ghv,
+                                                dresidual_out=dres)
+    torch.cuda.synchronize()
+    _check_oracle(dx, dw, h, g, w, inv, ghv, f"{rows}x{d} {dt}")
+    assert torch.equal(dres, dx)
+    acc = np.einsum("rd,rd->d", P.upcast(g).astype(np.float64),
+                    (P.upcast(h) * P.upcast(inv)).astype(np.float64))
+    P.assert_dweight(P.upcast(dw), acc, "dweight vs float64")
+    dx2, dw2 = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=ghv)
+    assert torch.equal(dx, dx2) and torch.equal(dw, dw2)
+
+
+def test_ring_idle_lanes_dx_equals_the_previous_kernel_bitwise(tmp_path):
+    _bitwise_against_previous_kernel(IDLE, tmp_path)
 
 
 def test_ring_dres_and_in_place_grad_h():

@@ -159,8 +159,9 @@ struct BwdPlan {
 
 // The ring-pipelined backward (bwd_ring_kernel): a ring of kRingPrefetch + 1 row buffers per
 // thread, so two rows are in flight while one reduces, in a branch-free steady loop.  It takes
-// whole rows only (dim == nv * tpr * V: every lane busy, no chunk guards), at most two chunks per
-// thread, and workgroups of at most kRingBlock threads (its launch bound: 256 VGPRs a lane for
+// rows of whole 16-byte chunks over whole waves (dim <= nv * tpr * V, at most 1/8 of the chunk
+// slots idle; idle lanes reload the row's last chunk, so no branch guards a load), at most two
+// chunks per thread, and workgroups of at most kRingBlock threads (its launch bound: 256 VGPRs a lane for
 // the three row buffers), one per CU, so each row slot walks twice as many rows as in the
 // 1024-thread persistent kernel.  Measured on MI355X at 16384 x 4096 bf16: 69.2 us against 72.4.
 constexpr int kRingBlock = 512;
@@ -192,10 +193,34 @@ inline BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned,
 }
 
 // Whether a row plan suits the ring-pipelined backward (see kRingBlock).
+// Rows may leave lanes idle (whole waves over fewer chunks), at most 1/8 of the row group's
+// chunk slots: the kernel's idle-lane variant (kRingTail) reloads the row's last chunk there.
 inline bool ring_eligible(const RowPlan& p, int64_t dim, int elem_bytes) {
   if (!p.vec || (elem_bytes != 2 && elem_bytes != 4)) return false;
-  return p.nv >= 1 && p.nv <= kRingMaxNV && p.tpr <= kRingBlock &&
-         (int64_t)p.nv * p.tpr * (16 / elem_bytes) == dim;
+  const int V = 16 / elem_bytes;
+  const int64_t slots = (int64_t)p.nv * p.tpr;
+  if (dim % V != 0) return false;
+  const int64_t chunks = dim / V;
+  return p.nv >= 1 && p.nv <= kRingMaxNV && p.tpr <= kRingBlock && chunks >= 1 &&
+         slots >= chunks && slots - chunks < p.tpr && (slots - chunks) * 8 <= slots;
+}
+
+// Whether the ring's idle-lane variant is planned for rows that leave lanes idle (whole rows
+// always take the ring).  Measured on MI355X against bwd_vec_kernel (16384 rows, backward only,
+// two alternating processes each, best of 3 batched rounds): faster everywhere except (a) rows
+// of one chunk per thread in 320-thread row groups, whose workgroup alone on its CU holds five
+// waves (2240 bf16: 56.1 us against 51.4; 1120 fp32 56.6 against 50.7), and (b) rows of two
+// chunks per thread in row groups of 448 or 512 threads that are not whole 128-byte lines (bf16
+// 7160: 131.0 against 125.4, 7176: 132.2 against 127.7, 8184: 150.2 against 148.3), where the
+// workgroup's seven or eight waves hold the ring while bwd_vec_kernel keeps twice the waves;
+// whole lines there still pay (6272 bf16: 105.8 against 112.9).  Elsewhere, e.g. bf16 4000:
+// 71.3 against 73.4, 5000 87.0 against 91.9, 3576 63.2 against 75.8, fp32 2240 74.4 against
+// 84.9.
+inline bool ring_tail_pays(const RowPlan& p, int64_t dim, int elem_bytes) {
+  const int64_t chunks = dim / (16 / elem_bytes);
+  if ((int64_t)p.nv * p.tpr == chunks) return true;
+  if (p.nv == 1) return (kRingBlock / p.tpr) * p.tpr >= 6 * kWave;
+  return p.tpr < 448 || (dim * elem_bytes) % 128 == 0;
 }
 
 // Plan of the ring-pipelined backward: row groups packed into workgroups of up to kRingBlock
@@ -213,7 +238,8 @@ inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool ali
   if (max_block > kRingBlock) max_block = kRingBlock;
   if (wgs_per_cu < 1) wgs_per_cu = 1;
   if (wgs_per_cu > 2) wgs_per_cu = 2;
-  b.ring = ring_eligible(b.rp, dim, elem_bytes) && b.rp.tpr <= max_block;
+  b.ring = ring_eligible(b.rp, dim, elem_bytes) && b.rp.tpr <= max_block &&
+           ring_tail_pays(b.rp, dim, elem_bytes);
   if (!b.ring) return b;
   if (b.rp.tpr * wgs_per_cu > kRingBlock) wgs_per_cu = 1;  // a row group fills the CU's waves
   RowPlan& p = b.rp;

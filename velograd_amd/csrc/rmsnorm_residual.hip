@@ -20,9 +20,10 @@
 //                       row's loads in flight while the current row reduces; the weight chunk and
 //                       the fp32 dweight column accumulators stay in registers for the whole walk;
 //                       each slot finally writes one fp32 partial row (no atomics).
-//   bwd_ring_kernel     the same walk for whole rows with a ring of three row buffers (two rows
-//                       in flight while one reduces) in a branch-free steady loop, 512-thread
-//                       workgroups, one per CU: the backward's default where the rows suit it.
+//   bwd_ring_kernel     the same walk for rows of whole 16-byte chunks (at most 1/8 of the lanes
+//                       idle) with a ring of three row buffers (two rows in flight while one
+//                       reduces) in a branch-free steady loop, 512-thread workgroups, one per
+//                       CU: the backward's default where the rows suit it.
 //   fwd_rope_kernel     the forward with the model's interleaved RoPE on y: strided row walks
 //                       with the rotation advanced by a recurrence.
 //   bwd_rope_ring_kernel  its backward (grad_y rotated back, then the norm's backward) in
@@ -1269,16 +1270,18 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward, whole rows, ring-pipelined (launch_plan.h: plan_bwd_ring).  Each row slot walks rows
-// slot, slot + S, ... as in bwd_vec_kernel, but keeps a ring of PF + 1 = 3 row buffers (2 with
-// grad_h): while a row reduces, the next two rows' loads are in flight.  Rows are whole (dim == NV * tpr * V),
-// and the steady loop covers only iterations in which every slot has a row, loading prefetch
-// rows past the end from the last row instead (never used), so it is free of branches around
-// memory operations: the wait for a row's data then counts exactly the later loads and stores
-// instead of draining them, which a guarded loop forces.  The loop is unrolled by the ring
-// length so the buffers are indexed at compile time.  kRingDres: dres is written too.
+// Backward, ring-pipelined (launch_plan.h: plan_bwd_ring).  Each row slot walks rows slot,
+// slot + S, ... as in bwd_vec_kernel, but keeps a ring of PF + 1 = 3 row buffers (2 with
+// grad_h): while a row reduces, the next two rows' loads are in flight.  Rows are of whole
+// 16-byte chunks, dim <= NV * tpr * V (kRingTail where lanes are left idle), and the steady loop
+// covers only iterations in which every slot has a row, loading prefetch rows past the end from
+// the last row instead (never used), so it is free of branches around memory operations: the
+// wait for a row's data then counts exactly the later loads and stores instead of draining them,
+// which a guarded loop forces.  The loop is unrolled by the ring length so the buffers are
+// indexed at compile time.  kRingDres: dres is written too.
 // ------------------------------------------------------------------------------------------
 constexpr int kRingDres = 8;
+constexpr int kRingTail = 32;
 
 template <int DT, int WDT, int NV, int FLAGS>
 __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const BwdArgs a) {
@@ -1287,6 +1290,10 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
   constexpr bool SAVED_IS_H = (FLAGS & kSavedIsH) != 0;
   constexpr bool HAS_GH = (FLAGS & kGradH) != 0;
   constexpr bool HAS_DRES = (FLAGS & kRingDres) != 0;
+  // kRingTail: rows of fewer chunks than the row group's lanes (whole waves, at most 1/8 idle):
+  // an idle lane loads the row's last chunk instead (no branch around the load), adds nothing
+  // and stores nothing
+  constexpr bool TAIL = (FLAGS & kRingTail) != 0;
   constexpr int NH = HAS_GH ? NV : 1;  // grad_h chunks (a dummy slot when absent)
   // With grad_h a third stream fills the ring: one row ahead keeps it within 256 VGPRs.
   constexpr int PF = HAS_GH ? 1 : vg_plan::kRingPrefetch;
@@ -1303,12 +1310,21 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
   const int64_t nslots = (int64_t)gridDim.x * groups;
   const bool has_w = a.w != nullptr;
   const int64_t last = a.rows - 1;
+  // chunk k of this lane (the row's last one for an idle lane) and whether it is its own
+  int chunk[NV];
+  bool own[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = lt + k * tpr;
+    own[k] = !TAIL || c < a.dim / V;
+    chunk[k] = own[k] ? c : a.dim / V - 1;
+  }
 
   WeightChunk<DT, WDT> wc[NV];
   float acc[NV][V];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    wc[k].load(has_w ? a.w : nullptr, (int64_t)(lt + k * tpr) * V);
+    wc[k].load(has_w ? a.w : nullptr, (int64_t)chunk[k] * V);
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[k][i] = 0.0f;
   }
@@ -1321,7 +1337,7 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
     r = a.inv_rms[rw];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int64_t col = (int64_t)(lt + k * tpr) * V;
+      const int64_t col = (int64_t)chunk[k] * V;
       gv[k] = load16_stream<DT>(a.g, rw * a.ld_g + col);
       sv[k] = load16_stream<DT>(a.saved, rw * a.ld_s + col);
       if constexpr (HAS_GH) hv[k] = load16_stream<DT>(a.gh, rw * a.ld_gh + col);
@@ -1352,14 +1368,19 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         gwk[k][i] = gfk[k][i] * wf[i];
-        s += gwk[k][i] * xhk[k][i];
+        if constexpr (TAIL) {
+          const float t = gwk[k][i] * xhk[k][i];
+          s += own[k] ? t : 0.0f;
+        } else {
+          s += gwk[k][i] * xhk[k][i];
+        }
       }
     }
     s = row_sum(s, tpr, grp, red[it & 1]);
     const float m = s / (float)a.dim;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int64_t col = (int64_t)(lt + k * tpr) * V;
+      const int64_t col = (int64_t)chunk[k] * V;
       const float* gf = gfk[k];
       const float* xh = xhk[k];
       float d[V];
@@ -1372,12 +1393,13 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
         for (int i = 0; i < V; ++i) d[i] = d[i] + ghf[i];
       }
       const u32x4 pv = C::pack(d);
-      if (ok) {
+      const bool store = TAIL ? ok && own[k] : ok;
+      if (store) {
         store16_stream<DT>(a.dx, row * a.ld_dx + col, pv);
         if constexpr (HAS_DRES) store16_stream<DT>(a.dres, row * a.ld_dres + col, pv);
       }
 #pragma unroll
-      for (int i = 0; i < V; ++i) acc[k][i] += ok ? gf[i] * xh[i] : 0.0f;
+      for (int i = 0; i < V; ++i) acc[k][i] += store ? gf[i] * xh[i] : 0.0f;
     }
   };
 
@@ -1413,7 +1435,8 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
   if (groups == 1) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int c = lt + k * tpr;
+      if (!own[k]) continue;
+      const int c = chunk[k];
 #pragma unroll
       for (int q = 0; q < V / 4; ++q)
         store16<VELOGRAD_DTYPE_F32>(prow, (int64_t)c * V + 4 * q,
@@ -1426,7 +1449,8 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
     if (grp == gi) {
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
-        const int c = lt + k * tpr;
+        if (!own[k]) continue;
+        const int c = chunk[k];
 #pragma unroll
         for (int i = 0; i < V; ++i)
           comb[c * V + i] = (gi == 0) ? acc[k][i] : comb[c * V + i] + acc[k][i];
@@ -2126,6 +2150,16 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
 template <int DT, int WDT, int F>
 void launch_bwd_ring(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
   const dim3 grid((uint32_t)b.wgs), block(b.rp.block);
+  // rows of fewer chunks than the row group's lanes take the idle-lane variant
+  if ((int64_t)b.rp.nv * b.rp.tpr * Codec<DT>::kVec != a.dim) {
+    if (b.rp.nv == 1)
+      hipLaunchKernelGGL((bwd_ring_kernel<DT, WDT, 1, F | kRingTail>), grid, block, b.lds_bytes,
+                         st, a);
+    else
+      hipLaunchKernelGGL((bwd_ring_kernel<DT, WDT, 2, F | kRingTail>), grid, block, b.lds_bytes,
+                         st, a);
+    return;
+  }
   if (b.rp.nv == 1)
     hipLaunchKernelGGL((bwd_ring_kernel<DT, WDT, 1, F>), grid, block, b.lds_bytes, st, a);
   else
