@@ -268,6 +268,42 @@ int main() {
             rope_walk_ok(16448, 2048, 64) && !rope_walk_ok(6000, 512, 1000),
         "rope_walk_ok on the test shapes");
   printf("rope walks checked: %ld\n", walks);
+  // The ring over rows of 8-byte alignment (kRing8): 2-byte dims of 8n + 4 only, one chunk per
+  // thread over the n whole chunks (a ring plan of dim - 4 columns), LDS for all dim columns when
+  // row groups combine, partial rows within the workspace query; 4100 and 2052 take it with
+  // 512- and 256-thread row groups, 4108 (513 whole chunks) and 100 (12 of 64 lanes) do not.
+  long ring8 = 0;
+  for (int64_t dim = 4; dim <= 8200; dim += 4) {
+    for (int64_t rows : {1, 300, 16384}) {
+      for (int eb = 2; eb <= 4; eb += 2) {
+        const BwdPlan r8 = plan_bwd_ring8(rows, dim, eb, 256);
+        if (!r8.ring) {
+          CHECK(!r8.x8, "refused ring8 plan marked x8 (dim=%lld)", (long long)dim);
+          continue;
+        }
+        ++ring8;
+        CHECK(eb == 2 && dim % 8 == 4 && r8.x8 && r8.rp.nv == 1, "ring8 plan dim=%lld eb=%d",
+              (long long)dim, eb);
+        check_row_plan(r8.rp, dim - 4, eb, true);
+        CHECK(ring_eligible(r8.rp, dim - 4, eb) && r8.rp.block <= kRingBlock,
+              "ring8 layout dim=%lld", (long long)dim);
+        CHECK(r8.lds_bytes == (r8.rp.groups > 1 ? (size_t)dim * sizeof(float) : 0),
+              "ring8 lds %zu dim=%lld", r8.lds_bytes, (long long)dim);
+        const size_t ws = bwd_workspace_bytes(rows, dim, 256, 0, 1024, 16);
+        CHECK((size_t)r8.wgs * (size_t)dim * sizeof(float) <= ws && r8.wgs <= 256,
+              "ring8 partials %lld x %lld exceed workspace %zu", (long long)r8.wgs,
+              (long long)dim, ws);
+      }
+    }
+  }
+  CHECK(plan_bwd_ring8(16384, 4100, 2, 256).ring && plan_bwd_ring8(16384, 4100, 2, 256).rp.tpr == 512,
+        "ring8 at 4100");
+  CHECK(plan_bwd_ring8(16384, 2052, 2, 256).ring && plan_bwd_ring8(16384, 2052, 2, 256).rp.tpr == 256,
+        "ring8 at 2052");
+  CHECK(!plan_bwd_ring8(16384, 4108, 2, 256).ring && !plan_bwd_ring8(16384, 100, 2, 256).ring &&
+            !plan_bwd_ring8(16384, 4100, 4, 256).ring && !plan_bwd_ring8(16384, 4104, 2, 256).ring,
+        "ring8 refusals");
+  printf("ring8 plans checked: %ld\n", ring8);
   // The ring backward over rows with idle lanes: bf16 rows of 1000, 3000, 4000 and 5000 leave
   // 3, 9, 12 and 15 of their chunk slots idle and take it; 768, 2056 and 4104 would leave more
   // than 1/8 idle, 2240 has one chunk per thread in 320-thread rows and 7160 and 8184 two in

@@ -160,6 +160,87 @@ def test_ring_idle_lanes_dx_equals_the_previous_kernel_bitwise(tmp_path):
     _bitwise_against_previous_kernel(IDLE, tmp_path)
 
 
+# Rows of 8n + 4 two-byte elements (hidden sizes such as 4100), whose rows start on 8-byte
+# boundaries only: each whole chunk moves as two 8-byte halves and the row's last 4 elements form
+# an extra half chunk of the row group's lane 0.  (rows, dim, dtype, weight dtype or None,
+# grad_h); one chunk per thread in row groups of 512, 256 and 128 threads, one idle lane (4092).
+RING8 = [(2049, 4100, torch.bfloat16, torch.bfloat16, False),
+         (1537, 4100, torch.float16, torch.float32, True),
+         (999, 2052, torch.bfloat16, torch.float32, False),   # two row groups a workgroup
+         (4097, 1028, torch.bfloat16, torch.bfloat16, True),  # four row groups a workgroup
+         (300, 4092, torch.float16, torch.float16, False),    # 511 whole chunks over 512 lanes
+         (5000, 4100, torch.bfloat16, None, False)]
+
+
+@pytest.mark.parametrize("rows,d,dt,wdt,gh", RING8,
+                         ids=[f"{r}x{d}-{str(t).split('.')[-1]}" for r, d, t, _, _ in RING8])
+def test_ring_rows_of_8_byte_alignment_match_oracle(rows, d, dt, wdt, gh):
+    print(f"ring backward, rows of 8-byte alignment {rows}x{d} {dt} w={wdt} grad_h={gh}",
+          flush=True)
+    rng = np.random.default_rng(rows + d)
+    h = P.to_device(P.gaussian(rng, (rows, d)), dt)
+    g = P.to_device(P.gaussian(rng, (rows, d)), dt)
+    w = P.to_device(P.weight_vec(rng, d), wdt) if wdt is not None else None
+    ghv = P.to_device(P.gaussian(rng, (rows, d)), dt) if gh else None
+    _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
+    dres = torch.empty_like(g)
+    dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=ghv,
+                                                dresidual_out=dres)
+    torch.cuda.synchronize()
+    g32, h32, r32 = P.upcast(g), P.upcast(h), P.upcast(inv)
+    w32 = P.upcast(w) if w is not None else None
+    xhat = h32 * r32
+    gw = g32 * w32 if w32 is not None else g32
+    if ghv is None:
+        rdx, rdw = ora.fused_rmsnorm_residual_backward(g32, xhat, w32, r32)
+    else:
+        rdx, rdw = ora.backward_with_residual_grad(g32, xhat, w32, r32, P.upcast(ghv))
+    P.dx_check(dx, rdx, gw, xhat, r32, f"{rows}x{d}",
+               grad_h=None if ghv is None else P.upcast(ghv))
+    assert torch.equal(dres, dx)
+    if w is None:
+        assert dw is None
+    else:
+        P.assert_dweight(P.upcast(dw), rdw.reshape(-1), f"{rows}x{d}")
+        acc = np.einsum("rd,rd->d", g32.astype(np.float64), xhat.astype(np.float64))
+        P.assert_dweight(P.upcast(dw), acc, "dweight vs float64")
+    dx2, dw2 = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=ghv)
+    assert torch.equal(dx, dx2)
+    if w is not None:
+        assert torch.equal(dw, dw2)
+
+
+def test_ring_rows_of_8_byte_alignment_in_wider_tensors():
+    """Streams of different row strides, all multiples of 8 bytes: g and dx in rows of 4104
+    elements, h in rows of 4100 (through the C ABI); the rows' places inside their 16-byte lines
+    then differ from stream to stream and from row to row."""
+    from velograd_amd import _lib
+    lib = _lib.load()
+    print("ring backward, 8-byte rows in tensors of strides 4104 and 4100", flush=True)
+    rows, d, wide = 1500, 4100, 4104
+    rng = np.random.default_rng(4100)
+    h = P.to_device(P.gaussian(rng, (rows, d)), torch.bfloat16)
+    gw = P.to_device(P.gaussian(rng, (rows, wide)), torch.bfloat16)
+    w = P.to_device(P.weight_vec(rng, d), torch.bfloat16)
+    _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
+    g = gw[:, :d].contiguous()
+    ref_dx, ref_dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True)
+    out = torch.full((rows, wide), 7.0, device="cuda", dtype=torch.bfloat16)
+    dw = torch.empty(d, device="cuda", dtype=torch.float32)
+    ws_bytes = vk.bwd_workspace_bytes(rows, d, torch.device("cuda"))
+    ws = torch.empty(ws_bytes, device="cuda", dtype=torch.uint8)
+    inv1 = inv.reshape(rows).contiguous()
+    rc = lib.velograd_rmsnorm_residual_bwd(
+        gw.data_ptr(), h.data_ptr(), 1, w.data_ptr(), inv1.data_ptr(), None, out.data_ptr(), None,
+        dw.data_ptr(), ws.data_ptr(), ws_bytes, rows, d, wide, d, d, wide, d,
+        _lib.DTYPE_BF16, _lib.DTYPE_BF16, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "ring backward over strided 8-byte rows")
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :d], ref_dx) and torch.equal(dw, ref_dw)
+    assert bool((out[:, d:] == 7.0).all()), "a store left its row"
+    _check_oracle(ref_dx, ref_dw, h, g, w, inv, None, "strided 8-byte rows")
+
+
 def test_ring_dres_and_in_place_grad_h():
     """dres gets the same bits as dx; dx may be grad_h itself (accumulation in place)."""
     from velograd_amd import _lib

@@ -169,6 +169,29 @@ __device__ inline void store16_stream(void* base, int64_t elem, const u32x4 v) {
 #endif
 }
 
+// Half a chunk (8 bytes) of a stream whose rows start on 8-byte boundaries only, with the same
+// cache policy as the 16-byte forms.
+template <int DT>
+__device__ inline u32x2 load8_stream(const void* base, int64_t elem) {
+  const u32x2* p = reinterpret_cast<const u32x2*>(static_cast<const char*>(base) +
+                                                  elem * Codec<DT>::kBytes);
+#if VG_STREAM_NT_LOAD
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
+template <int DT>
+__device__ inline void store8_stream(void* base, int64_t elem, const u32x2 v) {
+  u32x2* p = reinterpret_cast<u32x2*>(static_cast<char*>(base) + elem * Codec<DT>::kBytes);
+#if VG_STREAM_NT_STORE
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
+
 // ------------------------------------------------------------------------------------------
 // Reductions.
 // ------------------------------------------------------------------------------------------

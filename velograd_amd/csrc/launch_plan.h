@@ -152,6 +152,9 @@ struct BwdPlan {
   int64_t wgs;       // workgroups = dweight partial rows
   size_t lds_bytes;  // dynamic LDS of the group combine
   bool ring = false; // the ring-pipelined kernel (plan_bwd_ring) instead of bwd_vec_kernel
+  // the ring over rows of 8-byte alignment with a half chunk at their end (plan_bwd_ring8): rp
+  // lays out the row's whole chunks (dim - 4 elements)
+  bool x8 = false;
   // with the RoPE gradient: bwd_vec_kernel's plain plan, each pair's rotation evaluated directly
   // where g is decoded (rows too wide for the RoPE walk's bound)
   bool rope_direct = false;
@@ -251,6 +254,30 @@ inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool ali
   if (wgs > wgs_needed) wgs = wgs_needed;
   b.wgs = wgs;
   b.lds_bytes = p.groups > 1 ? (size_t)dim * sizeof(float) : 0;
+  return b;
+}
+
+// The ring over rows of a 2-byte dtype whose streams start on 8-byte boundaries only and hold
+// dim = 8 * n + 4 elements (hidden sizes such as 4100, whose rows alternate between the two
+// halves of a 16-byte line): the ring's plan for the n whole chunks (dim - 4 elements, each
+// moved as two 8-byte halves), the row's last 4 elements an extra half chunk of the row group's
+// lane 0, the group combine over all dim columns.  One chunk per thread: the extra chunk's ring
+// buffers and sums fit beside one chunk's, not beside two (the planner asks plan_bwd_ring for
+// one, so rows of up to kRingBlock whole chunks, dim <= 4100 bf16, take it).
+inline BwdPlan plan_bwd_ring8(int64_t rows, int64_t dim, int elem_bytes, int cus,
+                              int max_block = kRingBlock, int wgs_per_cu = 1) {
+  BwdPlan b;
+  b.rp = RowPlan{false, 0, kGenericBlock, 1, kGenericBlock};
+  b.wgs = 0;
+  b.lds_bytes = 0;
+  if (elem_bytes != 2 || dim < 12 || dim % 8 != 4) return b;
+  b = plan_bwd_ring(rows, dim - 4, elem_bytes, true, cus, 1, max_block, wgs_per_cu);
+  if (!b.ring || b.rp.nv != 1) {
+    b.ring = false;
+    return b;
+  }
+  b.x8 = true;
+  b.lds_bytes = b.rp.groups > 1 ? (size_t)dim * sizeof(float) : 0;
   return b;
 }
 
@@ -399,6 +426,8 @@ inline size_t bwd_workspace_bytes(int64_t rows, int64_t dim, int cus, int prefer
       if (rg.ring && rg.wgs > most) most = rg.wgs;
       const BwdPlan rr = plan_bwd_rope_ring(rows, dim, sizes[si], al != 0, cus);
       if (rr.ring && rr.wgs > most) most = rr.wgs;
+      const BwdPlan r8 = plan_bwd_ring8(rows, dim, sizes[si], cus, ring_block, ring_wgs_per_cu);
+      if (r8.ring && r8.wgs > most) most = r8.wgs;
     }
   }
   return (size_t)most * (size_t)dim * sizeof(float);

@@ -1273,7 +1273,8 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
 // Backward, ring-pipelined (launch_plan.h: plan_bwd_ring).  Each row slot walks rows slot,
 // slot + S, ... as in bwd_vec_kernel, but keeps a ring of PF + 1 = 3 row buffers (2 with
 // grad_h): while a row reduces, the next two rows' loads are in flight.  Rows are of whole
-// 16-byte chunks, dim <= NV * tpr * V (kRingTail where lanes are left idle), and the steady loop
+// 16-byte chunks, dim <= NV * tpr * V (kRingTail where lanes are left idle; kRing8 for rows of
+// 8-byte alignment with a half chunk at their end), and the steady loop
 // covers only iterations in which every slot has a row, loading prefetch rows past the end from
 // the last row instead (never used), so it is free of branches around memory operations: the
 // wait for a row's data then counts exactly the later loads and stores instead of draining them,
@@ -1282,6 +1283,7 @@ __global__ __launch_bounds__((FLAGS & kRopeG) ? vg_plan::max_block_for_nv_rope(N
 // ------------------------------------------------------------------------------------------
 constexpr int kRingDres = 8;
 constexpr int kRingTail = 32;
+constexpr int kRing8 = 64;
 
 template <int DT, int WDT, int NV, int FLAGS>
 __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const BwdArgs a) {
@@ -1294,10 +1296,19 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
   // an idle lane loads the row's last chunk instead (no branch around the load), adds nothing
   // and stores nothing
   constexpr bool TAIL = (FLAGS & kRingTail) != 0;
+  // kRing8: rows of a 2-byte dtype that start on 8-byte boundaries only, dim = n * V + V / 2
+  // (hidden sizes such as 4100): each of the n whole chunks moves as two 8-byte halves, and the
+  // row's last V / 2 elements form an extra half chunk that lane 0 of the row group owns; every
+  // lane of the group loads those same 8 bytes (one request per wave), so no branch guards the
+  // load.  The row group is laid out over the n whole chunks.
+  constexpr bool X8 = (FLAGS & kRing8) != 0;
+  static_assert(!X8 || C::kBytes == 2, "rows of 8-byte alignment are of a 2-byte dtype");
+  constexpr int VH = V / 2;
   constexpr int NH = HAS_GH ? NV : 1;  // grad_h chunks (a dummy slot when absent)
   // With grad_h a third stream fills the ring: one row ahead keeps it within 256 VGPRs.
   constexpr int PF = HAS_GH ? 1 : vg_plan::kRingPrefetch;
   constexpr int R = PF + 1;
+  constexpr int RX = X8 ? R : 1;  // extra half-chunk buffers (a dummy slot without kRing8)
   static_assert((FLAGS & kRopeG) == 0, "the RoPE gradient runs in bwd_vec_kernel");
   __shared__ float red[2][kMaxWavesPerRow];
   extern __shared__ __align__(16) float dyn_lds[];  // dim floats: the row groups' combine
@@ -1310,15 +1321,18 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
   const int64_t nslots = (int64_t)gridDim.x * groups;
   const bool has_w = a.w != nullptr;
   const int64_t last = a.rows - 1;
-  // chunk k of this lane (the row's last one for an idle lane) and whether it is its own
+  // chunk k of this lane (the row's last whole one for an idle lane) and whether it is its own
+  const int nfull = a.dim / V;
   int chunk[NV];
   bool own[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int c = lt + k * tpr;
-    own[k] = !TAIL || c < a.dim / V;
-    chunk[k] = own[k] ? c : a.dim / V - 1;
+    own[k] = !TAIL || c < nfull;
+    chunk[k] = own[k] ? c : nfull - 1;
   }
+  const int64_t xcol = (int64_t)a.dim - VH;  // kRing8: the extra half chunk's first column
+  const bool own_x = X8 && lt == 0;
 
   WeightChunk<DT, WDT> wc[NV];
   float acc[NV][V];
@@ -1328,19 +1342,63 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[k][i] = 0.0f;
   }
+  float wfx[VH], accx[VH];
+  if constexpr (X8) {
+#pragma unroll
+    for (int i = 0; i < VH; ++i) {
+      wfx[i] = 1.0f;
+      accx[i] = 0.0f;
+    }
+    if (has_w) {
+      if constexpr (WDT == VELOGRAD_DTYPE_F32) {
+        Codec<VELOGRAD_DTYPE_F32>::unpack(load16<VELOGRAD_DTYPE_F32>(a.w, xcol), wfx);
+      } else {
+        const u32x2 q = *reinterpret_cast<const u32x2*>(static_cast<const char*>(a.w) +
+                                                        xcol * Codec<WDT>::kBytes);
+        float t[V];
+        Codec<WDT>::unpack(u32x4{q.x, q.y, 0u, 0u}, t);
+#pragma unroll
+        for (int i = 0; i < VH; ++i) wfx[i] = t[i];
+      }
+    }
+  }
 
   u32x4 gr[R][NV], sr[R][NV], hr[R][NH];
+  u32x2 gx[RX][HAS_GH ? 3 : 2];  // kRing8: the extra half chunk's g, saved (and grad_h)
   float rr[R];
+  // One chunk of a stream: 16 bytes, or two 8-byte halves for kRing8 rows.
+  auto load_chunk = [&](const void* base, int64_t e) -> u32x4 {
+    if constexpr (X8) {
+      const u32x2 lo = load8_stream<DT>(base, e);
+      const u32x2 hi = load8_stream<DT>(base, e + VH);
+      return u32x4{lo.x, lo.y, hi.x, hi.y};
+    } else {
+      return load16_stream<DT>(base, e);
+    }
+  };
+  auto store_chunk = [&](void* base, int64_t e, const u32x4 v) {
+    if constexpr (X8) {
+      store8_stream<DT>(base, e, u32x2{v.x, v.y});
+      store8_stream<DT>(base, e + VH, u32x2{v.z, v.w});
+    } else {
+      store16_stream<DT>(base, e, v);
+    }
+  };
   // Row `row`'s g, saved, grad_h chunks and inv_rms; rows past the end read the last row.
-  auto load_row = [&](int64_t row, u32x4* gv, u32x4* sv, u32x4* hv, float& r) {
+  auto load_row = [&](int64_t row, u32x4* gv, u32x4* sv, u32x4* hv, float& r, u32x2* xv) {
     const int64_t rw = row < a.rows ? row : last;
     r = a.inv_rms[rw];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int64_t col = (int64_t)chunk[k] * V;
-      gv[k] = load16_stream<DT>(a.g, rw * a.ld_g + col);
-      sv[k] = load16_stream<DT>(a.saved, rw * a.ld_s + col);
-      if constexpr (HAS_GH) hv[k] = load16_stream<DT>(a.gh, rw * a.ld_gh + col);
+      gv[k] = load_chunk(a.g, rw * a.ld_g + col);
+      sv[k] = load_chunk(a.saved, rw * a.ld_s + col);
+      if constexpr (HAS_GH) hv[k] = load_chunk(a.gh, rw * a.ld_gh + col);
+    }
+    if constexpr (X8) {
+      xv[0] = load8_stream<DT>(a.g, rw * a.ld_g + xcol);
+      xv[1] = load8_stream<DT>(a.saved, rw * a.ld_s + xcol);
+      if constexpr (HAS_GH) xv[2] = load8_stream<DT>(a.gh, rw * a.ld_gh + xcol);
     }
   };
   auto decode = [&](const u32x4* gv, const u32x4* sv, float r, int k, float* gf, float* xh,
@@ -1357,8 +1415,8 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
   // decoded g * w and xhat stay in registers across the reduction (one workgroup per CU leaves
   // 256 VGPRs a lane): decoding them again after it, as bwd_vec_kernel does to save registers,
   // ran 16384 x 4096 bf16 in 69.2 us against 68.5 and 16384 x 5120 in 92.7 against 85.1.
-  auto process = [&](u32x4* gv, u32x4* sv, const u32x4* hv, float r, int64_t row, bool ok,
-                     int it) {
+  auto process = [&](u32x4* gv, u32x4* sv, const u32x4* hv, float r, const u32x2* xv,
+                     int64_t row, bool ok, int it) {
     float s = 0.0f;
     float gfk[NV][V], xhk[NV][V], gwk[NV][V];
 #pragma unroll
@@ -1374,6 +1432,21 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
         } else {
           s += gwk[k][i] * xhk[k][i];
         }
+      }
+    }
+    float gfx[VH], xhx[VH], gwx[VH];
+    if constexpr (X8) {
+      float t[V];
+      C::unpack(u32x4{xv[0].x, xv[0].y, 0u, 0u}, t);
+#pragma unroll
+      for (int i = 0; i < VH; ++i) gfx[i] = t[i];
+      C::unpack(u32x4{xv[1].x, xv[1].y, 0u, 0u}, t);
+#pragma unroll
+      for (int i = 0; i < VH; ++i) {
+        xhx[i] = SAVED_IS_H ? t[i] * r : t[i];
+        gwx[i] = gfx[i] * wfx[i];
+        const float p = gwx[i] * xhx[i];
+        s += own_x ? p : 0.0f;
       }
     }
     s = row_sum(s, tpr, grp, red[it & 1]);
@@ -1395,11 +1468,33 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
       const u32x4 pv = C::pack(d);
       const bool store = TAIL ? ok && own[k] : ok;
       if (store) {
-        store16_stream<DT>(a.dx, row * a.ld_dx + col, pv);
-        if constexpr (HAS_DRES) store16_stream<DT>(a.dres, row * a.ld_dres + col, pv);
+        store_chunk(a.dx, row * a.ld_dx + col, pv);
+        if constexpr (HAS_DRES) store_chunk(a.dres, row * a.ld_dres + col, pv);
       }
 #pragma unroll
       for (int i = 0; i < V; ++i) acc[k][i] += store ? gf[i] * xh[i] : 0.0f;
+    }
+    if constexpr (X8) {
+      float d[V];
+#pragma unroll
+      for (int i = 0; i < VH; ++i) d[i] = r * (gwx[i] - xhx[i] * m);
+#pragma unroll
+      for (int i = VH; i < V; ++i) d[i] = 0.0f;
+      if constexpr (HAS_GH) {
+        float t[V];
+        C::unpack(u32x4{xv[2].x, xv[2].y, 0u, 0u}, t);
+#pragma unroll
+        for (int i = 0; i < VH; ++i) d[i] = d[i] + t[i];
+      }
+      const u32x4 pv = C::pack(d);
+      const bool sx = ok && own_x;
+      if (sx) {
+        store8_stream<DT>(a.dx, row * a.ld_dx + xcol, u32x2{pv.x, pv.y});
+        if constexpr (HAS_DRES)
+          store8_stream<DT>(a.dres, row * a.ld_dres + xcol, u32x2{pv.x, pv.y});
+      }
+#pragma unroll
+      for (int i = 0; i < VH; ++i) accx[i] += sx ? gfx[i] * xhx[i] : 0.0f;
     }
   };
 
@@ -1407,14 +1502,17 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
   // into buffer (j + PF) % R, the one row j - 1 has just released.
   const int full = (int)(a.rows / nslots);  // iterations in which every slot has a row
 #pragma unroll
-  for (int j = 0; j < PF; ++j) load_row(slot + (int64_t)j * nslots, gr[j], sr[j], hr[j], rr[j]);
+  for (int j = 0; j < PF; ++j)
+    load_row(slot + (int64_t)j * nslots, gr[j], sr[j], hr[j], rr[j], gx[X8 ? j : 0]);
   int it = 0;
   for (; it + R <= full; it += R) {
 #pragma unroll
     for (int u = 0; u < R; ++u) {
       const int nb = (u + PF) % R;
-      load_row(slot + (int64_t)(it + u + PF) * nslots, gr[nb], sr[nb], hr[nb], rr[nb]);
-      process(gr[u], sr[u], hr[u], rr[u], slot + (int64_t)(it + u) * nslots, true, it + u);
+      load_row(slot + (int64_t)(it + u + PF) * nslots, gr[nb], sr[nb], hr[nb], rr[nb],
+               gx[X8 ? nb : 0]);
+      process(gr[u], sr[u], hr[u], rr[u], gx[X8 ? u : 0], slot + (int64_t)(it + u) * nslots, true,
+              it + u);
     }
   }
   // The last (up to R) iterations, some of whose slots may have no row.
@@ -1423,9 +1521,10 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
     if (it + u < a.iters) {
       const int nb = (u + PF) % R;
       if (it + u + PF < a.iters)
-        load_row(slot + (int64_t)(it + u + PF) * nslots, gr[nb], sr[nb], hr[nb], rr[nb]);
+        load_row(slot + (int64_t)(it + u + PF) * nslots, gr[nb], sr[nb], hr[nb], rr[nb],
+                 gx[X8 ? nb : 0]);
       const int64_t row = slot + (int64_t)(it + u) * nslots;
-      process(gr[u], sr[u], hr[u], rr[u], row, row < a.rows, it + u);
+      process(gr[u], sr[u], hr[u], rr[u], gx[X8 ? u : 0], row, row < a.rows, it + u);
     }
   }
 
@@ -1442,6 +1541,9 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
         store16<VELOGRAD_DTYPE_F32>(prow, (int64_t)c * V + 4 * q,
                                     Codec<VELOGRAD_DTYPE_F32>::pack(&acc[k][4 * q]));
     }
+    if constexpr (X8) {
+      if (own_x) store16<VELOGRAD_DTYPE_F32>(prow, xcol, Codec<VELOGRAD_DTYPE_F32>::pack(accx));
+    }
     return;
   }
   float* comb = dyn_lds;
@@ -1454,6 +1556,13 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
 #pragma unroll
         for (int i = 0; i < V; ++i)
           comb[c * V + i] = (gi == 0) ? acc[k][i] : comb[c * V + i] + acc[k][i];
+      }
+      if constexpr (X8) {
+        if (own_x) {
+#pragma unroll
+          for (int i = 0; i < VH; ++i)
+            comb[xcol + i] = (gi == 0) ? accx[i] : comb[xcol + i] + accx[i];
+        }
       }
     }
     __syncthreads();
@@ -2044,13 +2153,20 @@ RowPlan plan_fwd(int64_t dim, int elem_bytes, bool aligned, bool one_stream, boo
                                          : vg_plan::kFwdOrder);
 }
 
-BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus, bool rope,
-                 int64_t rope_seq) {
+// `aligned8`: every stream starts on an 8-byte boundary (the weight on a 16-byte one), the
+// condition of the ring's kRing8 rows.
+BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, bool aligned8, int cus,
+                 bool rope, int64_t rope_seq) {
   const Tuning& t = tuning();
   if (!rope && t.bwd_ring) {
     const BwdPlan r = vg_plan::plan_bwd_ring(rows, dim, elem_bytes, aligned, cus, t.bwd_nv,
                                              t.ring_block, t.ring_wgs_per_cu);
     if (r.ring) return r;
+    if (aligned8) {
+      const BwdPlan r8 = vg_plan::plan_bwd_ring8(rows, dim, elem_bytes, cus, t.ring_block,
+                                                 t.ring_wgs_per_cu);
+      if (r8.ring) return r8;
+    }
   }
   if (rope && t.bwd_ring) {
     const BwdPlan r = vg_plan::plan_bwd_rope_ring(rows, dim, elem_bytes, aligned, cus);
@@ -2064,6 +2180,8 @@ BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cu
 }
 
 bool ld_ok(int64_t ld, int elem_bytes) { return ((ld * elem_bytes) & 15) == 0; }
+bool ld_ok8(int64_t ld, int elem_bytes) { return ((ld * elem_bytes) & 7) == 0; }
+bool aligned8p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
 
 // ------------------------------------------------------------------------------------------
 // Typed launchers.
@@ -2150,6 +2268,18 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
 template <int DT, int WDT, int F>
 void launch_bwd_ring(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
   const dim3 grid((uint32_t)b.wgs), block(b.rp.block);
+  if constexpr (Codec<DT>::kBytes == 2) {
+    // rows of 8-byte alignment with a half chunk at their end: one chunk per thread
+    if (b.x8) {
+      if ((int64_t)b.rp.tpr * Codec<DT>::kVec != a.dim - Codec<DT>::kVec / 2)
+        hipLaunchKernelGGL((bwd_ring_kernel<DT, WDT, 1, F | kRing8 | kRingTail>), grid, block,
+                           b.lds_bytes, st, a);
+      else
+        hipLaunchKernelGGL((bwd_ring_kernel<DT, WDT, 1, F | kRing8>), grid, block, b.lds_bytes,
+                           st, a);
+      return;
+    }
+  }
   // rows of fewer chunks than the row group's lanes take the idle-lane variant
   if ((int64_t)b.rp.nv * b.rp.tpr * Codec<DT>::kVec != a.dim) {
     if (b.rp.nv == 1)
@@ -2471,16 +2601,24 @@ int32_t run_bwd(const void* grad_y, const void* saved, int32_t saved_is_h, const
                        (!dres || (aligned16(dres) && ld_ok(ld_dres, eb))) &&
                        (!grad_h || (aligned16(grad_h) && ld_ok(ld_grad_h, eb))) &&
                        (!weight || aligned16(weight));
+  const bool aligned8 = aligned8p(grad_y) && aligned8p(saved) && aligned8p(dx) &&
+                        ld_ok8(ld_g, eb) && ld_ok8(ld_saved, eb) && ld_ok8(ld_dx, eb) &&
+                        (!dres || (aligned8p(dres) && ld_ok8(ld_dres, eb))) &&
+                        (!grad_h || (aligned8p(grad_h) && ld_ok8(ld_grad_h, eb))) &&
+                        (!weight || aligned16(weight));
   const bool rope = rope_seq > 0;
-  BwdPlan plan = plan_bwd(rows, dim, eb, aligned, cus, rope, rope_seq);
+  BwdPlan plan = plan_bwd(rows, dim, eb, aligned, aligned8, cus, rope, rope_seq);
+  const int64_t plan_dim = plan.x8 ? dim - 4 : dim;  // the columns the row plan lays out
   // bwd_vec_kernel's RoPE walk keeps its step rotations (two floats per pair: dim floats) in the
   // same dynamic LDS as the group combine, one after the other.
   if (rope && plan.rp.vec && !plan.ring && !plan.rope_direct)
     plan.lds_bytes = (size_t)dim * sizeof(float);
-  if (!vg_plan::row_plan_valid(plan.rp, dim, eb) || plan.wgs < 1 || plan.wgs > INT32_MAX ||
-      plan.lds_bytes > 64 * 1024 ||
-      (plan.ring && !rope && (!vg_plan::ring_eligible(plan.rp, dim, eb) ||
+  if (!vg_plan::row_plan_valid(plan.rp, plan_dim, eb) || plan.wgs < 1 ||
+      plan.wgs > INT32_MAX || plan.lds_bytes > 64 * 1024 ||
+      (plan.ring && !rope && (!vg_plan::ring_eligible(plan.rp, plan_dim, eb) ||
                               plan.rp.block > vg_plan::kRingBlock)) ||
+      (plan.x8 && (rope || !plan.ring || eb != 2 || dim % 8 != 4 || plan.rp.nv != 1 ||
+                   !aligned8)) ||
       (plan.ring && rope && (!vg_plan::rope_ring_eligible(plan.rp, dim, eb) ||
                              !vg_plan::rope_walk_ok(rows, plan.wgs * plan.rp.groups, rope_seq))) ||
       (rope && plan.rp.vec && !plan.ring && !plan.rope_direct &&
