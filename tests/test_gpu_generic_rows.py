@@ -1,7 +1,9 @@
-"""The generic kernels on rows that are not 16-byte multiples (hidden sizes such as 4100 bf16):
-each row's 16-byte-aligned middle moves in 16-byte accesses and its head and tail element by
-element, and the backward sums its dweight columns in LDS, where a column moves between threads
-from row to row.  Checked against the oracle with tests/_parity.py's tolerances: contiguous
+"""Rows that are not 16-byte multiples (hidden sizes such as 4100 bf16).  Rows of 8n + 4
+two-byte elements whose streams start on 8-byte boundaries take the register-resident kernels
+(whole chunks in 8-byte halves, the last 4 elements a half chunk); the others take the generic
+kernels: each row's 16-byte-aligned middle moves in 16-byte accesses and its head and tail
+element by element, and the backward sums its dweight columns in LDS, where a column moves
+between threads from row to row.  Checked against the oracle with tests/_parity.py's tolerances: contiguous
 tensors (every row through the aligned middle), tensors of different row strides (rows whose
 streams disagree inside a 16-byte line take the element-wise path, so one workgroup mixes both),
 rows at the LDS limit and past it, and bitwise repeatability of dx and dweight."""
@@ -27,6 +29,13 @@ CASES = [
     (777, 16000, BF16, "same", False),   # LDS sums at their limit (kGenericLdsCols)
     (300, 16008, BF16, "same", True),    # past it: element-wise rows, sums in the partial row
     (64, 20002, F32, "same", False),
+    # rows of 8n + 4 two-byte elements on 8-byte boundaries: the register-resident kernels over
+    # the whole chunks in 8-byte halves plus a half chunk (fwd_vec_kernel X8, bwd_ring_kernel
+    # kRing8), down to one whole chunk (dim 12)
+    (999, 2052, F16, "f32", False),
+    (4097, 1028, BF16, None, True),
+    (300, 4092, BF16, "same", False),
+    (64, 12, BF16, "same", True),
 ]
 
 
@@ -106,3 +115,15 @@ def test_streams_of_different_row_strides(widths):
     by element, the others through the aligned middle, in the same workgroups."""
     print(f"generic rows 1500x4100 widths {widths}", flush=True)
     _check(1500, 4100, BF16, "same", True, seed=4100, widths=widths)
+
+
+def test_rows_of_8_byte_alignment_without_residual():
+    """The module form (no residual: y only, h is x) over rows of 8-byte alignment."""
+    print("8-byte rows without a residual, 2000x4100 bf16", flush=True)
+    rng = np.random.default_rng(41)
+    x = P.to_device(P.gaussian(rng, (2000, 4100)), BF16)
+    w = P.to_device(P.weight_vec(rng, 4100), BF16)
+    y, h, inv = vk.fused_rmsnorm_residual_forward(x, None, w, 1e-5)
+    ry, _, rinv = ora.fused_rmsnorm_residual_forward(P.upcast(x), None, P.upcast(w), 1e-5)
+    P.assert_within_ulp(y, ry, 1, "y")
+    assert P.rel_err(P.upcast(inv), rinv) <= P.FP32_REL_TOL

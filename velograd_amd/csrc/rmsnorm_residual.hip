@@ -331,10 +331,17 @@ __device__ inline uint32_t lane_group_max(uint32_t v) {
 // amax / 448, and y * (1 / scale) is stored as e4m3 codes: 8 bytes per bf16/fp16 chunk, 4 per
 // fp32 chunk.  kOutMxE4M3 / kOutMxE2M1: the 32 elements of an MX block are the chunks of 4
 // (bf16/fp16) or 8 (fp32) consecutive lanes, whose amax is reduced with DPP inside the group.
-template <int DT, int WDT, int NV, int OUT>
+// X8: rows of a 2-byte dtype that start on 8-byte boundaries only, dim = n * V + V / 2 (hidden
+// sizes such as 4100; plain outputs only): the row plan covers the n whole chunks, each moved as
+// two 8-byte halves, and the row's last V / 2 elements form an extra half chunk of lane 0 of the
+// row group (every lane of the group loads the same 8 bytes: one request per wave).
+template <int DT, int WDT, int NV, int OUT, bool X8 = false>
 __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const FwdArgs a) {
   using C = Codec<DT>;
   constexpr int V = C::kVec;
+  constexpr int VH = V / 2;
+  static_assert(!X8 || ((OUT == kOutDtype || OUT == kOutDtypeLateH) && C::kBytes == 2),
+                "rows of 8-byte alignment: plain outputs of a 2-byte dtype");
   __shared__ float red[kMaxWavesPerRow];
 
   const int tpr = a.tpr;
@@ -346,6 +353,26 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
   const int nchunk = a.dim / V;
   const bool has_res = a.res != nullptr;
   const bool has_w = a.w != nullptr;
+  const int64_t xcol = (int64_t)a.dim - VH;  // X8: the extra half chunk's first column
+  const bool own_x = X8 && lt == 0;
+  // One chunk of a stream: 16 bytes, or two 8-byte halves for X8 rows.
+  auto load_chunk = [&](const void* base, int64_t e) -> u32x4 {
+    if constexpr (X8) {
+      const u32x2 lo = load8_stream<DT>(base, e);
+      const u32x2 hi = load8_stream<DT>(base, e + VH);
+      return u32x4{lo.x, lo.y, hi.x, hi.y};
+    } else {
+      return load16_stream<DT>(base, e);
+    }
+  };
+  auto store_chunk = [&](void* base, int64_t e, const u32x4 v) {
+    if constexpr (X8) {
+      store8_stream<DT>(base, e, u32x2{v.x, v.y});
+      store8_stream<DT>(base, e + VH, u32x2{v.z, v.w});
+    } else {
+      store16_stream<DT>(base, e, v);
+    }
+  };
 
   // Only the packed 16-byte chunks stay live across the row reduction; fp32 h is formed again
   // after it (the same single fp32 add, so the same bits), which keeps VGPRs low enough for
@@ -358,8 +385,30 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
     xv[k] = u32x4{0u, 0u, 0u, 0u};
     rv[k] = u32x4{0u, 0u, 0u, 0u};
     if (row_ok && c < nchunk) {
-      xv[k] = load16_stream<DT>(a.x, row * a.ld_x + (int64_t)c * V);
-      if (has_res) rv[k] = load16_stream<DT>(a.res, row * a.ld_res + (int64_t)c * V);
+      xv[k] = load_chunk(a.x, row * a.ld_x + (int64_t)c * V);
+      if (has_res) rv[k] = load_chunk(a.res, row * a.ld_res + (int64_t)c * V);
+    }
+  }
+  u32x2 xx = u32x2{0u, 0u}, rx = u32x2{0u, 0u};
+  float wfx[VH];
+  if constexpr (X8) {
+    if (row_ok) {
+      xx = load8_stream<DT>(a.x, row * a.ld_x + xcol);
+      if (has_res) rx = load8_stream<DT>(a.res, row * a.ld_res + xcol);
+    }
+#pragma unroll
+    for (int i = 0; i < VH; ++i) wfx[i] = 1.0f;
+    if (has_w) {
+      if constexpr (WDT == VELOGRAD_DTYPE_F32) {
+        Codec<VELOGRAD_DTYPE_F32>::unpack(load16<VELOGRAD_DTYPE_F32>(a.w, xcol), wfx);
+      } else {
+        const u32x2 q = *reinterpret_cast<const u32x2*>(static_cast<const char*>(a.w) +
+                                                        xcol * Codec<WDT>::kBytes);
+        float t[V];
+        Codec<WDT>::unpack(u32x4{q.x, q.y, 0u, 0u}, t);
+#pragma unroll
+        for (int i = 0; i < VH; ++i) wfx[i] = t[i];
+      }
     }
   }
 #pragma unroll
@@ -368,6 +417,16 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
     wc[k].load((has_w && c < nchunk) ? a.w : nullptr, (int64_t)c * V);
   }
 
+  // the extra half chunk's h (X8), in the first VH of V slots, the rest 0
+  auto make_hx = [&](float* hf) {
+    C::unpack(u32x4{xx.x, xx.y, 0u, 0u}, hf);
+    if (has_res) {
+      float rf[V];
+      C::unpack(u32x4{rx.x, rx.y, 0u, 0u}, rf);
+#pragma unroll
+      for (int i = 0; i < VH; ++i) hf[i] = hf[i] + rf[i];
+    }
+  };
   auto make_h = [&](int k, float* hf) {
     C::unpack(xv[k], hf);
     if (has_res) {
@@ -389,7 +448,19 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
     for (int i = 0; i < V; ++i) ss += hf[i] * hf[i];
     const int c = lt + k * tpr;
     if (!kLateH && write_h && row_ok && c < nchunk)
-      store16_stream<DT>(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf));
+      store_chunk(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf));
+  }
+  if constexpr (X8) {
+    float hf[V];
+    make_hx(hf);
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VH; ++i) p += hf[i] * hf[i];
+    ss += own_x ? p : 0.0f;
+    if (!kLateH && write_h && row_ok && own_x) {
+      const u32x4 pv = C::pack(hf);
+      store8_stream<DT>(a.h, row * a.ld_h + xcol, u32x2{pv.x, pv.y});
+    }
   }
 
   ss = row_sum(ss, tpr, grp, red);
@@ -421,7 +492,7 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
         if (kLateH && write_h) {
           float hf[V];
           make_h(k, hf);
-          store16_stream<DT>(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf));
+          store_chunk(a.h, row * a.ld_h + (int64_t)c * V, C::pack(hf));
         }
         float yf[V];
         make_y(k, yf);
@@ -439,7 +510,24 @@ __global__ __launch_bounds__(max_block_for_nv(NV)) void fwd_vec_kernel(const Fwd
             yf[2 * q + 1] = y0 * sn + y1 * cs;                             // functional.py:314
           }
         }
-        store16_stream<DT>(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
+        store_chunk(a.y, row * a.ld_y + (int64_t)c * V, C::pack(yf));
+      }
+    }
+    if constexpr (X8) {
+      if (row_ok && own_x) {
+        float hf[V];
+        make_hx(hf);
+        if (kLateH && write_h) {
+          const u32x4 pv = C::pack(hf);
+          store8_stream<DT>(a.h, row * a.ld_h + xcol, u32x2{pv.x, pv.y});
+        }
+        float yf[V];
+#pragma unroll
+        for (int i = 0; i < VH; ++i) yf[i] = (hf[i] * r) * wfx[i];
+#pragma unroll
+        for (int i = VH; i < V; ++i) yf[i] = 0.0f;
+        const u32x4 pv = C::pack(yf);
+        store8_stream<DT>(a.y, row * a.ld_y + xcol, u32x2{pv.x, pv.y});
       }
     }
   } else if constexpr (OUT == kOutMxE4M3 || OUT == kOutMxE2M1) {
@@ -2265,6 +2353,32 @@ void launch_fwd(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
   }
 }
 
+// Rows of 8-byte alignment (fwd_vec_kernel's X8): `p` lays out the dim - V / 2 columns of whole
+// chunks.
+template <int DT, int WDT>
+void launch_fwd_x8(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
+  if constexpr (Codec<DT>::kBytes == 2) {
+    const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups)), block(p.block);
+    const bool late = vg_plan::fwd_late_h(p);
+    switch (p.nv * 2 + (late ? 1 : 0)) {
+#define VG_FWD_X8(N)                                                                          \
+  case 2 * (N):                                                                               \
+    hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, N, kOutDtype, true>), grid, block, 0, st, a); \
+    break;                                                                                    \
+  case 2 * (N) + 1:                                                                           \
+    hipLaunchKernelGGL((fwd_vec_kernel<DT, WDT, N, kOutDtypeLateH, true>), grid, block, 0, st, \
+                       a);                                                                    \
+    break;
+      VG_FWD_X8(1)
+      VG_FWD_X8(2)
+      VG_FWD_X8(3)
+      VG_FWD_X8(4)
+#undef VG_FWD_X8
+      default: break;
+    }
+  }
+}
+
 template <int DT, int WDT, int F>
 void launch_bwd_ring(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
   const dim3 grid((uint32_t)b.wgs), block(b.rp.block);
@@ -2499,9 +2613,23 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
                        (!h || (aligned16(h) && ld_ok(ld_h, eb))) && (!weight || aligned16(weight));
   // The fused norm + RoPE kernel holds one chunk per thread, so it keeps the residual order
   // (one chunk first) either way.
-  const RowPlan p = plan_fwd(dim, eb, aligned, residual == nullptr && out != kOutRopeI,
-                            out == kOutFp8Row || mx);
-  if (!vg_plan::row_plan_valid(p, dim, eb))
+  RowPlan p = plan_fwd(dim, eb, aligned, residual == nullptr && out != kOutRopeI,
+                       out == kOutFp8Row || mx);
+  // Rows of 8n + 4 two-byte elements on 8-byte boundaries (fwd_vec_kernel's X8): the plan of
+  // their whole chunks, the last 4 elements an extra half chunk.
+  const bool aligned8 = aligned8p(x) && ld_ok8(ld_x, eb) && aligned8p(y) && ld_ok8(ld_y, eb) &&
+                        (!residual || (aligned8p(residual) && ld_ok8(ld_res, eb))) &&
+                        (!h || (aligned8p(h) && ld_ok8(ld_h, eb))) &&
+                        (!weight || aligned16(weight));
+  bool x8 = false;
+  if (!p.vec && out == kOutDtype && eb == 2 && dim >= 12 && dim % 8 == 4 && aligned8) {
+    const RowPlan px = plan_fwd(dim - 4, eb, true, residual == nullptr, false);
+    if (px.vec) {
+      p = px;
+      x8 = true;
+    }
+  }
+  if (!vg_plan::row_plan_valid(p, x8 ? dim - 4 : dim, eb))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: internal launch plan rejected (dim=%lld)",
                 what, (long long)dim);
 
@@ -2536,7 +2664,12 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
     case kOutMxE4M3: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutMxE4M3>(a, p, st))); break;
     case kOutMxE2M1: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutMxE2M1>(a, p, st))); break;
     case kOutRopeI: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutRopeI>(a, p, st))); break;
-    default: VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutDtype>(a, p, st))); break;
+    default:
+      if (x8)
+        VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd_x8<kD, kW>(a, p, st)));
+      else
+        VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutDtype>(a, p, st)));
+      break;
   }
   return check_launch(what);
 }
