@@ -52,8 +52,11 @@ def _check_oracle(dx, dw, h, g, w, inv, gh, what):
     P.assert_dweight(P.upcast(dw), rdw, what)
 
 
-# 256 CUs x 2 row groups of 256 threads = 512 row slots at dim 4096 bf16
-RING_ROWS = [1, 2, 300, 511, 512, 513, 1024, 1025, 1535, 1536, 1537, 2047, 2560, 16385]
+# 256 CUs x 1 row group of 512 threads = 256 row slots at dim 4096 bf16 (512 slots of two
+# 256-thread row groups when two chunks per thread are asked for); rings of 3 iterations (2 with
+# grad_h): every pattern of the walk around 256, 512 and 768 rows
+RING_ROWS = [1, 2, 255, 256, 257, 300, 511, 512, 513, 767, 768, 769, 1024, 1025, 1535, 1536,
+             1537, 2047, 2304, 2560, 16385]
 
 
 @pytest.mark.parametrize("grad_h", [False, True], ids=["ring3", "ring2-grad_h"])
@@ -66,12 +69,13 @@ def test_ring_row_counts_match_oracle(rows, grad_h):
     _check_oracle(dx, dw, h, g, w, inv, gh, f"rows={rows} grad_h={grad_h}")
 
 
-# (rows, dim, dtype, weight dtype, grad_h): one row group per workgroup (tpr 512), eight groups
-# of one wave (dim 512), fp32 and fp16 with an fp32 weight
-LAYOUTS = [(3000, 8192, torch.bfloat16, torch.bfloat16, False),
-           (2049, 512, torch.bfloat16, torch.float32, True),
-           (1500, 2048, torch.float32, torch.float32, False),
-           (999, 1024, torch.float16, torch.float32, True)]
+# (rows, dim, dtype, weight dtype, grad_h, chunks per thread of the ring's plan): one 512-thread
+# row group of two chunks (dim 8192), eight row groups of one wave (dim 512), two 256-thread row
+# groups of two chunks in fp32, four 128-thread row groups in fp16 with an fp32 weight
+LAYOUTS = [(3000, 8192, torch.bfloat16, torch.bfloat16, False, 2),
+           (2049, 512, torch.bfloat16, torch.float32, True, 1),
+           (1500, 2048, torch.float32, torch.float32, False, 2),
+           (999, 1024, torch.float16, torch.float32, True, 1)]
 
 _CHILD = r"""
 import json, sys
@@ -97,17 +101,26 @@ np.savez(sys.argv[3], **out)
 
 
 def _bitwise_against_previous_kernel(layouts, tmp_path):
-    cases = [(r, d, str(dt).split(".")[-1], str(wdt).split(".")[-1], gh)
-             for r, d, dt, wdt, gh in layouts]
-    path = str(tmp_path / "legacy.npz")
-    env = dict(os.environ, VELOGRAD_BWD_RING="0")
-    print("child process: the same backwards with VELOGRAD_BWD_RING=0", flush=True)
-    r = subprocess.run([sys.executable, "-c", _CHILD, REPO, json.dumps(cases), path], env=env,
-                       capture_output=True, text=True, timeout=110)
-    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
-    legacy = np.load(path)
-    for i, (rows, d, dt, wdt, gh) in enumerate(layouts):
-        print(f"ring vs previous kernel: {rows}x{d} {dt} w={wdt} grad_h={gh}", flush=True)
+    """dx of the ring bit for bit against bwd_vec_kernel's in a child process
+    (VELOGRAD_BWD_RING=0) over the same row layout (VELOGRAD_BWD_NV = the ring's chunks per
+    thread), so both sum each row in the same order."""
+    legacy = {}
+    for nv in sorted({case[5] for case in layouts}):
+        idx = [i for i, case in enumerate(layouts) if case[5] == nv]
+        cases = [(r, d, str(dt).split(".")[-1], str(wdt).split(".")[-1], gh)
+                 for r, d, dt, wdt, gh, _ in (layouts[i] for i in idx)]
+        path = str(tmp_path / f"legacy{nv}.npz")
+        env = dict(os.environ, VELOGRAD_BWD_RING="0", VELOGRAD_BWD_NV=str(nv))
+        print(f"child process: the same backwards with VELOGRAD_BWD_RING=0 VELOGRAD_BWD_NV={nv}",
+              flush=True)
+        r = subprocess.run([sys.executable, "-c", _CHILD, REPO, json.dumps(cases), path],
+                           env=env, capture_output=True, text=True, timeout=110)
+        assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+        got = np.load(path)
+        for k, i in enumerate(idx):
+            legacy[i] = got[f"dx{k}"]
+    for i, (rows, d, dt, wdt, gh, nv) in enumerate(layouts):
+        print(f"ring vs previous kernel: {rows}x{d} {dt} w={wdt} grad_h={gh} nv={nv}", flush=True)
         rng = np.random.default_rng(rows * 7 + d)
         h = P.to_device(P.gaussian(rng, (rows, d)), dt)
         g = P.to_device(P.gaussian(rng, (rows, d)), dt)
@@ -116,7 +129,7 @@ def _bitwise_against_previous_kernel(layouts, tmp_path):
         _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
         dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=ghv)
         bits = dx.view(torch.int16 if dx.element_size() == 2 else torch.int32).cpu().numpy()
-        assert np.array_equal(bits, legacy[f"dx{i}"]), f"dx differs at {rows}x{d} {dt}"
+        assert np.array_equal(bits, legacy[i]), f"dx differs at {rows}x{d} {dt}"
         _check_oracle(dx, dw, h, g, w, inv, ghv, f"{rows}x{d} {dt}")
 
 
@@ -124,23 +137,80 @@ def test_ring_dx_equals_the_previous_kernel_bitwise(tmp_path):
     _bitwise_against_previous_kernel(LAYOUTS, tmp_path)
 
 
+_CHILD_NV2 = r"""
+import json, sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+from tests import _parity as P
+from velograd_amd import kernels as vk
+cases = json.loads(sys.argv[2])
+out = {}
+for i, (rows, d, dt, wdt, gh) in enumerate(cases):
+    dt, wdt = getattr(torch, dt), getattr(torch, wdt)
+    rng = np.random.default_rng(rows * 5 + d)
+    h = P.to_device(P.gaussian(rng, (rows, d)), dt)
+    g = P.to_device(P.gaussian(rng, (rows, d)), dt)
+    w = P.to_device(P.weight_vec(rng, d), wdt)
+    ghv = P.to_device(P.gaussian(rng, (rows, d)), dt) if gh else None
+    _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
+    dx, dw = vk.fused_rmsnorm_residual_backward(g, h, w, inv, saved_is_h=True, grad_h=ghv)
+    out[f"dx{i}"] = dx.float().cpu().numpy()
+    out[f"dw{i}"] = dw.cpu().numpy()
+np.savez(sys.argv[3], **out)
+"""
+
+# Two chunks per thread in row groups of 256, 128 and 64 threads (two, four and eight row groups
+# a workgroup, combined in LDS), whole and with idle lanes: the layouts the planner takes when
+# VELOGRAD_BWD_NV=2 asks for them (by default one chunk per thread comes first).
+NV2 = [(2500, 4096, torch.bfloat16, torch.bfloat16, False),
+       (1537, 4000, torch.bfloat16, torch.bfloat16, True),
+       (999, 2048, torch.float16, torch.float32, False),
+       (1200, 1000, torch.bfloat16, torch.bfloat16, True),
+       (700, 2000, torch.float32, torch.float32, False)]
+
+
+def test_ring_two_chunks_per_thread_match_oracle(tmp_path):
+    cases = [(r, d, str(dt).split(".")[-1], str(wdt).split(".")[-1], gh)
+             for r, d, dt, wdt, gh in NV2]
+    path = str(tmp_path / "nv2.npz")
+    env = dict(os.environ, VELOGRAD_BWD_NV="2")
+    print("child process: ring backwards with VELOGRAD_BWD_NV=2", flush=True)
+    r = subprocess.run([sys.executable, "-c", _CHILD_NV2, REPO, json.dumps(cases), path], env=env,
+                       capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    got = np.load(path)
+    for i, (rows, d, dt, wdt, gh) in enumerate(NV2):
+        print(f"two chunks per thread: {rows}x{d} {dt} w={wdt} grad_h={gh}", flush=True)
+        rng = np.random.default_rng(rows * 5 + d)
+        h = P.to_device(P.gaussian(rng, (rows, d)), dt)
+        g = P.to_device(P.gaussian(rng, (rows, d)), dt)
+        w = P.to_device(P.weight_vec(rng, d), wdt)
+        ghv = P.to_device(P.gaussian(rng, (rows, d)), dt) if gh else None
+        _, _, inv = vk.fused_rmsnorm_residual_forward(h, None, w, 1e-5)
+        dx = torch.from_numpy(got[f"dx{i}"]).to(dt)
+        dw = torch.from_numpy(got[f"dw{i}"])
+        _check_oracle(dx, dw, h, g, w, inv, ghv, f"nv2 {rows}x{d} {dt}")
+
+
 # Rows of fewer 16-byte chunks than their row group's lanes hold (at most 1/8 of the slots idle):
 # the idle lanes reload the row's last chunk, add nothing to the row's sum and dweight and store
 # nothing.  (rows, dim, dtype, weight dtype, grad_h); the comments give idle / all chunk slots.
-IDLE = [(1537, 4000, torch.bfloat16, torch.bfloat16, False),  # 12/512, two row groups a workgroup
-        (2049, 5000, torch.bfloat16, torch.bfloat16, True),   # 15/640, one 320-thread row group
-        (1000, 3000, torch.float16, torch.float32, False),    # 9/384, two 192-thread row groups
-        (4097, 1000, torch.bfloat16, torch.bfloat16, True),   # 3/128, eight 64-thread row groups
-        (3001, 2000, torch.float32, torch.float32, False),    # 12/512
-        (777, 1000, torch.float32, torch.float32, True),      # 6/256, fewer rows than row slots
-        (999, 456, torch.bfloat16, torch.float32, True),      # 7/64, one chunk per thread
-        (2500, 3200, torch.float16, torch.float16, False),    # 48/448, one chunk per thread
-        (700, 6272, torch.bfloat16, torch.bfloat16, True)]    # 112/896, 448-thread row groups
+IDLE = [(1537, 4000, torch.bfloat16, torch.bfloat16, False, 1),  # 12/512, one row group
+        (2049, 5000, torch.bfloat16, torch.bfloat16, True, 2),   # 15/640, 320 threads, 2 chunks
+        (1000, 3000, torch.float16, torch.float32, False, 1),    # 9/384, one 384-thread group
+        (4097, 1000, torch.bfloat16, torch.bfloat16, True, 1),   # 3/128, four row groups
+        (3001, 2000, torch.float32, torch.float32, False, 2),    # 12/512, two row groups
+        (401, 1000, torch.float32, torch.float32, True, 2),      # 6/256, four row groups, more
+                                                                  # row slots than rows
+        (999, 456, torch.bfloat16, torch.float32, True, 1),      # 7/64, eight row groups
+        (2500, 3200, torch.float16, torch.float16, False, 1),    # 48/448
+        (700, 6272, torch.bfloat16, torch.bfloat16, True, 2)]    # 112/896, 448 threads, 2 chunks
 
 
-@pytest.mark.parametrize("rows,d,dt,wdt,gh", IDLE,
-                         ids=[f"{r}x{d}-{str(t).split('.')[-1]}" for r, d, t, _, _ in IDLE])
-def test_ring_idle_lanes_match_oracle(rows, d, dt, wdt, gh):
+@pytest.mark.parametrize("rows,d,dt,wdt,gh,nv", IDLE,
+                         ids=[f"{r}x{d}-{str(t).split('.')[-1]}" for r, d, t, _, _, _ in IDLE])
+def test_ring_idle_lanes_match_oracle(rows, d, dt, wdt, gh, nv):
     print(f"ring backward with idle lanes {rows}x{d} {dt} w={wdt} grad_h={gh}", flush=True)
     h, g, w, inv, ghv = _inputs(rows, d, dt, wdt, rows + d, gh)
     dres = torch.empty_like(g)

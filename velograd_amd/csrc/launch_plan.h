@@ -232,17 +232,34 @@ inline bool ring_tail_pays(const RowPlan& p, int64_t dim, int elem_bytes) {
 // `max_block` (at most kRingBlock) bounds the workgroup and `wgs_per_cu` (1 or 2) sets the
 // resident workgroups per CU: two 256-thread workgroups per CU hold the same waves as one of 512
 // (the ring's registers allow eight waves per CU) without sharing a barrier.
+// Without a preference (`prefer_nv` 0), for 2-byte dtypes a ring row group of one chunk per
+// thread comes first where it is planned (rows of up to kRingBlock chunks), else the backward's
+// order: one chunk per thread in row groups of up to 512 threads beat two in half as many (no
+// LDS combine of the row groups' dweight columns when one row group fills the workgroup).
+// Measured on MI355X (16384 rows, alternating processes): the bench's config C backward
+// 67.3-67.5 us against 68.6-68.7 in three runs each (the step 6094-6098 GB/s against
+// 6062-6070), and with batched launches (best of 3 rounds, two runs each) bf16 1024 22.0 against
+// 23.5, 1536 30.2 against 36.7, 2048 37.5 against 38.6, 3584 60.1 against 62.7, 4000 68.0
+// against 71.5, 4096 68.2 against 69.4, 512, 768, 2560 and 3072 equal.  fp32 rows keep two
+// chunks per thread first: one ran 1024 in 39.7 against 37.5 us, 1536 62.2 against 53.4, 2048
+// 74.1 against 68.2.
 inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
                              int prefer_nv, int max_block = kRingBlock, int wgs_per_cu = 1) {
   BwdPlan b;
-  b.rp = plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrder);
   b.wgs = 0;
   b.lds_bytes = 0;
   if (max_block > kRingBlock) max_block = kRingBlock;
   if (wgs_per_cu < 1) wgs_per_cu = 1;
   if (wgs_per_cu > 2) wgs_per_cu = 2;
-  b.ring = ring_eligible(b.rp, dim, elem_bytes) && b.rp.tpr <= max_block &&
-           ring_tail_pays(b.rp, dim, elem_bytes);
+  auto suits = [&](const RowPlan& p) {
+    return ring_eligible(p, dim, elem_bytes) && p.tpr <= max_block &&
+           ring_tail_pays(p, dim, elem_bytes);
+  };
+  const bool one_first = prefer_nv == 0 && elem_bytes == 2;
+  b.rp = plan_rows(dim, elem_bytes, aligned, one_first ? 1 : prefer_nv, kBwdOrder);
+  if (one_first && !(b.rp.vec && b.rp.nv == 1 && suits(b.rp)))
+    b.rp = plan_rows(dim, elem_bytes, aligned, 0, kBwdOrder);
+  b.ring = suits(b.rp);
   if (!b.ring) return b;
   if (b.rp.tpr * wgs_per_cu > kRingBlock) wgs_per_cu = 1;  // a row group fills the CU's waves
   RowPlan& p = b.rp;
