@@ -36,6 +36,8 @@ CASES = [
     (4097, 1028, BF16, None, True),
     (300, 4092, BF16, "same", False),
     (64, 12, BF16, "same", True),
+    (1, 4100, BF16, "same", True),
+    (3, 508, F16, None, False),
 ]
 
 

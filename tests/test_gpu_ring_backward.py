@@ -239,7 +239,10 @@ RING8 = [(2049, 4100, torch.bfloat16, torch.bfloat16, False),
          (999, 2052, torch.bfloat16, torch.float32, False),   # two row groups a workgroup
          (4097, 1028, torch.bfloat16, torch.bfloat16, True),  # four row groups a workgroup
          (300, 4092, torch.float16, torch.float16, False),    # 511 whole chunks over 512 lanes
-         (5000, 4100, torch.bfloat16, None, False)]
+         (5000, 4100, torch.bfloat16, None, False),
+         (1, 4100, torch.bfloat16, torch.bfloat16, True),     # one row, one workgroup
+         (2, 508, torch.bfloat16, torch.bfloat16, False),     # 63 whole chunks, 64-thread rows
+         (513, 508, torch.float16, torch.float32, True)]      # eight row groups a workgroup
 
 
 @pytest.mark.parametrize("rows,d,dt,wdt,gh", RING8,
