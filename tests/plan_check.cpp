@@ -304,6 +304,22 @@ int main() {
             !plan_bwd_ring8(16384, 4100, 4, 256).ring && !plan_bwd_ring8(16384, 4104, 2, 256).ring,
         "ring8 refusals");
   printf("ring8 plans checked: %ld\n", ring8);
+  // One chunk per thread first in the ring for 2-byte rows, for walks of up to
+  // kRingOneChunkMaxIters rows per slot; longer walks, fp32 rows and an explicit preference
+  // keep the backward's order (two chunks per thread first).
+  {
+    const BwdPlan c = plan_bwd_ring(16384, 4096, 2, true, 256, 0);
+    const BwdPlan edge = plan_bwd_ring(49152, 4096, 2, true, 256, 0);
+    const BwdPlan longer = plan_bwd_ring(49153, 4096, 2, true, 256, 0);
+    const BwdPlan f32 = plan_bwd_ring(16384, 2048, 4, true, 256, 0);
+    const BwdPlan asked = plan_bwd_ring(16384, 4096, 2, true, 256, 2);
+    CHECK(c.ring && c.rp.nv == 1 && c.rp.tpr == 512 && c.wgs == 256, "config C ring plan");
+    CHECK(edge.ring && edge.rp.nv == 1, "one chunk per thread at 192 rows per slot");
+    CHECK(longer.ring && longer.rp.nv == 2 && longer.rp.tpr == 256,
+          "two chunks per thread past 192 rows per slot");
+    CHECK(f32.ring && f32.rp.nv == 2 && asked.ring && asked.rp.nv == 2,
+          "fp32 rows and an explicit preference keep two chunks per thread");
+  }
   // The ring backward over rows with idle lanes: bf16 rows of 1000, 3000, 4000 and 5000 leave
   // 3, 9, 12 and 15 of their chunk slots idle and take it; 768, 2056 and 4104 would leave more
   // than 1/8 idle, 2240 has one chunk per thread in 320-thread rows and 7160 and 8184 two in

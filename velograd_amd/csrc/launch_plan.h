@@ -243,35 +243,49 @@ inline bool ring_tail_pays(const RowPlan& p, int64_t dim, int elem_bytes) {
 // against 71.5, 4096 68.2 against 69.4, 512, 768, 2560 and 3072 equal.  fp32 rows keep two
 // chunks per thread first: one ran 1024 in 39.7 against 37.5 us, 1536 62.2 against 53.4, 2048
 // 74.1 against 68.2.
+// Walks of more than kRingOneChunkMaxIters rows per slot keep the backward's order: one chunk per
+// thread halves the row slots, and its walks of 256 rows ran slower than two chunks' walks of 128
+// (bf16 65536 x 4096: 265.9-268.3 us against 259.7-260.0; 131072 x 2048: 267.2-269.0 against
+// 260.9), while walks of up to 192 rows kept its lead (49152 x 4096: 193.4 against 194.3; 32768
+// x 4096: 128.5-128.7 against 130.7-131.2).
+constexpr int64_t kRingOneChunkMaxIters = 192;
+
 inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool aligned, int cus,
                              int prefer_nv, int max_block = kRingBlock, int wgs_per_cu = 1) {
-  BwdPlan b;
-  b.wgs = 0;
-  b.lds_bytes = 0;
   if (max_block > kRingBlock) max_block = kRingBlock;
   if (wgs_per_cu < 1) wgs_per_cu = 1;
   if (wgs_per_cu > 2) wgs_per_cu = 2;
-  auto suits = [&](const RowPlan& p) {
-    return ring_eligible(p, dim, elem_bytes) && p.tpr <= max_block &&
-           ring_tail_pays(p, dim, elem_bytes);
+  // The ring's launch over row layout `rp`: `ring` false when the layout does not suit it.
+  auto complete = [&](const RowPlan& rp) {
+    BwdPlan b;
+    b.rp = rp;
+    b.wgs = 0;
+    b.lds_bytes = 0;
+    b.ring = ring_eligible(rp, dim, elem_bytes) && rp.tpr <= max_block &&
+             ring_tail_pays(rp, dim, elem_bytes);
+    if (!b.ring) return b;
+    int wpc = wgs_per_cu;
+    if (rp.tpr * wpc > kRingBlock) wpc = 1;  // a row group fills the CU's waves
+    RowPlan& p = b.rp;
+    p.groups = max_block / p.tpr;
+    if (p.groups * wpc * p.tpr > kRingBlock) p.groups = kRingBlock / (wpc * p.tpr);
+    p.block = p.tpr * p.groups;
+    const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
+    int64_t wgs = cus > 0 ? (int64_t)cus * wpc : 1;
+    if (wgs > wgs_needed) wgs = wgs_needed;
+    b.wgs = wgs;
+    b.lds_bytes = p.groups > 1 ? (size_t)dim * sizeof(float) : 0;
+    return b;
   };
-  const bool one_first = prefer_nv == 0 && elem_bytes == 2;
-  b.rp = plan_rows(dim, elem_bytes, aligned, one_first ? 1 : prefer_nv, kBwdOrder);
-  if (one_first && !(b.rp.vec && b.rp.nv == 1 && suits(b.rp)))
-    b.rp = plan_rows(dim, elem_bytes, aligned, 0, kBwdOrder);
-  b.ring = suits(b.rp);
-  if (!b.ring) return b;
-  if (b.rp.tpr * wgs_per_cu > kRingBlock) wgs_per_cu = 1;  // a row group fills the CU's waves
-  RowPlan& p = b.rp;
-  p.groups = max_block / p.tpr;
-  if (p.groups * wgs_per_cu * p.tpr > kRingBlock) p.groups = kRingBlock / (wgs_per_cu * p.tpr);
-  p.block = p.tpr * p.groups;
-  const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
-  int64_t wgs = cus > 0 ? (int64_t)cus * wgs_per_cu : 1;
-  if (wgs > wgs_needed) wgs = wgs_needed;
-  b.wgs = wgs;
-  b.lds_bytes = p.groups > 1 ? (size_t)dim * sizeof(float) : 0;
-  return b;
+  if (prefer_nv == 0 && elem_bytes == 2) {
+    const RowPlan one = plan_rows(dim, elem_bytes, aligned, 1, kBwdOrder);
+    if (one.vec && one.nv == 1) {
+      const BwdPlan b = complete(one);
+      const int64_t slots = b.wgs * b.rp.groups;
+      if (b.ring && (rows + slots - 1) / slots <= kRingOneChunkMaxIters) return b;
+    }
+  }
+  return complete(plan_rows(dim, elem_bytes, aligned, prefer_nv, kBwdOrder));
 }
 
 // The ring over rows of a 2-byte dtype whose streams start on 8-byte boundaries only and hold
