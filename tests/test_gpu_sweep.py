@@ -2,7 +2,8 @@
 oracle, with the tolerances of tests/_parity.py: dtype and weight dtype (or no weight), residual
 or none, leading dimensions, row strides from slicing wider tensors, the saved tensor (h or
 xhat), a residual-stream gradient, and a second dresidual buffer; row lengths from 1 to 9000
-(register path and generic path)."""
+(the register paths, whole rows and rows that leave lanes idle, rows of 8-byte alignment, and the
+generic path)."""
 
 import numpy as np
 import pytest
@@ -15,7 +16,8 @@ from velograd_amd import kernels as vk
 pytestmark = pytest.mark.gpu
 
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
-DIMS = [1, 2, 7, 8, 16, 31, 64, 96, 200, 512, 640, 1000, 1024, 2048, 2056, 4096, 5120, 9000]
+DIMS = [1, 2, 7, 8, 16, 31, 64, 96, 200, 508, 512, 640, 1000, 1024, 1028, 2048, 2052, 2056, 3000,
+        3576, 4000, 4096, 4100, 5120, 9000]
 
 
 def _case(i):
@@ -30,7 +32,7 @@ def _case(i):
                 gh=bool(rng.integers(2)), dres=bool(rng.integers(4) == 0), seed=1000 + i)
 
 
-CASES = [_case(i) for i in range(48)]
+CASES = [_case(i) for i in range(64)]
 
 
 def _tensor(rng, shape, dtype, strided):
