@@ -198,7 +198,7 @@ def test_ring_two_chunks_per_thread_match_oracle(tmp_path):
 # nothing.  (rows, dim, dtype, weight dtype, grad_h); the comments give idle / all chunk slots.
 IDLE = [(1537, 4000, torch.bfloat16, torch.bfloat16, False, 1),  # 12/512, one row group
         (2049, 5000, torch.bfloat16, torch.bfloat16, True, 2),   # 15/640, 320 threads, 2 chunks
-        (1000, 3000, torch.float16, torch.float32, False, 1),    # 9/384, one 384-thread group
+        (1000, 3000, torch.float16, torch.float32, False, 2),    # 9/384, two 192-thread groups
         (4097, 1000, torch.bfloat16, torch.bfloat16, True, 1),   # 3/128, four row groups
         (3001, 2000, torch.float32, torch.float32, False, 2),    # 12/512, two row groups
         (401, 1000, torch.float32, torch.float32, True, 2),      # 6/256, four row groups, more

@@ -242,7 +242,11 @@ inline bool ring_tail_pays(const RowPlan& p, int64_t dim, int elem_bytes) {
 // 23.5, 1536 30.2 against 36.7, 2048 37.5 against 38.6, 3584 60.1 against 62.7, 4000 68.0
 // against 71.5, 4096 68.2 against 69.4, 512, 768, 2560 and 3072 equal.  fp32 rows keep two
 // chunks per thread first: one ran 1024 in 39.7 against 37.5 us, 1536 62.2 against 53.4, 2048
-// 74.1 against 68.2.
+// 74.1 against 68.2.  Nor do one-chunk row groups of 320 or 384 threads come first (one
+// workgroup of five or six waves a CU): bf16 3000 ran 59.4-59.6 us against 55.8-56.0 with two
+// chunks per thread in two 192-thread row groups, 3072 55.6-56.0 against 54.7, and 2560
+// 52.6-53.0 against 52.0-52.3 in bwd_vec_kernel; 448-thread ones stay first (3500 70.9-71.6
+// against 72.2-72.6, 3584 60.9-62.1 against 62.5-62.7; 3200 within 1%).
 // Walks of more than kRingOneChunkMaxIters rows per slot keep the backward's order: one chunk per
 // thread halves the row slots, and its walks of 256 rows ran slower than two chunks' walks of 128
 // (bf16 65536 x 4096: 265.9-268.3 us against 259.7-260.0; 131072 x 2048: 267.2-269.0 against
@@ -279,7 +283,7 @@ inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool ali
   };
   if (prefer_nv == 0 && elem_bytes == 2) {
     const RowPlan one = plan_rows(dim, elem_bytes, aligned, 1, kBwdOrder);
-    if (one.vec && one.nv == 1) {
+    if (one.vec && one.nv == 1 && one.tpr != 320 && one.tpr != 384) {
       const BwdPlan b = complete(one);
       const int64_t slots = b.wgs * b.rp.groups;
       if (b.ring && (rows + slots - 1) / slots <= kRingOneChunkMaxIters) return b;
