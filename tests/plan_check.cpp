@@ -134,12 +134,15 @@ int main() {
                     CHECK(ring_eligible(rg.rp, dim, eb), "ring plan not eligible dim=%lld",
                           (long long)dim);
                     {
-                      // whole waves over the row's chunks, at most 1/8 of the slots idle, and
-                      // fewer idle slots than one chunk per lane
+                      // whole waves over the row's chunks, at most 1/8 of the slots idle (for
+                      // 2-byte rows of one chunk per thread, less than the last wave), and fewer
+                      // idle slots than one chunk per lane
                       const int64_t slots = (int64_t)rg.rp.nv * rg.rp.tpr;
                       const int64_t chunks = dim / (16 / eb);
+                      const bool part_wave = rg.rp.nv == 1 && eb == 2 && slots - chunks < kWave;
                       CHECK(dim % (16 / eb) == 0 && slots >= chunks &&
-                                (slots - chunks) * 8 <= slots && slots - chunks < rg.rp.tpr,
+                                ((slots - chunks) * 8 <= slots || part_wave) &&
+                                slots - chunks < rg.rp.tpr,
                             "ring plan idle lanes dim=%lld slots=%lld", (long long)dim,
                             (long long)slots);
                     }
@@ -270,8 +273,9 @@ int main() {
   printf("rope walks checked: %ld\n", walks);
   // The ring over rows of 8-byte alignment (kRing8): 2-byte dims of 8n + 4 only, one chunk per
   // thread over the n whole chunks (a ring plan of dim - 4 columns), LDS for all dim columns when
-  // row groups combine, partial rows within the workspace query; 4100 and 2052 take it with
-  // 512- and 256-thread row groups, 4108 (513 whole chunks) and 100 (12 of 64 lanes) do not.
+  // row groups combine, partial rows within the workspace query; 4100, 2052 and 100 take it with
+  // 512-, 256- and 64-thread row groups (at 100, 12 of 64 lanes busy), 4108 (513 whole chunks)
+  // does not.
   long ring8 = 0;
   for (int64_t dim = 4; dim <= 8200; dim += 4) {
     for (int64_t rows : {1, 300, 16384}) {
@@ -300,9 +304,11 @@ int main() {
         "ring8 at 4100");
   CHECK(plan_bwd_ring8(16384, 2052, 2, 256).ring && plan_bwd_ring8(16384, 2052, 2, 256).rp.tpr == 256,
         "ring8 at 2052");
-  CHECK(!plan_bwd_ring8(16384, 4108, 2, 256).ring && !plan_bwd_ring8(16384, 100, 2, 256).ring &&
-            !plan_bwd_ring8(16384, 4100, 4, 256).ring && !plan_bwd_ring8(16384, 4104, 2, 256).ring,
+  CHECK(!plan_bwd_ring8(16384, 4108, 2, 256).ring && !plan_bwd_ring8(16384, 4100, 4, 256).ring &&
+            !plan_bwd_ring8(16384, 4104, 2, 256).ring,
         "ring8 refusals");
+  CHECK(plan_bwd_ring8(16384, 100, 2, 256).ring && plan_bwd_ring8(16384, 100, 2, 256).rp.tpr == 64,
+        "ring8 at 100 (12 whole chunks in one partly idle wave)");
   printf("ring8 plans checked: %ld\n", ring8);
   // One chunk per thread first in the ring for 2-byte rows, for walks of up to
   // kRingOneChunkMaxIters rows per slot; longer walks, fp32 rows and an explicit preference
@@ -321,19 +327,21 @@ int main() {
           "fp32 rows and an explicit preference keep two chunks per thread");
   }
   // The ring backward over rows with idle lanes: bf16 rows of 1000, 3000, 4000 and 5000 leave
-  // 3, 9, 12 and 15 of their chunk slots idle and take it; 768, 2056 and 4104 would leave more
-  // than 1/8 idle, 2240 has one chunk per thread in 320-thread rows and 7160 and 8184 two in
-  // 448- and 512-thread rows that are not whole 128-byte lines: those stay on bwd_vec_kernel,
-  // as do none of the whole rows (2560 in 320-thread rows, 8192).
-  for (int64_t dim : {1000, 3000, 4000, 5000, 768, 2056, 4104, 2240, 7160, 8184, 2560, 8192,
-                      6272, 3576}) {
+  // 3, 9, 12 and 15 of their chunk slots idle and take it, and 768 and 1280 32 of one chunk per
+  // thread's 128 and 192 (a partly idle last wave); 2056 and 4104 would leave more than 1/8
+  // idle, 2240 has one chunk per thread in 320-thread rows and 7160 and 8184 two in 448- and
+  // 512-thread rows that are not whole 128-byte lines: those stay on bwd_vec_kernel, as do none
+  // of the whole rows (2560 in 320-thread rows, 8192).
+  for (int64_t dim : {1000, 3000, 4000, 5000, 768, 1280, 2056, 4104, 2240, 7160, 8184, 2560,
+                      8192, 6272, 3576}) {
     const BwdPlan rg = plan_bwd_ring(16384, dim, 2, true, 256, 0);
     const int64_t idle = (int64_t)rg.rp.nv * rg.rp.tpr - dim / 8;
     const bool want = dim == 1000 || dim == 3000 || dim == 4000 || dim == 5000 || dim == 2560 ||
-                      dim == 8192 || dim == 6272 || dim == 3576;
+                      dim == 8192 || dim == 6272 || dim == 3576 || dim == 768 || dim == 1280;
     CHECK(rg.ring == want, "ring plan over %lld bf16 columns: %d", (long long)dim, (int)rg.ring);
     CHECK(!want || idle == (dim == 1000 ? 3 : dim == 3000 ? 9 : dim == 4000 ? 12 :
-                            dim == 5000 ? 15 : dim == 6272 ? 112 : dim == 3576 ? 1 : 0),
+                            dim == 5000 ? 15 : dim == 6272 ? 112 : dim == 3576 ? 1 :
+                            dim == 768 || dim == 1280 ? 32 : 0),
           "idle chunk slots at %lld: %lld", (long long)dim, (long long)idle);
   }
   // Where the forward stores h: after the reduction for the measured bf16 rows of 2048, 3072

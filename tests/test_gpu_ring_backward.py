@@ -205,7 +205,9 @@ IDLE = [(1537, 4000, torch.bfloat16, torch.bfloat16, False, 1),  # 12/512, one r
                                                                   # row slots than rows
         (999, 456, torch.bfloat16, torch.float32, True, 1),      # 7/64, eight row groups
         (2500, 3200, torch.float16, torch.float16, False, 1),    # 48/448
-        (700, 6272, torch.bfloat16, torch.bfloat16, True, 2)]    # 112/896, 448 threads, 2 chunks
+        (700, 6272, torch.bfloat16, torch.bfloat16, True, 2),    # 112/896, 448 threads, 2 chunks
+        (3000, 768, torch.bfloat16, torch.bfloat16, True, 1),    # 32/128: a partly idle last wave
+        (1700, 1280, torch.float16, torch.float32, False, 1)]    # 32/192, two row groups
 
 
 @pytest.mark.parametrize("rows,d,dt,wdt,gh,nv", IDLE,
@@ -242,7 +244,8 @@ RING8 = [(2049, 4100, torch.bfloat16, torch.bfloat16, False),
          (5000, 4100, torch.bfloat16, None, False),
          (1, 4100, torch.bfloat16, torch.bfloat16, True),     # one row, one workgroup
          (2, 508, torch.bfloat16, torch.bfloat16, False),     # 63 whole chunks, 64-thread rows
-         (513, 508, torch.float16, torch.float32, True)]      # eight row groups a workgroup
+         (513, 508, torch.float16, torch.float32, True),      # eight row groups a workgroup
+         (2000, 100, torch.bfloat16, torch.bfloat16, True)]   # 12 whole chunks, 64-thread rows
 
 
 @pytest.mark.parametrize("rows,d,dt,wdt,gh", RING8,

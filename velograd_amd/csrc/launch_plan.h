@@ -163,7 +163,8 @@ struct BwdPlan {
 // The ring-pipelined backward (bwd_ring_kernel): a ring of kRingPrefetch + 1 row buffers per
 // thread, so two rows are in flight while one reduces, in a branch-free steady loop.  It takes
 // rows of whole 16-byte chunks over whole waves (dim <= nv * tpr * V, at most 1/8 of the chunk
-// slots idle; idle lanes reload the row's last chunk, so no branch guards a load), at most two
+// slots idle, or for 2-byte rows of one chunk per thread a partly idle last wave; idle lanes
+// reload the row's last chunk, so no branch guards a load), at most two
 // chunks per thread, and workgroups of at most kRingBlock threads (its launch bound: 256 VGPRs a lane for
 // the three row buffers), one per CU, so each row slot walks twice as many rows as in the
 // 1024-thread persistent kernel.  Measured on MI355X at 16384 x 4096 bf16: 69.2 us against 72.4.
@@ -197,7 +198,12 @@ inline BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned,
 
 // Whether a row plan suits the ring-pipelined backward (see kRingBlock).
 // Rows may leave lanes idle (whole waves over fewer chunks), at most 1/8 of the row group's
-// chunk slots: the kernel's idle-lane variant (kRingTail) reloads the row's last chunk there.
+// chunk slots, or for 2-byte rows of one chunk per thread any part of the last wave: the
+// kernel's idle-lane variant (kRingTail) reloads the row's last chunk there.  Measured on
+// MI355X (bf16, 16384 rows, alternating processes, two runs each), one-chunk row groups with a
+// partly idle last wave against the plans before them (two or three chunks per thread in
+// bwd_vec_kernel): 640 19.1 against 20.6 us, 768 19.5 against 21.9, 1152 29.6 against 32.4, 1280
+// 30.2 against 34.0.
 inline bool ring_eligible(const RowPlan& p, int64_t dim, int elem_bytes) {
   if (!p.vec || (elem_bytes != 2 && elem_bytes != 4)) return false;
   const int V = 16 / elem_bytes;
@@ -205,7 +211,8 @@ inline bool ring_eligible(const RowPlan& p, int64_t dim, int elem_bytes) {
   if (dim % V != 0) return false;
   const int64_t chunks = dim / V;
   return p.nv >= 1 && p.nv <= kRingMaxNV && p.tpr <= kRingBlock && chunks >= 1 &&
-         slots >= chunks && slots - chunks < p.tpr && (slots - chunks) * 8 <= slots;
+         slots >= chunks && slots - chunks < p.tpr &&
+         ((p.nv == 1 && elem_bytes == 2) ? slots - chunks < kWave : (slots - chunks) * 8 <= slots);
 }
 
 // Whether the ring's idle-lane variant is planned for rows that leave lanes idle (whole rows
@@ -282,7 +289,12 @@ inline BwdPlan plan_bwd_ring(int64_t rows, int64_t dim, int elem_bytes, bool ali
     return b;
   };
   if (prefer_nv == 0 && elem_bytes == 2) {
-    const RowPlan one = plan_rows(dim, elem_bytes, aligned, 1, kBwdOrder);
+    // one chunk per thread in whole waves, the last one partly idle where the chunks end there
+    RowPlan one = plan_rows(dim, elem_bytes, aligned, 1, kBwdOrder);
+    if (aligned && dim % 8 == 0 && dim / 8 <= kRingBlock) {
+      const int t = (int)((dim / 8 + kWave - 1) / kWave) * kWave;
+      one = RowPlan{true, 1, t, 1, t};
+    }
     if (one.vec && one.nv == 1 && one.tpr != 320 && one.tpr != 384) {
       const BwdPlan b = complete(one);
       const int64_t slots = b.wgs * b.rp.groups;
