@@ -20,10 +20,11 @@
 //                       row's loads in flight while the current row reduces; the weight chunk and
 //                       the fp32 dweight column accumulators stay in registers for the whole walk;
 //                       each slot finally writes one fp32 partial row (no atomics).
-//   bwd_ring_kernel     the same walk for rows of whole 16-byte chunks (at most 1/8 of the lanes
-//                       idle) with a ring of three row buffers (two rows in flight while one
-//                       reduces) in a branch-free steady loop, 512-thread workgroups, one per
-//                       CU: the backward's default where the rows suit it.
+//   bwd_ring_kernel     the same walk for rows of whole 16-byte chunks (some lanes may idle;
+//                       2-byte rows of 8n + 4 elements in 8-byte halves) with a ring of three
+//                       row buffers (two rows in flight while one reduces) in a branch-free
+//                       steady loop, 512-thread workgroups, one per CU: the backward's default
+//                       where the rows suit it.
 //   fwd_rope_kernel     the forward with the model's interleaved RoPE on y: strided row walks
 //                       with the rotation advanced by a recurrence.
 //   bwd_rope_ring_kernel  its backward (grad_y rotated back, then the norm's backward) in
@@ -1380,7 +1381,7 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
   constexpr bool SAVED_IS_H = (FLAGS & kSavedIsH) != 0;
   constexpr bool HAS_GH = (FLAGS & kGradH) != 0;
   constexpr bool HAS_DRES = (FLAGS & kRingDres) != 0;
-  // kRingTail: rows of fewer chunks than the row group's lanes (whole waves, at most 1/8 idle):
+  // kRingTail: rows of fewer chunks than the row group's lanes (launch_plan.h ring_eligible):
   // an idle lane loads the row's last chunk instead (no branch around the load), adds nothing
   // and stores nothing
   constexpr bool TAIL = (FLAGS & kRingTail) != 0;
