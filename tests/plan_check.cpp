@@ -310,6 +310,38 @@ int main() {
   CHECK(plan_bwd_ring8(16384, 100, 2, 256).ring && plan_bwd_ring8(16384, 100, 2, 256).rp.tpr == 64,
         "ring8 at 100 (12 whole chunks in one partly idle wave)");
   printf("ring8 plans checked: %ld\n", ring8);
+  // The element-strided ring: 4 or 8 elements a lane (8 only where 4 would need more than
+  // kRingBlock lanes), whole waves with less than one idle, every column covered, workgroups
+  // within kRingBlock threads and one per CU, LDS for the combine of several row groups, the
+  // partial rows within the workspace query; none past 4096 elements.
+  long relem = 0;
+  for (int64_t dim = 1; dim <= 4200; dim += (dim < 600 ? 1 : 7)) {
+    for (int eb = 2; eb <= 4; eb += 2) {
+      for (int64_t rows : {1, 300, 16384}) {
+        const BwdPlan e = plan_bwd_ring_elem(rows, dim, eb, 256);
+        if (dim > 4096) {
+          CHECK(e.elem_m == 0, "element ring past 4096 (dim=%lld)", (long long)dim);
+          continue;
+        }
+        ++relem;
+        const int m = e.elem_m;
+        const int64_t lanes = (dim + m - 1) / m;
+        CHECK((m == 4 || (m == 8 && (dim + 3) / 4 > kRingBlock)) && e.rp.tpr % kWave == 0 &&
+                  e.rp.tpr <= kRingBlock && e.rp.tpr - lanes < kWave && lanes <= e.rp.tpr &&
+                  (int64_t)m * e.rp.tpr >= dim,
+              "element ring layout dim=%lld m=%d tpr=%d", (long long)dim, m, e.rp.tpr);
+        CHECK(e.rp.groups >= 1 && e.rp.block == e.rp.groups * e.rp.tpr &&
+                  e.rp.block <= kRingBlock && e.wgs >= 1 && e.wgs <= 256 &&
+                  e.wgs <= (rows + e.rp.groups - 1) / e.rp.groups &&
+                  e.lds_bytes == (e.rp.groups > 1 ? (size_t)dim * sizeof(float) : 0),
+              "element ring launch dim=%lld", (long long)dim);
+        CHECK((size_t)e.wgs * (size_t)dim * sizeof(float) <=
+                  bwd_workspace_bytes(rows, dim, 256, 0, 1024, 16),
+              "element ring partials exceed the workspace (dim=%lld)", (long long)dim);
+      }
+    }
+  }
+  printf("element ring plans checked: %ld\n", relem);
   // One chunk per thread first in the ring for 2-byte rows, for walks of up to
   // kRingOneChunkMaxIters rows per slot; longer walks, fp32 rows and an explicit preference
   // keep the backward's order (two chunks per thread first).

@@ -155,6 +155,8 @@ struct BwdPlan {
   // the ring over rows of 8-byte alignment with a half chunk at their end (plan_bwd_ring8): rp
   // lays out the row's whole chunks (dim - 4 elements)
   bool x8 = false;
+  // the element-strided ring (plan_bwd_ring_elem): elements per lane, 0 when not planned
+  int elem_m = 0;
   // with the RoPE gradient: bwd_vec_kernel's plain plan, each pair's rotation evaluated directly
   // where g is decoded (rows too wide for the RoPE walk's bound)
   bool rope_direct = false;
@@ -328,6 +330,38 @@ inline BwdPlan plan_bwd_ring8(int64_t rows, int64_t dim, int elem_bytes, int cus
   return b;
 }
 
+// The element-strided ring (bwd_ring_elem_kernel) for rows the chunked kernels cannot take (odd
+// lengths, streams that start anywhere in a 16-byte line): M elements per lane, 4 or 8, the
+// fewer that keeps a row group within kRingBlock threads (rows of up to 4096 elements), row
+// groups of whole waves packed into workgroups of up to kRingBlock threads, one per CU.
+constexpr int kRingElemMaxM = 8;
+
+inline BwdPlan plan_bwd_ring_elem(int64_t rows, int64_t dim, int elem_bytes, int cus) {
+  BwdPlan b;
+  b.rp = RowPlan{false, 0, kGenericBlock, 1, kGenericBlock};
+  b.wgs = 0;
+  b.lds_bytes = 0;
+  if ((elem_bytes != 2 && elem_bytes != 4) || dim <= 0 ||
+      dim > (int64_t)kRingElemMaxM * kRingBlock)
+    return b;
+  int m = 4;
+  while ((dim + m - 1) / m > kRingBlock) m *= 2;
+  const int64_t lanes = (dim + m - 1) / m;
+  RowPlan& p = b.rp;
+  p.tpr = (int)((lanes + kWave - 1) / kWave) * kWave;
+  p.groups = kRingBlock / p.tpr;
+  p.block = p.tpr * p.groups;
+  p.nv = 0;
+  p.vec = false;
+  const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
+  int64_t wgs = cus > 0 ? (int64_t)cus : 1;
+  if (wgs > wgs_needed) wgs = wgs_needed;
+  b.wgs = wgs;
+  b.lds_bytes = p.groups > 1 ? (size_t)dim * sizeof(float) : 0;
+  b.elem_m = m;
+  return b;
+}
+
 // The ring-pipelined backward with the fused RoPE gradient (bwd_rope_ring_kernel): whole rows
 // of one 16-byte chunk per thread where a row has at most kRingBlock chunks (its rotation state
 // and tables keep it at 128 VGPRs), else of two (rows of up to 2 * kRingBlock chunks; 256
@@ -475,6 +509,8 @@ inline size_t bwd_workspace_bytes(int64_t rows, int64_t dim, int cus, int prefer
       if (rr.ring && rr.wgs > most) most = rr.wgs;
       const BwdPlan r8 = plan_bwd_ring8(rows, dim, sizes[si], cus, ring_block, ring_wgs_per_cu);
       if (r8.ring && r8.wgs > most) most = r8.wgs;
+      const BwdPlan re = plan_bwd_ring_elem(rows, dim, sizes[si], cus);
+      if (re.elem_m > 0 && re.wgs > most) most = re.wgs;
     }
   }
   return (size_t)most * (size_t)dim * sizeof(float);

@@ -1661,6 +1661,161 @@ __global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_kernel(const Bwd
 }
 
 // ------------------------------------------------------------------------------------------
+// Backward, rows of any length and alignment that bwd_ring_kernel cannot take (odd lengths,
+// streams that start anywhere in a 16-byte line), in bwd_ring_kernel's walk and ring
+// (launch_plan.h: plan_bwd_ring_elem).  Element-strided lanes: lane lt of a row group holds
+// columns lt, lt + tpr, ..., lt + (M - 1) tpr, so each element load or store of a wave moves
+// one contiguous run of 64 elements; a column past the row's end loads the row's last element
+// (no branch around a load) and adds and stores nothing.  Rows of M * tpr elements at most: M 4
+// or 8 (106-232 VGPRs; sixteen spilled 21-258 VGPRs a lane even one row ahead), so rows of up
+// to 4096 elements.
+// ------------------------------------------------------------------------------------------
+template <int DT, int WDT, int M, int FLAGS>
+__global__ __launch_bounds__(vg_plan::kRingBlock) void bwd_ring_elem_kernel(const BwdArgs a) {
+  using C = Codec<DT>;
+  using Raw = std::conditional_t<C::kBytes == 2, uint16_t, uint32_t>;
+  constexpr bool SAVED_IS_H = (FLAGS & kSavedIsH) != 0;
+  constexpr bool HAS_GH = (FLAGS & kGradH) != 0;
+  constexpr bool HAS_DRES = (FLAGS & kRingDres) != 0;
+  constexpr int MH = HAS_GH ? M : 1;  // grad_h elements (a dummy slot when absent)
+  constexpr int PF = HAS_GH ? 1 : vg_plan::kRingPrefetch;
+  constexpr int R = PF + 1;
+  static_assert((FLAGS & (kRopeG | kRingTail | kRing8)) == 0, "plain rows only");
+  static_assert(M == 4 || M == 8, "sixteen elements a lane spill past 256 VGPRs");
+  __shared__ float red[2][kMaxWavesPerRow];
+  extern __shared__ __align__(16) float dyn_lds[];  // dim floats: the row groups' combine
+
+  const int tpr = a.tpr;
+  const int grp = threadIdx.x / tpr;
+  const int lt = threadIdx.x - grp * tpr;
+  const int groups = blockDim.x / tpr;
+  const int64_t slot = (int64_t)blockIdx.x * groups + grp;
+  const int64_t nslots = (int64_t)gridDim.x * groups;
+  const bool has_w = a.w != nullptr;
+  const int64_t last = a.rows - 1;
+  // column m of this lane (the row's last one past its end) and whether it is the lane's own
+  int col[M];
+  bool own[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int c = lt + m * tpr;
+    own[m] = c < a.dim;
+    col[m] = own[m] ? c : a.dim - 1;
+  }
+  float wf[M], acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    wf[m] = has_w ? Codec<WDT>::load1(a.w, col[m]) : 1.0f;
+    acc[m] = 0.0f;
+  }
+  auto load_raw = [&](const void* base, int64_t i) -> uint32_t {
+    return (uint32_t)__builtin_nontemporal_load(static_cast<const Raw*>(base) + i);
+  };
+  auto decode = [&](uint32_t u) -> float {
+    if constexpr (DT == VELOGRAD_DTYPE_BF16) {
+      return __builtin_bit_cast(float, u << 16);
+    } else if constexpr (DT == VELOGRAD_DTYPE_F16) {
+      return (float)__builtin_bit_cast(_Float16, (uint16_t)u);
+    } else {
+      return __builtin_bit_cast(float, u);
+    }
+  };
+  auto store_one = [&](void* base, int64_t i, float f) {
+    Raw v;
+    if constexpr (DT == VELOGRAD_DTYPE_BF16) v = __builtin_bit_cast(uint16_t, (__bf16)f);
+    else if constexpr (DT == VELOGRAD_DTYPE_F16) v = __builtin_bit_cast(uint16_t, (_Float16)f);
+    else v = __builtin_bit_cast(uint32_t, f);
+    __builtin_nontemporal_store(v, static_cast<Raw*>(base) + i);
+  };
+
+  uint32_t gr[R][M], sr[R][M], hr[R][MH];
+  float rr[R];
+  // Row `row`'s g, saved, grad_h elements and inv_rms; rows past the end read the last row.
+  auto load_row = [&](int64_t row, uint32_t* gv, uint32_t* sv, uint32_t* hv, float& r) {
+    const int64_t rw = row < a.rows ? row : last;
+    r = a.inv_rms[rw];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      gv[m] = load_raw(a.g, rw * a.ld_g + col[m]);
+      sv[m] = load_raw(a.saved, rw * a.ld_s + col[m]);
+      if constexpr (HAS_GH) hv[m] = load_raw(a.gh, rw * a.ld_gh + col[m]);
+    }
+  };
+  // The backward of one row (bwd_ring_kernel's, element by element); `ok` = the row exists.
+  auto process = [&](const uint32_t* gv, const uint32_t* sv, const uint32_t* hv, float r,
+                     int64_t row, bool ok, int it) {
+    float gf[M], xh[M], gw[M];
+    float s = 0.0f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      gf[m] = decode(gv[m]);
+      xh[m] = decode(sv[m]);
+      if constexpr (SAVED_IS_H) xh[m] = xh[m] * r;
+      gw[m] = gf[m] * wf[m];
+      const float t = gw[m] * xh[m];
+      s += own[m] ? t : 0.0f;
+    }
+    s = row_sum(s, tpr, grp, red[it & 1]);
+    const float mean = s / (float)a.dim;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float d = r * (gw[m] - xh[m] * mean);
+      if constexpr (HAS_GH) d = d + decode(hv[m]);
+      const bool store = ok && own[m];
+      if (store) {
+        store_one(a.dx, row * a.ld_dx + col[m], d);
+        if constexpr (HAS_DRES) store_one(a.dres, row * a.ld_dres + col[m], d);
+      }
+      acc[m] += store ? gf[m] * xh[m] : 0.0f;
+    }
+  };
+
+  // The walk and ring of bwd_ring_kernel.
+  const int full = (int)(a.rows / nslots);
+#pragma unroll
+  for (int j = 0; j < PF; ++j) load_row(slot + (int64_t)j * nslots, gr[j], sr[j], hr[j], rr[j]);
+  int it = 0;
+  for (; it + R <= full; it += R) {
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const int nb = (u + PF) % R;
+      load_row(slot + (int64_t)(it + u + PF) * nslots, gr[nb], sr[nb], hr[nb], rr[nb]);
+      process(gr[u], sr[u], hr[u], rr[u], slot + (int64_t)(it + u) * nslots, true, it + u);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    if (it + u < a.iters) {
+      const int nb = (u + PF) % R;
+      if (it + u + PF < a.iters)
+        load_row(slot + (int64_t)(it + u + PF) * nslots, gr[nb], sr[nb], hr[nb], rr[nb]);
+      const int64_t row = slot + (int64_t)(it + u) * nslots;
+      process(gr[u], sr[u], hr[u], rr[u], row, row < a.rows, it + u);
+    }
+  }
+
+  if (a.partial == nullptr) return;
+  // One fp32 partial row per workgroup; row groups added in group order through LDS.
+  float* prow = a.partial + (int64_t)blockIdx.x * a.dim;
+  if (groups == 1) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      if (own[m]) prow[col[m]] = acc[m];
+    return;
+  }
+  float* comb = dyn_lds;
+  for (int gi = 0; gi < groups; ++gi) {
+    if (grp == gi) {
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+        if (own[m]) comb[col[m]] = (gi == 0) ? acc[m] : comb[col[m]] + acc[m];
+    }
+    __syncthreads();
+  }
+  for (int q = threadIdx.x; q < a.dim; q += blockDim.x) prow[q] = comb[q];
+}
+
+// ------------------------------------------------------------------------------------------
 // Backward with the fused RoPE gradient, ring-pipelined (launch_plan.h: plan_bwd_rope_ring):
 // whole rows of NV (1 or 2) 16-byte chunks per thread, the saved tensor h, no grad_h or dres (the
 // module's backward).  The walk, ring and steady loop are bwd_ring_kernel's: slot s walks rows
@@ -2264,8 +2419,14 @@ BwdPlan plan_bwd(int64_t rows, int64_t dim, int elem_bytes, bool aligned, bool a
   if (rope)
     return vg_plan::plan_bwd_rope(rows, dim, elem_bytes, aligned, cus, t.bwd_nv, t.bwd_block,
                                   t.bwd_waves_per_cu);
-  return vg_plan::plan_bwd(rows, dim, elem_bytes, aligned, cus, t.bwd_nv, t.bwd_block,
-                           t.bwd_waves_per_cu);
+  const BwdPlan p = vg_plan::plan_bwd(rows, dim, elem_bytes, aligned, cus, t.bwd_nv, t.bwd_block,
+                                      t.bwd_waves_per_cu);
+  // rows the chunked kernels cannot take: the element-strided ring where it fits
+  if (!p.rp.vec && t.bwd_ring) {
+    const BwdPlan e = vg_plan::plan_bwd_ring_elem(rows, dim, elem_bytes, cus);
+    if (e.elem_m > 0) return e;
+  }
+  return p;
 }
 
 bool ld_ok(int64_t ld, int elem_bytes) { return ((ld * elem_bytes) & 15) == 0; }
@@ -2412,11 +2573,29 @@ void launch_bwd_ring(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
 }
 
 template <int DT, int WDT, int F>
+void launch_bwd_ring_elem(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
+  const dim3 grid((uint32_t)b.wgs), block(b.rp.block);
+  if (b.elem_m == 4)
+    hipLaunchKernelGGL((bwd_ring_elem_kernel<DT, WDT, 4, F>), grid, block, b.lds_bytes, st, a);
+  else
+    hipLaunchKernelGGL((bwd_ring_elem_kernel<DT, WDT, 8, F>), grid, block, b.lds_bytes, st, a);
+}
+
+template <int DT, int WDT, int F>
 void launch_bwd_flags(const BwdArgs& a, const BwdPlan& b, hipStream_t st) {
   const RowPlan& p = b.rp;
   const dim3 grid((uint32_t)b.wgs);
   const dim3 block(p.block);
   const size_t lds = b.lds_bytes;
+  if constexpr ((F & kRopeG) == 0) {
+    if (b.elem_m > 0) {
+      if (a.dres != nullptr)
+        launch_bwd_ring_elem<DT, WDT, F | kRingDres>(a, b, st);
+      else
+        launch_bwd_ring_elem<DT, WDT, F>(a, b, st);
+      return;
+    }
+  }
   if (!p.vec) {
     hipLaunchKernelGGL((bwd_generic_kernel<DT, WDT, F>), grid, block,
                        vg_plan::generic_bwd_lds_bytes(a.dim, a.partial != nullptr), st, a);
@@ -2747,8 +2926,12 @@ int32_t run_bwd(const void* grad_y, const void* saved, int32_t saved_is_h, const
   // same dynamic LDS as the group combine, one after the other.
   if (rope && plan.rp.vec && !plan.ring && !plan.rope_direct)
     plan.lds_bytes = (size_t)dim * sizeof(float);
-  if (!vg_plan::row_plan_valid(plan.rp, plan_dim, eb) || plan.wgs < 1 ||
-      plan.wgs > INT32_MAX || plan.lds_bytes > 64 * 1024 ||
+  const bool elem_ok =
+      plan.elem_m > 0 && !rope && plan.rp.tpr % kWave == 0 && plan.rp.tpr >= kWave &&
+      plan.rp.groups >= 1 && plan.rp.block == plan.rp.tpr * plan.rp.groups &&
+      plan.rp.block <= vg_plan::kRingBlock && (int64_t)plan.elem_m * plan.rp.tpr >= dim;
+  if ((plan.elem_m > 0 ? !elem_ok : !vg_plan::row_plan_valid(plan.rp, plan_dim, eb)) ||
+      plan.wgs < 1 || plan.wgs > INT32_MAX || plan.lds_bytes > 64 * 1024 ||
       (plan.ring && !rope && (!vg_plan::ring_eligible(plan.rp, plan_dim, eb) ||
                               plan.rp.block > vg_plan::kRingBlock)) ||
       (plan.x8 && (rope || !plan.ring || eb != 2 || dim % 8 != 4 || plan.rp.nv != 1 ||
