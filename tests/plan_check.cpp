@@ -310,8 +310,8 @@ int main() {
   CHECK(plan_bwd_ring8(16384, 100, 2, 256).ring && plan_bwd_ring8(16384, 100, 2, 256).rp.tpr == 64,
         "ring8 at 100 (12 whole chunks in one partly idle wave)");
   printf("ring8 plans checked: %ld\n", ring8);
-  // The element-strided ring: 4 or 8 elements a lane (8 only where 4 would need more than
-  // kRingBlock lanes), whole waves with less than one idle, every column covered, workgroups
+  // The element-strided ring: 4 elements a lane for rows of up to 512, else 8, whole waves
+  // with less than one idle, every column covered, workgroups
   // within kRingBlock threads and one per CU, LDS for the combine of several row groups, the
   // partial rows within the workspace query; none past 4096 elements.
   long relem = 0;
@@ -326,7 +326,7 @@ int main() {
         ++relem;
         const int m = e.elem_m;
         const int64_t lanes = (dim + m - 1) / m;
-        CHECK((m == 4 || (m == 8 && (dim + 3) / 4 > kRingBlock)) && e.rp.tpr % kWave == 0 &&
+        CHECK(m == (dim <= 512 ? 4 : 8) && e.rp.tpr % kWave == 0 &&
                   e.rp.tpr <= kRingBlock && e.rp.tpr - lanes < kWave && lanes <= e.rp.tpr &&
                   (int64_t)m * e.rp.tpr >= dim,
               "element ring layout dim=%lld m=%d tpr=%d", (long long)dim, m, e.rp.tpr);

@@ -21,12 +21,12 @@ BF16, F16, F32 = torch.bfloat16, torch.float16, torch.float32
 CASES = [
     # rows, dim, dtype, weight ("same", "f32", None), grad_h, dres, row stride or None
     (5000, 99, BF16, "same", False, False, None),     # 4 a lane, eight 64-thread row groups
-    (3000, 255, F16, "f32", True, True, None),
+    (3000, 255, F16, "f32", True, True, None),       # 64 lanes, one partly idle
     (1, 1, BF16, "same", False, False, None),         # one element, one row
     (2, 3, F32, None, True, False, None),
-    (1700, 1001, F32, "same", False, True, None),     # 251 lanes: four 64-lane waves, one idle
-    (2049, 2047, BF16, "same", True, False, None),    # 4 a lane, 512-thread row groups
-    (1000, 2049, F16, "same", False, False, None),    # 8 a lane
+    (1700, 1001, F32, "same", False, True, None),     # 8 a lane: 126 of 128 lanes, four groups
+    (2049, 2047, BF16, "same", True, False, None),    # 8 a lane, two 256-thread row groups
+    (1000, 2049, F16, "same", False, False, None),    # 257 lanes: one 320-thread row group
     (777, 4095, BF16, "f32", True, True, None),       # 8 a lane, 512 threads, one idle lane
     (600, 1001, BF16, "same", False, False, 1013),    # odd row strides
     (600, 4096, F16, "same", True, False, 4099),      # aligned length, rows of odd stride
