@@ -214,10 +214,11 @@ VELOGRAD_API int32_t velograd_rmsnorm_residual_bwd(
  *   Limit: returns VELOGRAD_ERR_WORKSPACE_TOO_SMALL, launching nothing, when dweight would
  *   need more than the 16 MiB, i.e. one fp32 row of dim per partial.  With the default launch
  *   plans on a 256-CU MI355X that is 256 partials for 16-byte-aligned rows up to dim 16384
- *   bf16/fp16 or 8192 fp32 (and for bf16/fp16 rows of 8n + 4 elements on 8-byte boundaries,
- *   dim up to 4100), and up to min(rows, 4 per CU) partials on the generic path (other
- *   unaligned or odd-sized rows: dim up to 4096 at 1024 or more rows).  The VELOGRAD_BWD_*
- *   tuning variables change the plans, and with them which shapes are refused.
+ *   bf16/fp16 or 8192 fp32, for bf16/fp16 rows of 8n + 4 elements on 8-byte boundaries up
+ *   to dim 4100, and for other rows up to dim 4096 (the element-strided kernel); wider rows of
+ *   those kinds take the generic path with min(rows, 4 per CU) partials, refused when those
+ *   pass 16 MiB (at 1024 or more rows, any dim above 4096).  The VELOGRAD_BWD_* tuning
+ *   variables change the plans, and with them which shapes are refused.
  *   Calls that overlap on one GPU (several streams or host threads at once) share the scratch
  *   and race: serialise them.  The scratch keeps the last call's contents; nothing in it has
  *   to start at zero.
