@@ -1,6 +1,6 @@
-"""The element-strided ring backward (bwd_ring_elem_kernel): rows the chunked kernels cannot
-take (odd lengths, streams that start anywhere inside a 16-byte line) up to 4096 elements, each
-lane holding columns lt, lt + tpr, ... of its row group.  Checked against the oracle with
+"""The element-strided kernels (fwd_elem_kernel, bwd_ring_elem_kernel): rows the chunked kernels
+cannot take (odd lengths, streams that start anywhere inside a 16-byte line) up to 4096
+elements, each lane holding columns lt, lt + tpr, ... of its row group.  Checked against the oracle with
 tests/_parity.py's tolerances over dtypes, weights (same dtype, fp32, none), the residual-stream
 gradient, a second dresidual buffer, row strides from wider tensors, row counts from one row to
 more rows than row slots, rows of 1 to 4095 elements (4 and 8 elements a lane, one to eight row
@@ -83,3 +83,31 @@ def test_element_ring_matches_oracle(rows, d, dtype, wkind, gh, dres, stride):
     assert torch.equal(dx, dx2)
     if w is not None:
         assert torch.equal(dw, dw2)
+
+
+@pytest.mark.parametrize("rows,d,dtype,wkind,gh,dres,stride", CASES,
+                         ids=[f"{r}x{d}-{str(t).split('.')[-1]}" for r, d, t, *_ in CASES])
+def test_element_forward_matches_oracle(rows, d, dtype, wkind, gh, dres, stride):
+    """The forward over the same rows (element-strided up to 1024 elements, the generic kernel
+    beyond): with a residual (y and h written) when the case has a residual-stream gradient,
+    else without one (the module form's plain norm)."""
+    print(f"element forward {rows}x{d} {dtype} w={wkind} residual={gh} stride={stride}",
+          flush=True)
+    rng = np.random.default_rng(rows * 5 + d)
+    x = _dev(rng, rows, d, dtype, stride)
+    res = _dev(rng, rows, d, dtype, stride) if gh else None
+    w = None
+    if wkind is not None:
+        w = P.to_device(P.weight_vec(rng, d), dtype if wkind == "same" else F32)
+    y, h, inv = vk.fused_rmsnorm_residual_forward(x, res, w, 1e-5)
+    torch.cuda.synchronize()
+    ry, rh, rinv = ora.fused_rmsnorm_residual_forward(
+        P.upcast(x), P.upcast(res) if res is not None else None,
+        P.upcast(w) if w is not None else None, 1e-5)
+    if dtype == F32:
+        assert np.array_equal(P.upcast(h), rh)
+        assert P.rel_err(P.upcast(y), ry) <= P.FP32_REL_TOL
+    else:
+        P.assert_within_ulp(h, rh, 0, "h")
+        P.assert_within_ulp(y, ry, 1, "y")
+    assert P.rel_err(P.upcast(inv), rinv) <= P.FP32_REL_TOL

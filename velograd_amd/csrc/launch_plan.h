@@ -330,30 +330,41 @@ inline BwdPlan plan_bwd_ring8(int64_t rows, int64_t dim, int elem_bytes, int cus
   return b;
 }
 
-// The element-strided ring (bwd_ring_elem_kernel) for rows the chunked kernels cannot take (odd
-// lengths, streams that start anywhere in a 16-byte line): M elements per lane, 4 for rows of
-// up to 512 elements, else 8 (rows of up to 4096 elements), row groups of whole waves packed
-// into workgroups of up to kRingBlock threads, one per CU.  Eight elements a lane in half the
-// lanes (more row groups a workgroup) ran bf16 16384 x 1535 in 42.3 us against 55.5 with four,
-// 2047 49.4 against 60.5, 1001 30.0 against 31.8, and 3001 and 4095 alike.
+// Element-strided rows (fwd_elem_kernel, bwd_ring_elem_kernel) for rows the chunked kernels
+// cannot take (odd lengths, streams that start anywhere in a 16-byte line): M elements a lane,
+// 4 for rows of up to 512 elements, else 8 (0: a row longer than kRingElemMaxM * kRingBlock
+// elements), row groups of whole waves packed into workgroups of up to kRingBlock threads.
+// Eight elements a lane in half the lanes (more row groups a workgroup) ran the backward at bf16
+// 16384 x 1535 in 42.3 us against 55.5 with four, 2047 49.4 against 60.5, 1001 30.0 against
+// 31.8, and 3001 and 4095 alike.
 constexpr int kRingElemMaxM = 8;
 
+inline int elem_per_lane(int64_t dim) {
+  if (dim <= 0 || dim > (int64_t)kRingElemMaxM * kRingBlock) return 0;
+  return dim > 512 ? 8 : 4;
+}
+
+inline RowPlan plan_elem_rows(int64_t dim) {
+  RowPlan p{false, 0, kGenericBlock, 1, kGenericBlock};
+  const int m = elem_per_lane(dim);
+  if (m == 0) return p;
+  const int64_t lanes = (dim + m - 1) / m;
+  p.tpr = (int)((lanes + kWave - 1) / kWave) * kWave;
+  p.groups = kRingBlock / p.tpr;
+  p.block = p.tpr * p.groups;
+  return p;
+}
+
+// The element-strided ring backward: plan_elem_rows' row groups, one workgroup per CU.
 inline BwdPlan plan_bwd_ring_elem(int64_t rows, int64_t dim, int elem_bytes, int cus) {
   BwdPlan b;
   b.rp = RowPlan{false, 0, kGenericBlock, 1, kGenericBlock};
   b.wgs = 0;
   b.lds_bytes = 0;
-  if ((elem_bytes != 2 && elem_bytes != 4) || dim <= 0 ||
-      dim > (int64_t)kRingElemMaxM * kRingBlock)
-    return b;
-  const int m = dim > 512 ? 8 : 4;
-  const int64_t lanes = (dim + m - 1) / m;
-  RowPlan& p = b.rp;
-  p.tpr = (int)((lanes + kWave - 1) / kWave) * kWave;
-  p.groups = kRingBlock / p.tpr;
-  p.block = p.tpr * p.groups;
-  p.nv = 0;
-  p.vec = false;
+  const int m = elem_per_lane(dim);
+  if ((elem_bytes != 2 && elem_bytes != 4) || m == 0) return b;
+  b.rp = plan_elem_rows(dim);
+  const RowPlan& p = b.rp;
   const int64_t wgs_needed = rows > 0 ? (rows + p.groups - 1) / p.groups : 1;
   int64_t wgs = cus > 0 ? (int64_t)cus : 1;
   if (wgs > wgs_needed) wgs = wgs_needed;

@@ -848,6 +848,91 @@ __global__ __launch_bounds__(max_block_for_nv(1)) void fwd_rope_kernel(const Fwd
 }
 
 // ------------------------------------------------------------------------------------------
+// Forward, rows of any length and alignment up to 4096 elements that the chunked kernels cannot
+// take (odd lengths, streams that start anywhere inside a 16-byte line): one-shot rows as in
+// fwd_vec_kernel, several short rows a workgroup, with bwd_ring_elem_kernel's element-strided
+// lanes (lane lt of a row group holds columns lt, lt + tpr, ..., M of them), so each of a
+// wave's element loads and stores moves one contiguous run of 64 elements.  y in the activation
+// dtype (the plain output) only; short rows (kFwdElemMaxDim), where the generic kernel's one row
+// per workgroup is bound by each row's latency.
+// ------------------------------------------------------------------------------------------
+constexpr int64_t kFwdElemMaxDim = 1024;  // the host plans it for rows of at most this length
+
+template <int DT, int WDT, int M>
+__global__ __launch_bounds__(vg_plan::kRingBlock) void fwd_elem_kernel(const FwdArgs a) {
+  using C = Codec<DT>;
+  using Raw = std::conditional_t<C::kBytes == 2, uint16_t, uint32_t>;
+  static_assert(M == 4 || M == 8, "four or eight elements a lane");
+  __shared__ float red[kMaxWavesPerRow];
+  const int tpr = a.tpr;
+  const int grp = threadIdx.x / tpr;
+  const int lt = threadIdx.x - grp * tpr;
+  const int groups = blockDim.x / tpr;
+  const int64_t row = (int64_t)blockIdx.x * groups + grp;
+  const bool row_ok = row < a.rows;
+  const int64_t rw = row_ok ? row : a.rows - 1;  // a row group past the end reads the last row
+  const bool has_res = a.res != nullptr;
+  const bool write_h = has_res && a.h != nullptr;
+  int col[M];
+  bool own[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int c = lt + m * tpr;
+    own[m] = c < a.dim;
+    col[m] = own[m] ? c : a.dim - 1;
+  }
+  auto decode = [&](uint32_t u) -> float {
+    if constexpr (DT == VELOGRAD_DTYPE_BF16) {
+      return __builtin_bit_cast(float, u << 16);
+    } else if constexpr (DT == VELOGRAD_DTYPE_F16) {
+      return (float)__builtin_bit_cast(_Float16, (uint16_t)u);
+    } else {
+      return __builtin_bit_cast(float, u);
+    }
+  };
+  auto load_raw = [&](const void* base, int64_t i) -> uint32_t {
+    return (uint32_t)__builtin_nontemporal_load(static_cast<const Raw*>(base) + i);
+  };
+  auto store_one = [&](void* base, int64_t i, float f) {
+    Raw v;
+    if constexpr (DT == VELOGRAD_DTYPE_BF16) v = __builtin_bit_cast(uint16_t, (__bf16)f);
+    else if constexpr (DT == VELOGRAD_DTYPE_F16) v = __builtin_bit_cast(uint16_t, (_Float16)f);
+    else v = __builtin_bit_cast(uint32_t, f);
+    __builtin_nontemporal_store(v, static_cast<Raw*>(base) + i);
+  };
+
+  uint32_t xr[M], rr[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    xr[m] = load_raw(a.x, rw * a.ld_x + col[m]);
+    rr[m] = has_res ? load_raw(a.res, rw * a.ld_res + col[m]) : 0u;
+  }
+  float wf[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) wf[m] = a.w != nullptr ? Codec<WDT>::load1(a.w, col[m]) : 1.0f;
+  float hf[M];
+  float ss = 0.0f;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    hf[m] = decode(xr[m]);
+    if (has_res) hf[m] = hf[m] + decode(rr[m]);
+    const float t = hf[m] * hf[m];
+    ss += own[m] ? t : 0.0f;
+  }
+  ss = row_sum(ss, tpr, grp, red);
+  const float mean_sq = floor_mean_sq(ss / (float)a.dim, a.ms_floor);
+  const float r = 1.0f / __builtin_sqrtf(mean_sq + a.eps);
+  if (row_ok && lt == 0 && a.inv_rms != nullptr) a.inv_rms[row] = r;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    if (row_ok && own[m]) {
+      if (write_h) store_one(a.h, row * a.ld_h + col[m], hf[m]);
+      store_one(a.y, row * a.ld_y + col[m], (hf[m] * r) * wf[m]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
 // Forward, any dim / alignment: one row per workgroup, two passes over the row (the second
 // re-reads x and residual, normally from L2, and recomputes the identical fp32 h).
 // ------------------------------------------------------------------------------------------
@@ -2373,6 +2458,7 @@ struct Tuning {
   int bwd_ring;           // 1: the ring-pipelined backward where the rows suit it
   int ring_block;         // upper bound on the ring backward's workgroup size
   int ring_wgs_per_cu;    // ring backward workgroups per CU (1 or 2)
+  int fwd_elem;           // 1: the element-strided forward where the chunked kernels cannot go
 };
 
 const Tuning& tuning() {
@@ -2384,6 +2470,7 @@ const Tuning& tuning() {
       env_int("VELOGRAD_BWD_RING", 1, 0, 1),
       env_int("VELOGRAD_BWD_RING_BLOCK", vg_plan::kRingBlock, 64, vg_plan::kRingBlock),
       env_int("VELOGRAD_BWD_RING_WGS_PER_CU", 1, 1, 2),
+      env_int("VELOGRAD_FWD_ELEM", 1, 0, 1),
   };
   return t;
 }
@@ -2539,6 +2626,16 @@ void launch_fwd_x8(const FwdArgs& a, const RowPlan& p, hipStream_t st) {
       default: break;
     }
   }
+}
+
+// Rows of element-strided lanes (fwd_elem_kernel): `p` from plan_elem_rows, m elements a lane.
+template <int DT, int WDT>
+void launch_fwd_elem(const FwdArgs& a, const RowPlan& p, int m, hipStream_t st) {
+  const dim3 grid((uint32_t)((a.rows + p.groups - 1) / p.groups)), block(p.block);
+  if (m == 4)
+    hipLaunchKernelGGL((fwd_elem_kernel<DT, WDT, 4>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((fwd_elem_kernel<DT, WDT, 8>), grid, block, 0, st, a);
 }
 
 template <int DT, int WDT, int F>
@@ -2809,7 +2906,20 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
       x8 = true;
     }
   }
-  if (!vg_plan::row_plan_valid(p, x8 ? dim - 4 : dim, eb))
+  // other short rows the chunked kernels cannot take: element-strided lanes, several rows a
+  // workgroup.  Longer rows keep the generic kernel, whose row middles move in 16-byte accesses:
+  // bf16 16384 x 99 10.6 us against 38.6 in the generic kernel, 255 13.3 against 40.2, 1001 46.6
+  // against 49.2, but 2047 85.9 against 60.2, 3001 154.3 against 81.4, 4095 161.5 against 100.4.
+  int elem_m = 0;
+  if (!p.vec && !x8 && out == kOutDtype && (eb == 2 || eb == 4) && dim <= kFwdElemMaxDim &&
+      tuning().fwd_elem) {
+    elem_m = vg_plan::elem_per_lane(dim);
+    if (elem_m > 0) p = vg_plan::plan_elem_rows(dim);
+  }
+  const bool elem_ok = p.tpr % kWave == 0 && p.tpr >= kWave && p.groups >= 1 &&
+                       p.block == p.tpr * p.groups && p.block <= vg_plan::kRingBlock &&
+                       (int64_t)elem_m * p.tpr >= dim;
+  if (elem_m > 0 ? !elem_ok : !vg_plan::row_plan_valid(p, x8 ? dim - 4 : dim, eb))
     return fail(VELOGRAD_ERR_INVALID_ARGUMENT, "%s: internal launch plan rejected (dim=%lld)",
                 what, (long long)dim);
 
@@ -2847,6 +2957,8 @@ int32_t run_fwd(const char* what, int out, const void* x, const void* residual,
     default:
       if (x8)
         VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd_x8<kD, kW>(a, p, st)));
+      else if (elem_m > 0)
+        VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd_elem<kD, kW>(a, p, elem_m, st)));
       else
         VG_DISPATCH_TYPES(dtype, w_dtype, (launch_fwd<kD, kW, kOutDtype>(a, p, st)));
       break;
