@@ -61,8 +61,8 @@ def _run(lib, noalloc, g, saved, saved_is_h, w, inv, gh, with_dres, with_dw):
 
 
 # (rows, dim, dtype, weight dtype, saved is h, grad_h, dres): the first call is the largest;
-# every later one is smaller and takes another plan (1024-thread rows, 64-thread row groups,
-# the generic kernel for an odd dim).
+# every later one is smaller and takes another plan (one-chunk ring rows of 512 threads, 128-
+# thread row groups, the element-strided ring for an odd dim).
 CALLS = [
     (4096, 4096, torch.bfloat16, torch.bfloat16, True, False, True),
     (300, 1000, torch.bfloat16, torch.float32, False, True, False),
