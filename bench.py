@@ -47,9 +47,12 @@ CONFIGS = {
     "B": (8192, 4096, 1e-5, False),
     "C": (16384, 4096, 1e-5, True),
     "D": (32768, 8192, 1e-5, True),
-    # not a BASELINE configuration: rows of 4100 bf16 elements (8200 bytes, not a 16-byte
-    # multiple) take the generic kernels' aligned-middle path
+    # not BASELINE configurations.  U: rows of 4100 bf16 elements (8200 bytes, not a 16-byte
+    # multiple) start on 8-byte boundaries and take the register-resident kernels in 8-byte
+    # halves; O (only with --config O): rows of 4095, odd, take the element-strided backward and
+    # the generic forward
     "U": (16384, 4100, 1e-5, True),
+    "O": (16384, 4095, 1e-5, True),
 }
 
 
