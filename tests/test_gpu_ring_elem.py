@@ -1,10 +1,11 @@
 """The element-strided kernels (fwd_elem_kernel, bwd_ring_elem_kernel): rows the chunked kernels
 cannot take (odd lengths, streams that start anywhere inside a 16-byte line) up to 4096
-elements, each lane holding columns lt, lt + tpr, ... of its row group.  Checked against the oracle with
-tests/_parity.py's tolerances over dtypes, weights (same dtype, fp32, none), the residual-stream
-gradient, a second dresidual buffer, row strides from wider tensors, row counts from one row to
-more rows than row slots, rows of 1 to 4095 elements (4 and 8 elements a lane, one to eight row
-groups a workgroup), and bitwise repeatable dx and dweight."""
+elements, each lane holding columns lt, lt + tpr, ... of its row group.  Checked against the
+oracle with tests/_parity.py's tolerances over dtypes, weights (same dtype, fp32, none), the
+residual-stream gradient, a second dresidual buffer, row strides from wider tensors, row counts
+from one row to more rows than row slots (up to 16384 rows of 4095), rows of 1 to 4095 elements
+(4 and 8 elements a lane, one to eight row groups a workgroup), and bitwise repeatable dx and
+dweight."""
 
 import numpy as np
 import pytest
@@ -30,6 +31,8 @@ CASES = [
     (777, 4095, BF16, "f32", True, True, None),       # 8 a lane, 512 threads, one idle lane
     (600, 1001, BF16, "same", False, False, 1013),    # odd row strides
     (600, 4096, F16, "same", True, False, 4099),      # aligned length, rows of odd stride
+    (16384, 4095, BF16, "same", False, False, None),  # bench.py --config O: 64 rows a slot
+    (16384, 4095, BF16, "same", True, False, None),   # the same with grad_h
 ]
 
 
